@@ -1,0 +1,494 @@
+// qw6_dev.h -- device building blocks of the gfx950 MoE FFN kernels.
+//
+// GGUF super-block decoders that turn one 32-weight "unit" of a block into a
+// dot product with activations held in registers, the IQ lattice tables as
+// device constants (staged into LDS by the kernels that need them), exact
+// fp16 decoding, LDS byte readers for blocks that are only 2-byte aligned,
+// and wave64 reductions.
+//
+// Unit j (0..7) of a 256-weight block covers 32 columns of that block:
+//   Q4_K / Q5_K: qs bytes [16j, 16j+16): low nibbles are columns
+//                64(j/2) + 16(j%2) + i, high nibbles the same + 32 (i < 16);
+//   Q6_K:        half h = j/4, l in [8(j%4), 8(j%4)+8): columns
+//                128h + 32k + l for k = 0..3;
+//   IQ2_XXS / IQ2_S / IQ3_S: columns 32j .. 32j+31.
+// Each unit only needs its own bytes plus the block header, so a lane can
+// keep the same unit across rows with its 32 activations in registers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "iq_grid_data.h"
+
+namespace qw6 {
+
+enum Fmt : int { F_Q4K = 0, F_Q5K = 1, F_Q6K = 2, F_IQ2XXS = 3, F_IQ2S = 4, F_IQ3S = 5, F_NFMT = 6 };
+
+// qw6_quant_t (qw6.h:76-91) -> internal format, -1 if no block decoder.
+__host__ __device__ inline int fmt_of_quant(int q) {
+    switch (q) {
+    case 4: case 5: return F_Q4K;
+    case 6: return F_Q5K;
+    case 7: return F_Q6K;
+    case 13: return F_IQ2XXS;
+    case 11: return F_IQ2S;
+    case 9: return F_IQ3S;
+    default: return -1;
+    }
+}
+
+__host__ __device__ inline uint32_t fmt_block_bytes(int f) {
+    switch (f) {
+    case F_Q4K: return 144;
+    case F_Q5K: return 176;
+    case F_Q6K: return 210;
+    case F_IQ2XXS: return 66;
+    case F_IQ2S: return 82;
+    default: return 110;
+    }
+}
+
+// Which LDS lattice tables a format needs (bit 0: iq2xxs, 1: iq2s, 2: iq3s).
+__host__ __device__ inline uint32_t fmt_table_mask(int f) {
+    return f == F_IQ2XXS ? 1u : f == F_IQ2S ? 2u : f == F_IQ3S ? 4u : 0u;
+}
+
+// ---- IQ lattice tables --------------------------------------------------------
+
+struct IqTables {
+    uint64_t iq2xxs[256];
+    uint64_t iq2s[1024];
+    uint32_t iq3s[512];
+};
+constexpr uint32_t kTabOffIq2xxs = 0;
+constexpr uint32_t kTabOffIq2s = 256 * 8;
+constexpr uint32_t kTabOffIq3s = kTabOffIq2s + 1024 * 8;
+constexpr uint32_t kTabBytes = kTabOffIq3s + 512 * 4;   // 12 KB
+
+constexpr uint64_t expand_iq2(uint16_t c) {
+    uint64_t v = 0;
+    for (int j = 0; j < 8; j++) v |= (uint64_t)QW6_IQ2_LEVEL((c >> (2 * j)) & 3) << (8 * j);
+    return v;
+}
+constexpr uint32_t expand_iq3(uint16_t c) {
+    uint32_t v = 0;
+    for (int j = 0; j < 4; j++) v |= (uint32_t)(2 * ((c >> (3 * j)) & 7) + 1) << (8 * j);
+    return v;
+}
+constexpr IqTables make_tables() {
+    IqTables t{};
+    for (int i = 0; i < 256; i++) t.iq2xxs[i] = expand_iq2(qw6_iq2xxs_codes[i]);
+    for (int i = 0; i < 1024; i++) t.iq2s[i] = expand_iq2(qw6_iq2s_codes[i]);
+    for (int i = 0; i < 512; i++) t.iq3s[i] = expand_iq3(qw6_iq3s_codes[i]);
+    return t;
+}
+
+// ---- scalar helpers ------------------------------------------------------------
+
+// Exact binary16 -> binary32 in integer arithmetic (independent of the fp16
+// denormal mode): subnormal halves are m * 2^-24, exact in fp32.
+__device__ __forceinline__ float h2f(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu;
+    const uint32_t m = h & 0x3ffu;
+    uint32_t bits = sign | ((e + 112u) << 23) | (m << 13);
+    if (e == 0x1f) bits = sign | 0x7f800000u | (m << 13);
+    if (e == 0) bits = sign | __float_as_uint((float)m * 0x1p-24f);
+    return __uint_as_float(bits);
+}
+
+// float -> binary16, round to nearest even, subnormals kept (synthetic data).
+__host__ __device__ inline uint16_t f2h_rne(float f) {
+    uint32_t x;
+    __builtin_memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) return (uint16_t)(sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0));
+    if (ax >= 0x477ff000u) return (uint16_t)(sign | 0x7c00u);   // rounds to inf
+    const int e = (int)(ax >> 23) - 127;
+    if (e < -25) return (uint16_t)sign;
+    uint32_t mant = (ax & 0x7fffffu) | 0x800000u;
+    int shift;                   // bits dropped from the 24-bit significand
+    uint32_t base;
+    if (e < -14) { shift = 13 + (-14 - e); base = 0; }
+    else { shift = 13; base = (uint32_t)(e + 15) << 10; mant &= 0x7fffffu; }
+    uint32_t q = mant >> shift;
+    const uint32_t rem = mant & ((1u << shift) - 1);
+    const uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (q & 1))) q++;
+    return (uint16_t)(sign | (base + q));   // carry into the exponent is correct
+}
+
+// ---- LDS byte readers ---------------------------------------------------------
+// s: LDS viewed as 32-bit words; off: byte offset. 2-byte-aligned dwords are
+// rebuilt from two aligned words (the staging buffers carry 16 bytes of pad).
+
+__device__ __forceinline__ uint32_t lds32(const uint32_t* s, uint32_t off) {
+    const uint32_t i = off >> 2;
+    return __builtin_amdgcn_alignbyte(s[i + 1], s[i], off & 3);
+}
+__device__ __forceinline__ uint32_t lds16(const uint32_t* s, uint32_t off) {
+    return (s[off >> 2] >> ((off & 2) * 8)) & 0xffffu;
+}
+__device__ __forceinline__ uint32_t lds8(const uint32_t* s, uint32_t off) {
+    return (s[off >> 2] >> ((off & 3) * 8)) & 0xffu;
+}
+__device__ __forceinline__ uint64_t lds64_tab(const uint32_t* s, uint32_t off) {
+    const uint2 v = *(const uint2*)(s + (off >> 2));   // 8-byte aligned table entry
+    return (uint64_t)v.x | ((uint64_t)v.y << 32);
+}
+
+__device__ __forceinline__ float ub(uint32_t w, int n) { return (float)((w >> (8 * n)) & 0xffu); }
+// ±v where bit n of `signs` set means negative.
+__device__ __forceinline__ float sgn(float v, uint32_t signs, int n) {
+    return __uint_as_float(__float_as_uint(v) ^ (((signs >> n) & 1u) << 31));
+}
+
+// ---- activations for a unit ------------------------------------------------------
+
+// Load the 32 activations of unit j of block blk for format f from x (one
+// token, contiguous), and the partial sums the decoders use.
+__device__ __forceinline__ void load_unit_x(int f, const float* __restrict__ x, uint32_t blk,
+                                            int j, float (&xr)[32], float (&sx)[4]) {
+    const float* b = x + blk * 256;
+    if (f == F_Q4K || f == F_Q5K) {
+        const float4* p0 = (const float4*)(b + 64 * (j >> 1) + 16 * (j & 1));
+        const float4* p1 = (const float4*)(b + 64 * (j >> 1) + 32 + 16 * (j & 1));
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            float4 a = p0[i], c = p1[i];
+            xr[4 * i] = a.x; xr[4 * i + 1] = a.y; xr[4 * i + 2] = a.z; xr[4 * i + 3] = a.w;
+            xr[16 + 4 * i] = c.x; xr[17 + 4 * i] = c.y; xr[18 + 4 * i] = c.z; xr[19 + 4 * i] = c.w;
+        }
+    } else if (f == F_Q6K) {
+        const float* base = b + 128 * (j >> 2) + 8 * (j & 3);
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float4 a = *(const float4*)(base + 32 * k);
+            float4 c = *(const float4*)(base + 32 * k + 4);
+            xr[8 * k] = a.x; xr[8 * k + 1] = a.y; xr[8 * k + 2] = a.z; xr[8 * k + 3] = a.w;
+            xr[8 * k + 4] = c.x; xr[8 * k + 5] = c.y; xr[8 * k + 6] = c.z; xr[8 * k + 7] = c.w;
+        }
+    } else {
+        const float4* p = (const float4*)(b + 32 * j);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            float4 a = p[i];
+            xr[4 * i] = a.x; xr[4 * i + 1] = a.y; xr[4 * i + 2] = a.z; xr[4 * i + 3] = a.w;
+        }
+    }
+    if (f == F_Q6K) {
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            float s = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) s += xr[8 * k + i];
+            sx[k] = s;
+        }
+    } else {
+        float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) { s0 += xr[i]; s1 += xr[16 + i]; }
+        sx[0] = s0; sx[1] = s1; sx[2] = 0.f; sx[3] = 0.f;
+    }
+}
+
+// ---- unit decoders: acc[t] += sum_i w_i * xr[t][i] ----------------------------
+// s: LDS words; bo: byte offset of the block in LDS; tab: LDS words of the
+// lattice tables (IqTables layout at offset 0).
+
+// Q4_K (qw6.c:1492-1516): w = (d*sc)*q - dmin*m per 32-run.
+template <int T>
+__device__ __forceinline__ void unit_q4k(const uint32_t* s, uint32_t bo, int j,
+                                         const float (&xr)[T][32], const float (&sx)[T][4],
+                                         float (&acc)[T]) {
+    const uint32_t dm = s[bo >> 2];
+    const float d = h2f(dm & 0xffffu), dmin = h2f(dm >> 16);
+    const uint64_t sl = (uint64_t)s[(bo + 4) >> 2] | ((uint64_t)s[(bo + 8) >> 2] << 32);
+    const uint32_t sh = s[(bo + 12) >> 2];
+    auto byte = [&](int k) -> uint32_t {
+        return k < 8 ? (uint32_t)(sl >> (8 * k)) & 0xffu : (sh >> (8 * (k - 8))) & 0xffu;
+    };
+    const int p = j >> 1;
+    const int sa = 2 * p, sb = 2 * p + 1;
+    uint32_t sca, ma, scb, mb;
+    if (p < 2) {
+        sca = byte(sa) & 63; ma = byte(sa + 4) & 63;
+        scb = byte(sb) & 63; mb = byte(sb + 4) & 63;
+    } else {
+        sca = (byte(sa + 4) & 0xf) | ((byte(sa - 4) >> 6) << 4);
+        ma = (byte(sa + 4) >> 4) | ((byte(sa) >> 6) << 4);
+        scb = (byte(sb + 4) & 0xf) | ((byte(sb - 4) >> 6) << 4);
+        mb = (byte(sb + 4) >> 4) | ((byte(sb) >> 6) << 4);
+    }
+    const uint4 q = *(const uint4*)(s + ((bo + 16 + 16 * j) >> 2));
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    float lo[T], hi[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) { lo[t] = 0.f; hi[t] = 0.f; }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t l4 = qw[k] & 0x0f0f0f0fu, h4 = (qw[k] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const float fl = ub(l4, n), fh = ub(h4, n);
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                lo[t] = fmaf(fl, xr[t][4 * k + n], lo[t]);
+                hi[t] = fmaf(fh, xr[t][16 + 4 * k + n], hi[t]);
+            }
+        }
+    }
+    const float da = d * (float)sca, mma = dmin * (float)ma;
+    const float db = d * (float)scb, mmb = dmin * (float)mb;
+#pragma unroll
+    for (int t = 0; t < T; t++)
+        acc[t] += (da * lo[t] - mma * sx[t][0]) + (db * hi[t] - mmb * sx[t][1]);
+}
+
+// Q5_K (qw6.c:1518-1548): as Q4_K with a fifth bit from qh.
+template <int T>
+__device__ __forceinline__ void unit_q5k(const uint32_t* s, uint32_t bo, int j,
+                                         const float (&xr)[T][32], const float (&sx)[T][4],
+                                         float (&acc)[T]) {
+    const uint32_t dm = s[bo >> 2];
+    const float d = h2f(dm & 0xffffu), dmin = h2f(dm >> 16);
+    const uint64_t sl = (uint64_t)s[(bo + 4) >> 2] | ((uint64_t)s[(bo + 8) >> 2] << 32);
+    const uint32_t sh = s[(bo + 12) >> 2];
+    auto byte = [&](int k) -> uint32_t {
+        return k < 8 ? (uint32_t)(sl >> (8 * k)) & 0xffu : (sh >> (8 * (k - 8))) & 0xffu;
+    };
+    const int p = j >> 1;
+    const int sa = 2 * p, sb = 2 * p + 1;
+    uint32_t sca, ma, scb, mb;
+    if (p < 2) {
+        sca = byte(sa) & 63; ma = byte(sa + 4) & 63;
+        scb = byte(sb) & 63; mb = byte(sb + 4) & 63;
+    } else {
+        sca = (byte(sa + 4) & 0xf) | ((byte(sa - 4) >> 6) << 4);
+        ma = (byte(sa + 4) >> 4) | ((byte(sa) >> 6) << 4);
+        scb = (byte(sb + 4) & 0xf) | ((byte(sb - 4) >> 6) << 4);
+        mb = (byte(sb + 4) >> 4) | ((byte(sb) >> 6) << 4);
+    }
+    const uint4 q = *(const uint4*)(s + ((bo + 48 + 16 * j) >> 2));
+    const uint4 h = *(const uint4*)(s + ((bo + 16 + 16 * (j & 1)) >> 2));
+    const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
+    const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
+    float lo[T], hi[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) { lo[t] = 0.f; hi[t] = 0.f; }
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t l5 = (qw[k] & 0x0f0f0f0fu) | (((hw[k] >> sa) & 0x01010101u) << 4);
+        const uint32_t h5 = ((qw[k] >> 4) & 0x0f0f0f0fu) | (((hw[k] >> sb) & 0x01010101u) << 4);
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const float fl = ub(l5, n), fh = ub(h5, n);
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                lo[t] = fmaf(fl, xr[t][4 * k + n], lo[t]);
+                hi[t] = fmaf(fh, xr[t][16 + 4 * k + n], hi[t]);
+            }
+        }
+    }
+    const float da = d * (float)sca, mma = dmin * (float)ma;
+    const float db = d * (float)scb, mmb = dmin * (float)mb;
+#pragma unroll
+    for (int t = 0; t < T; t++)
+        acc[t] += (da * lo[t] - mma * sx[t][0]) + (db * hi[t] - mmb * sx[t][1]);
+}
+
+// Q6_K (qw6.c:1550-1578), qw6's even-scale rule: the 32-run k of half h uses
+// scales[8h + 2k] for all its weights.
+template <int T>
+__device__ __forceinline__ void unit_q6k(const uint32_t* s, uint32_t bo, int j,
+                                         const float (&xr)[T][32], const float (&sx)[T][4],
+                                         float (&acc)[T]) {
+    const int h = j >> 2, lq = j & 3;
+    const uint32_t oa = bo + 64 * h + 8 * lq;
+    const uint32_t a0 = lds32(s, oa), a1 = lds32(s, oa + 4);
+    const uint32_t b0 = lds32(s, oa + 32), b1 = lds32(s, oa + 36);
+    const uint32_t oh = bo + 128 + 32 * h + 8 * lq;
+    const uint32_t h0 = lds32(s, oh), h1 = lds32(s, oh + 4);
+    const uint32_t sc0 = lds32(s, bo + 192 + 8 * h), sc1 = lds32(s, bo + 196 + 8 * h);
+    const float d = h2f(lds16(s, bo + 208));
+    const float sc[4] = {(float)(int8_t)(sc0 & 0xff), (float)(int8_t)((sc0 >> 16) & 0xff),
+                         (float)(int8_t)(sc1 & 0xff), (float)(int8_t)((sc1 >> 16) & 0xff)};
+    const uint32_t aw[2] = {a0, a1}, bw[2] = {b0, b1}, hw[2] = {h0, h1};
+    float part[T][4];
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) part[t][k] = 0.f;
+#pragma unroll
+    for (int w = 0; w < 2; w++) {
+        const uint32_t v0 = (aw[w] & 0x0f0f0f0fu) | ((hw[w] & 0x03030303u) << 4);
+        const uint32_t v1 = (bw[w] & 0x0f0f0f0fu) | (((hw[w] >> 2) & 0x03030303u) << 4);
+        const uint32_t v2 = ((aw[w] >> 4) & 0x0f0f0f0fu) | (((hw[w] >> 4) & 0x03030303u) << 4);
+        const uint32_t v3 = ((bw[w] >> 4) & 0x0f0f0f0fu) | (((hw[w] >> 6) & 0x03030303u) << 4);
+        const uint32_t vv[4] = {v0, v1, v2, v3};
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+#pragma unroll
+            for (int n = 0; n < 4; n++) {
+                const float fv = ub(vv[k], n);
+#pragma unroll
+                for (int t = 0; t < T; t++)
+                    part[t][k] = fmaf(fv, xr[t][8 * k + 4 * w + n], part[t][k]);
+            }
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        float r = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) r += (d * sc[k]) * (part[t][k] - 32.f * sx[t][k]);
+        acc[t] += r;
+    }
+}
+
+// IQ2_XXS (qw6.c:1580-1602).
+template <int T>
+__device__ __forceinline__ void unit_iq2xxs(const uint32_t* s, uint32_t bo, int j,
+                                            const uint32_t* tab, const float (&xr)[T][32],
+                                            float (&acc)[T]) {
+    const uint32_t aux0 = lds32(s, bo + 2 + 8 * j), aux1 = lds32(s, bo + 6 + 8 * j);
+    const float d = h2f(lds16(s, bo));
+    const float db = d * (0.5f + (float)(aux1 >> 28)) * 0.25f;
+    float sum[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) sum[t] = 0.f;
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+        const uint64_t g = lds64_tab(tab, kTabOffIq2xxs + 8 * ((aux0 >> (8 * l)) & 0xffu));
+        const uint32_t s7 = (aux1 >> (7 * l)) & 127u;
+        const uint32_t signs = s7 | ((__builtin_popcount(s7) & 1u) << 7);
+        const uint32_t g0 = (uint32_t)g, g1 = (uint32_t)(g >> 32);
+#pragma unroll
+        for (int n = 0; n < 8; n++) {
+            const float gv = ub(n < 4 ? g0 : g1, n & 3);
+#pragma unroll
+            for (int t = 0; t < T; t++) sum[t] = fmaf(gv, sgn(xr[t][8 * l + n], signs, n), sum[t]);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) acc[t] += db * sum[t];
+}
+
+// IQ2_S (qw6.c:1604-1630).
+template <int T>
+__device__ __forceinline__ void unit_iq2s(const uint32_t* s, uint32_t bo, int j,
+                                          const uint32_t* tab, const float (&xr)[T][32],
+                                          float (&acc)[T]) {
+    const uint32_t qs4 = lds32(s, bo + 2 + 4 * j), sg4 = lds32(s, bo + 34 + 4 * j);
+    const uint32_t qh = lds8(s, bo + 66 + j), sc = lds8(s, bo + 74 + j);
+    const float d = h2f(lds16(s, bo));
+    const float db0 = d * (0.5f + (float)(sc & 0xf)) * 0.25f;
+    const float db1 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
+    float s0[T], s1[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) { s0[t] = 0.f; s1[t] = 0.f; }
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+        const uint32_t gi = ((qs4 >> (8 * l)) & 0xffu) | ((qh << (8 - 2 * l)) & 0x300u);
+        const uint64_t g = lds64_tab(tab, kTabOffIq2s + 8 * gi);
+        const uint32_t signs = (sg4 >> (8 * l)) & 0xffu;
+        const uint32_t g0 = (uint32_t)g, g1 = (uint32_t)(g >> 32);
+#pragma unroll
+        for (int n = 0; n < 8; n++) {
+            const float gv = ub(n < 4 ? g0 : g1, n & 3);
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                if (l < 2) s0[t] = fmaf(gv, sgn(xr[t][8 * l + n], signs, n), s0[t]);
+                else s1[t] = fmaf(gv, sgn(xr[t][8 * l + n], signs, n), s1[t]);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) acc[t] += db0 * s0[t] + db1 * s1[t];
+}
+
+// IQ3_S (qw6.c:1632-1672).
+template <int T>
+__device__ __forceinline__ void unit_iq3s(const uint32_t* s, uint32_t bo, int j,
+                                          const uint32_t* tab, const float (&xr)[T][32],
+                                          float (&acc)[T]) {
+    const uint32_t qa = lds32(s, bo + 2 + 8 * j), qb = lds32(s, bo + 6 + 8 * j);
+    const uint32_t qh = lds8(s, bo + 66 + j);
+    const uint32_t sg4 = lds32(s, bo + 74 + 4 * j);
+    const uint32_t scb = lds8(s, bo + 106 + (j >> 1));
+    const uint32_t nib = (j & 1) ? (scb >> 4) : (scb & 0xf);
+    const float d = h2f(lds16(s, bo));
+    const float db = d * (float)(1 + 2 * (int)nib);
+    float sum[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) sum[t] = 0.f;
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+        const uint32_t qw = l < 2 ? qa : qb;
+        const uint32_t i1 = ((qw >> (16 * (l & 1))) & 0xffu) | ((qh << (8 - 2 * l)) & 256u);
+        const uint32_t i2 = ((qw >> (16 * (l & 1) + 8)) & 0xffu) | ((qh << (7 - 2 * l)) & 256u);
+        const uint32_t g1 = tab[(kTabOffIq3s >> 2) + i1];
+        const uint32_t g2 = tab[(kTabOffIq3s >> 2) + i2];
+        const uint32_t signs = (sg4 >> (8 * l)) & 0xffu;
+#pragma unroll
+        for (int n = 0; n < 4; n++) {
+            const float v1 = ub(g1, n), v2 = ub(g2, n);
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                sum[t] = fmaf(v1, sgn(xr[t][8 * l + n], signs, n), sum[t]);
+                sum[t] = fmaf(v2, sgn(xr[t][8 * l + 4 + n], signs, n + 4), sum[t]);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < T; t++) acc[t] += db * sum[t];
+}
+
+template <int T>
+__device__ __forceinline__ void unit_dot(int f, const uint32_t* s, uint32_t bo, int j,
+                                         const uint32_t* tab, const float (&xr)[T][32],
+                                         const float (&sx)[T][4], float (&acc)[T]) {
+    switch (f) {
+    case F_Q4K: unit_q4k<T>(s, bo, j, xr, sx, acc); break;
+    case F_Q5K: unit_q5k<T>(s, bo, j, xr, sx, acc); break;
+    case F_Q6K: unit_q6k<T>(s, bo, j, xr, sx, acc); break;
+    case F_IQ2XXS: unit_iq2xxs<T>(s, bo, j, tab, xr, acc); break;
+    case F_IQ2S: unit_iq2s<T>(s, bo, j, tab, xr, acc); break;
+    default: unit_iq3s<T>(s, bo, j, tab, xr, acc); break;
+    }
+}
+
+// ---- reductions ----------------------------------------------------------------
+
+// Sum over aligned groups of `g` lanes (g a power of two <= 64).
+__device__ __forceinline__ float group_sum(float v, uint32_t g) {
+    for (uint32_t m = g >> 1; m >= 1; m >>= 1) v += __shfl_xor(v, (int)m, 64);
+    return v;
+}
+
+// ---- synthetic data hash (twin of qw6_amd/synth.py) ------------------------------
+
+__host__ __device__ inline uint64_t sm_mix(uint64_t z) {
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+__host__ __device__ inline uint64_t sm_stream_key(uint64_t seed, uint64_t stream) {
+    const uint64_t k = sm_mix(seed + 0x632BE59BD9B4E019ull);
+    return sm_mix(k ^ (stream * 0xD1B54A32D192ED03ull));
+}
+__host__ __device__ inline uint64_t sm_hash(uint64_t key, uint64_t i) {
+    return sm_mix(key + (i + 1) * 0x9E3779B97F4A7C15ull);
+}
+// Irwin-Hall(12) standard normal from hashes hidx, hidx+1, hidx+2.
+__host__ __device__ inline float sm_normal(uint64_t key, uint64_t hidx) {
+    int64_t s = 0;
+    for (int t = 0; t < 3; t++) {
+        const uint64_t h = sm_hash(key, hidx + t);
+        for (int q = 0; q < 4; q++) s += (int64_t)((h >> (16 * q)) & 0xffffu);
+    }
+    return (float)(s - 393210) * (1.0f / 65536.0f);
+}
+
+}  // namespace qw6

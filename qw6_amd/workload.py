@@ -1,0 +1,110 @@
+"""Seeded synthetic MoE layers resident on the device.
+
+Weights are generated in HBM by the library's synth kernels (the device twin
+of qw6_amd.synth), expert matrices laid out as GGUF expert packs: expert e of
+a pack at base + e * expert_bytes (bind_expert_pack, qw6.c:542-597), every
+expert 256-byte aligned. Mixed per-expert quants (IQ3_S / IQ2_S downs) get
+per-expert sizes in one pack.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import Context, make_layer
+from . import synth as S
+from . import synth_blocks, synth_normal
+
+MIXES = {
+    "q4k": (S.Q_Q4_K_M, lambda e: S.Q_Q6_K),
+    "iq2m": (S.Q_IQ2_XXS, lambda e: S.Q_IQ3_S if e % 2 == 0 else S.Q_IQ2_S),
+}
+SHARED_Q = (S.Q_Q4_K_M, S.Q_Q4_K_M, S.Q_Q6_K)
+
+
+def _align(n: int, a: int = 256) -> int:
+    return (n + a - 1) // a * a
+
+
+class SynthLayer:
+    """One MoE layer generated on the device (torch uint8/float32 buffers)."""
+
+    def __init__(self, ctx: Context, seed: int, layer: int = 0, mix: str = "q4k",
+                 shared: bool = True, hidden: int = 2048, inter: int = 512,
+                 n_experts: int = 256, top_k: int = 8, router: bool = True):
+        import torch
+        self.ctx, self.seed, self.layer, self.mix = ctx, seed, layer, mix
+        self.hidden, self.inter, self.n_experts, self.top_k = hidden, inter, n_experts, top_k
+        dev = torch.device("cuda", ctx.device)
+        gq, down_fn = MIXES[mix]
+        self.quants = [(gq, gq, down_fn(e)) for e in range(n_experts)]
+        shapes = ((inter, hidden), (inter, hidden), (hidden, inter))
+        kinds = (S.K_GATE, S.K_UP, S.K_DOWN)
+        self.packs, self.offsets, self.mats = [], [], []
+        for k in range(3):
+            sizes = [S.row_bytes(self.quants[e][k], shapes[k][1]) * shapes[k][0]
+                     for e in range(n_experts)]
+            offs = np.cumsum([0] + [_align(s) for s in sizes])
+            buf = torch.empty(int(offs[-1]), dtype=torch.uint8, device=dev)
+            for e in range(n_experts):
+                q = self.quants[e][k]
+                nb = shapes[k][0] * shapes[k][1] // 256
+                synth_blocks(buf.data_ptr() + int(offs[e]), q, nb, seed,
+                             S.stream_id(layer, kinds[k], e))
+            self.packs.append(buf)
+            self.offsets.append(offs)
+            self.mats.append([(buf.data_ptr() + int(offs[e]), self.quants[e][k], shapes[k][0],
+                               shapes[k][1]) for e in range(n_experts)])
+        self.router = None
+        if router:
+            self.router = torch.empty(n_experts * hidden, dtype=torch.float32, device=dev)
+            synth_normal(self.router, n_experts * hidden, 0.02, seed,
+                         S.stream_id(layer, S.K_ROUTER))
+        self.shared = None
+        self.shared_bufs = []
+        if shared:
+            sh = []
+            for k, q, kind in zip(range(3), SHARED_Q, (S.K_SGATE, S.K_SUP, S.K_SDOWN)):
+                r, c = shapes[k]
+                buf = torch.empty(S.row_bytes(q, c) * r, dtype=torch.uint8, device=dev)
+                synth_blocks(buf, q, r * c // 256, seed, S.stream_id(layer, kind))
+                self.shared_bufs.append(buf)
+                sh.append((buf.data_ptr(), q, r, c))
+            self.shared = tuple(sh)
+        self.experts = ctx.experts(*self.mats)
+        self.desc = make_layer(hidden, inter, top_k, self.experts, router=self.router,
+                               shared=self.shared)
+        torch.cuda.synchronize()
+
+    # ---- bytes a decode step must read -------------------------------------------
+    def expert_bytes(self, e: int) -> int:
+        shapes = ((self.inter, self.hidden), (self.inter, self.hidden), (self.hidden, self.inter))
+        return sum(S.row_bytes(self.quants[e][k], shapes[k][1]) * shapes[k][0] for k in range(3))
+
+    def shared_bytes(self) -> int:
+        if self.shared is None:
+            return 0
+        return sum(S.row_bytes(m[1], m[3]) * m[2] for m in self.shared)
+
+    # ---- host copies (for the CPU checker and the CPU baseline) ---------------------
+    def expert_host(self, e: int):
+        out = []
+        shapes = ((self.inter, self.hidden), (self.inter, self.hidden), (self.hidden, self.inter))
+        for k in range(3):
+            q = self.quants[e][k]
+            n = S.row_bytes(q, shapes[k][1]) * shapes[k][0]
+            o = int(self.offsets[k][e])
+            out.append((self.packs[k][o:o + n].cpu().numpy(), q))
+        return tuple(out)
+
+    def shared_host(self):
+        if self.shared is None:
+            return None
+        return tuple((b.cpu().numpy(), m[1]) for b, m in zip(self.shared_bufs, self.shared))
+
+    def router_host(self) -> np.ndarray:
+        return self.router.cpu().numpy()
+
+    def free(self):
+        self.experts.free()
+        self.packs = self.shared_bufs = []
+        self.router = None
