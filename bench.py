@@ -163,16 +163,19 @@ def main():
     ctx.profile(0)
     kus = [1e3 * m / calls for m in ms]
     gu_b = float(np.mean(gu_bytes))
-    achieved = gu_b / (kus[1] * 1e-6) / 1e9
-    r_b = N_EXPERTS * HIDDEN * 4 + pool[0].shared_bytes() * 2 / 3 + HIDDEN * 4
+    achieved = gu_b / (kus[2] * 1e-6) / 1e9
+    sh_gu = sum(S.row_bytes(m[1], m[3]) * m[2] for m in pool[0].shared[:2])
+    r_b = N_EXPERTS * HIDDEN * 4 + sh_gu + HIDDEN * 4 + N_EXPERTS * 4
+    rt_b = N_EXPERTS * 4
     d_b = bytes_per_step - r_b - gu_b
     kernels = {
         "moe_router": {"us": round(kus[0], 2), "bytes": int(r_b),
                        "GBps": round(r_b / kus[0] / 1e3, 1)},
-        "moe_gate_up": {"us": round(kus[1], 2), "bytes": int(gu_b),
+        "moe_route": {"us": round(kus[1], 2), "bytes": int(rt_b)},
+        "moe_gate_up": {"us": round(kus[2], 2), "bytes": int(gu_b),
                         "GBps": round(achieved, 1)},
-        "moe_down": {"us": round(kus[2], 2), "bytes": int(d_b),
-                     "GBps": round(d_b / kus[2] / 1e3, 1)},
+        "moe_down": {"us": round(kus[3], 2), "bytes": int(d_b),
+                     "GBps": round(d_b / kus[3] / 1e3, 1)},
     }
     log("graph %.2f us/layer, eager %.2f us/layer, kernels %s" % (us_layer, eager_us, kernels))
 

@@ -149,11 +149,11 @@ int qw6_hip_set_mode(qw6_hip_ctx_t *ctx, int mode);
 
 /* Per-kernel timing of qw6_hip_moe_forward with HIP events on its launch
  * stream (eager calls only, not under graph capture). max_calls > 0 starts
- * recording for up to that many calls (events between the three decode
+ * recording for up to that many calls (events between the four decode
  * kernels), 0 stops. qw6_hip_profile_read synchronizes and returns the summed
- * elapsed ms of [router, gate_up, down] over the recorded calls. */
+ * elapsed ms of [router, route, gate_up, down] over the recorded calls. */
 int qw6_hip_profile(qw6_hip_ctx_t *ctx, uint32_t max_calls);
-int qw6_hip_profile_read(qw6_hip_ctx_t *ctx, float ms[3], uint32_t *calls);
+int qw6_hip_profile_read(qw6_hip_ctx_t *ctx, float ms[4], uint32_t *calls);
 
 /* y = rmsnorm(x) * w per token (qw6_cpu_rmsnorm, qw6.c:2503-2513). */
 int qw6_hip_rmsnorm(qw6_hip_ctx_t *ctx, const float *x, const float *w,

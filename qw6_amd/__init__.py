@@ -51,6 +51,12 @@ def lib():
     """Load libqw6_hip.so; raises if it was not built (no CPU fallback)."""
     global _lib
     if _lib is None:
+        # Load torch's HIP runtime first when torch is present: the library
+        # then binds to the same libamdhip64.so.7 instead of a second copy.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         if not LIB_PATH.exists():
             raise Qw6HipError("%s not built (run python -m qw6_amd.build)" % LIB_PATH)
         L = C.CDLL(str(LIB_PATH))
@@ -238,7 +244,7 @@ class Context:
         _check(lib().qw6_hip_profile(self.handle, max_calls))
 
     def profile_read(self):
-        ms = (C.c_float * 3)()
+        ms = (C.c_float * 4)()
         n = C.c_uint32()
         _check(lib().qw6_hip_profile_read(self.handle, ms, C.byref(n)))
         return list(ms), n.value

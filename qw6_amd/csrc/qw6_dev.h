@@ -460,11 +460,66 @@ __device__ __forceinline__ void unit_dot(int f, const uint32_t* s, uint32_t bo, 
 }
 
 // ---- reductions ----------------------------------------------------------------
+// Lane exchanges at distance m within aligned groups, without LDS traffic:
+// m = 32 / 16 swap halves / odd-even rows with the gfx950 permlane swaps,
+// m = 8 / 4 pair mirror lanes (DPP row_mirror / row_half_mirror), m = 2 / 1
+// use DPP quad permutes. For a reduction only the pairing between the two
+// halves of each 2m-block matters, so mirror partners serve like xor ones.
 
-// Sum over aligned groups of `g` lanes (g a power of two <= 64).
+__device__ __forceinline__ float partner(float v, uint32_t m, uint32_t lane) {
+    const uint32_t u = __float_as_uint(v);
+    switch (m) {
+    case 32: {
+        const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+        return __uint_as_float((lane & 32u) ? r[0] : r[1]);
+    }
+    case 16: {
+        const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+        return __uint_as_float((lane & 16u) ? r[0] : r[1]);
+    }
+    case 8: return __uint_as_float(__builtin_amdgcn_update_dpp(0u, u, 0x140, 0xf, 0xf, false));
+    case 4: return __uint_as_float(__builtin_amdgcn_update_dpp(0u, u, 0x141, 0xf, 0xf, false));
+    case 2: return __uint_as_float(__builtin_amdgcn_update_dpp(0u, u, 0x4e, 0xf, 0xf, false));
+    default: return __uint_as_float(__builtin_amdgcn_update_dpp(0u, u, 0xb1, 0xf, 0xf, false));
+    }
+}
+
+// Sum over aligned groups of g lanes (g a power of two <= 64); every lane of
+// a group receives the sum.
 __device__ __forceinline__ float group_sum(float v, uint32_t g) {
-    for (uint32_t m = g >> 1; m >= 1; m >>= 1) v += __shfl_xor(v, (int)m, 64);
+    const uint32_t lane = threadIdx.x & 63u;
+    for (uint32_t m = g >> 1; m >= 1; m >>= 1) v += partner(v, m, lane);
     return v;
+}
+
+// Reduce-scatter: each lane holds S partial sums v[0..S) (one per row step)
+// of a group of g lanes (S <= g). Returns the full group sum of step
+// s = (lane & (g-1)) >> log2(g/S); all lanes of each g/S sub-group get it.
+template <int S>
+__device__ __forceinline__ float reduce_scatter(float (&v)[S], uint32_t g) {
+    const uint32_t lane = threadIdx.x & 63u;
+    float w[S];
+#pragma unroll
+    for (int i = 0; i < S; i++) w[i] = v[i];
+    uint32_t m = g >> 1;
+#pragma unroll
+    for (int n = S / 2; n >= 1; n /= 2) {
+        const bool up = (lane & m) != 0;
+#pragma unroll
+        for (int i = 0; i < n; i++) {
+            const float a = w[i], b = w[i + n];
+            w[i] = (up ? b : a) + partner(up ? a : b, m, lane);
+        }
+        m >>= 1;
+    }
+    float r = w[0];
+    for (; m >= 1; m >>= 1) r += partner(r, m, lane);
+    return r;
+}
+
+template <int S>
+__device__ __forceinline__ uint32_t scatter_step(uint32_t lane, uint32_t g) {
+    return S == 1 ? 0u : (lane & (g - 1)) / (g / S);
 }
 
 // ---- synthetic data hash (twin of qw6_amd/synth.py) ------------------------------

@@ -1,23 +1,27 @@
 // qw6_hip.hip -- gfx950 kernels and C ABI of the routed-expert MoE FFN path.
 //
-// Decode path (fp32 accumulation), three kernels per MoE layer:
-//   moe_router : router GEMV over all experts; the last workgroup to finish
-//                (device-scope counter) runs the softmax top-k for every token
-//                and builds the list of distinct selected experts ("slots");
-//                extra workgroups run the shared expert's gate/up/SiLU, which
-//                does not depend on routing.
-//   moe_gate_up: one workgroup per (slot, row tile): stages the tile's gate
-//                and up rows into LDS with direct-to-LDS 16-byte loads, then
-//                dequantizes in registers and writes silu(gate) * up.
-//   moe_down   : one workgroup per tile of output rows, over all slots plus the
-//                shared expert in a fixed order, gate-weighted combine (and
-//                residual) in registers -- no atomics, deterministic.
+// Decode path (fp32 accumulation), four kernels per MoE layer:
+//   moe_router : router GEMV over all experts (one wave per expert row); extra
+//                workgroups run the shared expert's gate/up/SiLU, which does
+//                not depend on routing.
+//   moe_route  : one workgroup: softmax top-k of every token, distinct
+//                selected experts numbered in first-use order ("slots"),
+//                their matrices resolved into slot descriptors.
+//   moe_gate_up: one workgroup per (slot, row tile): each wave streams its
+//                rows into LDS with direct-to-LDS 16-byte loads and
+//                dequantizes step s while step s+1 is still in flight;
+//                writes silu(gate) * up.
+//   moe_down   : one workgroup per tile of output rows, one wave per selected
+//                expert (plus the shared one); per-expert row sums meet in LDS
+//                and are combined in selection order, with the residual --
+//                no atomics, deterministic.
 // Routing never leaves the device (qw6's Vulkan path reads idx/w back to the
 // host per layer, qw6_vk.c:3371-3374).
 //
 // Lane mapping: a row of K columns has U = K/32 units of 32 weights
-// (qw6_dev.h); a wave covers 64/U rows per step, lane -> (row, unit) fixed,
-// so each lane keeps its unit's activations in registers across rows.
+// (qw6_dev.h); a wave covers 64/U rows per step with lane -> (row, unit)
+// fixed, so each lane keeps its unit's activations in registers across rows,
+// and the rows of one step are always 8 GGUF blocks (<= 1680 bytes).
 
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
@@ -25,6 +29,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <type_traits>
 #include <vector>
 
 #include "../../include/qw6_hip.h"
@@ -39,6 +44,7 @@ __device__ const IqTables g_tabs = make_tables();
 constexpr int kWG = 256;           // threads per workgroup (4 waves)
 constexpr uint32_t kMaxTok = 4;    // tokens per decode launch
 constexpr uint32_t kLdsBudget = 64 * 1024;
+constexpr int kProfEv = 5;         // events per profiled MoE call (4 kernels)
 
 thread_local char g_err[512];
 
@@ -65,29 +71,33 @@ typedef __attribute__((address_space(1))) void glb_void_t;
 // ---- staging: global bytes -> LDS ----------------------------------------------
 
 // Copy `bytes` (even) from 16-byte-aligned global src to 16-byte-aligned LDS
-// dst with all threads of the workgroup: 16-byte direct-to-LDS loads for the
-// body, 2-byte copies for the tail. The caller waits (stage_wait) before use.
-__device__ __forceinline__ void stage(uint8_t* dst, const uint8_t* src, uint32_t bytes) {
-    const uint32_t tid = threadIdx.x, wave = tid >> 6;
+// dst with the waves [w0, w0 + nw) of the workgroup: 16-byte direct-to-LDS
+// loads (gfx950 global_load_lds_dwordx4; a wave's 64 lanes fill 1 KB) for the
+// body, 2-byte copies for the tail. Waves outside the range return at once.
+// The caller waits (stage_wait / wave_wait) before reading.
+__device__ __forceinline__ void stage(uint8_t* dst, const uint8_t* src, uint32_t bytes,
+                                      uint32_t w0 = 0, uint32_t nw = 0xffffu) {
+    const uint32_t wave = (threadIdx.x >> 6) - w0, lane = threadIdx.x & 63u;
+    const uint32_t nwv = min(nw, (uint32_t)(blockDim.x >> 6));
+    if (wave >= nwv) return;
     const uint32_t n16 = bytes >> 4;
-    for (uint32_t c0 = 0; c0 < n16; c0 += kWG) {
-        const uint32_t wbase = c0 + wave * 64;
-        if (wbase < n16) {
-            const uint32_t c = c0 + tid;
-            if (c < n16)
-                __builtin_amdgcn_global_load_lds((glb_void_t*)(src + 16ull * c),
-                                                 (lds_void_t*)(dst + 16u * wbase), 16, 0, 0);
-        }
+    for (uint32_t c0 = wave * 64; c0 < n16; c0 += nwv * 64) {
+        const uint32_t c = c0 + lane;
+        if (c < n16)
+            __builtin_amdgcn_global_load_lds((glb_void_t*)(src + 16ull * c),
+                                             (lds_void_t*)(dst + 16u * c0), 16, 0, 0);
     }
     const uint32_t rem = (bytes & 15u) >> 1;
-    if (tid < rem) {
-        const uint16_t v = ((const uint16_t*)(src + 16ull * n16))[tid];
-        ((uint16_t*)(dst + 16u * n16))[tid] = v;
+    if (wave == 0 && lane < rem) {
+        const uint16_t v = ((const uint16_t*)(src + 16ull * n16))[lane];
+        ((uint16_t*)(dst + 16u * n16))[lane] = v;
     }
 }
 
+__device__ __forceinline__ void wave_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 __device__ __forceinline__ void stage_wait() {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    wave_wait();
     __syncthreads();
 }
 
@@ -103,6 +113,8 @@ __host__ __device__ inline uint32_t tab_bytes(uint32_t mask) {
     return mask & 4u ? kTabBytes : mask & 2u ? kTabOffIq3s : mask & 1u ? kTabOffIq2s : 0u;
 }
 
+__host__ __device__ inline uint32_t align16(uint32_t n) { return (n + 15u) & ~15u; }
+
 // ---- one matrix tile: per-row dot products --------------------------------------
 
 struct MatD {
@@ -111,53 +123,77 @@ struct MatD {
     uint32_t rows, cols, rb;   // rb: bytes per row
 };
 
-// Rows [0, rows_valid) of a tile staged at LDS word pointer `tile`; wave w
-// processes steps s: local row = (w*steps + s)*rps + lane/U. emit(row, acc)
-// is called on the first lane of each row group.
-template <int T, typename Emit>
-__device__ __forceinline__ void tile_rows(int f, const uint32_t* lds, uint32_t tile_off,
-                                          uint32_t rb, uint32_t K, const float* x,
-                                          uint32_t ldx, const uint32_t* tab,
-                                          uint32_t rows_valid, uint32_t steps, Emit emit) {
+// Row tile staged in LDS at byte offset tile_off (rows [0, rows_valid)).
+// Wave `wave` owns S steps of rps = 64/U rows: local row of step s for lane
+// group q = lane/U is (wave*S + s)*rps + q. Each lane accumulates its unit's
+// partial sums for all S steps, then one reduce-scatter per token leaves step
+// scatter_step<S>(lane) on each lane; emit(row, value[T]) runs on the first
+// lane of each sub-group that owns a row.
+template <int T, int S, int FF, typename Emit>
+__device__ __forceinline__ void tile_rows(int f_rt, const uint32_t* lds, uint32_t tile_off,
+                                          uint32_t rb, uint32_t K, const float (&xr)[T][32],
+                                          const float (&sx)[T][4], uint32_t rows_valid,
+                                          uint32_t wave, Emit emit) {
+    const int f = FF >= 0 ? FF : f_rt;
     const uint32_t U = K >> 5, rps = 64 / U;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t unit = lane & (U - 1), blk = unit >> 3;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t unit = lane & (U - 1), blk = unit >> 3, q = lane / U;
     const int j = (int)(unit & 7);
     const uint32_t bb = fmt_block_bytes(f);
-    float xr[T][32], sx[T][4];
+    float acc[T][S];
 #pragma unroll
-    for (int t = 0; t < T; t++) load_unit_x(f, x + (size_t)t * ldx, blk, j, xr[t], sx[t]);
-    for (uint32_t s = 0; s < steps; s++) {
-        const uint32_t rl = (wave * steps + s) * rps + lane / U;
-        float acc[T];
+    for (int s = 0; s < S; s++) {
+        const uint32_t rl = (wave * S + s) * rps + q;
+        float a[T];
 #pragma unroll
-        for (int t = 0; t < T; t++) acc[t] = 0.f;
-        if (rl < rows_valid) unit_dot<T>(f, lds, tile_off + rl * rb + blk * bb, j, tab, xr, sx, acc);
+        for (int t = 0; t < T; t++) a[t] = 0.f;
+        if (rl < rows_valid) unit_dot<T>(f, lds, tile_off + rl * rb + blk * bb, j, lds, xr, sx, a);
 #pragma unroll
-        for (int t = 0; t < T; t++) acc[t] = group_sum(acc[t], U);
-        if (unit == 0 && rl < rows_valid) emit(rl, acc);
+        for (int t = 0; t < T; t++) acc[t][s] = a[t];
     }
+    float r[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) r[t] = reduce_scatter<S>(acc[t], U);
+    const uint32_t s = scatter_step<S>(lane, U);
+    const uint32_t rl = (wave * S + s) * rps + q;
+    if ((unit & (U / S - 1)) == 0 && rl < rows_valid) emit(rl, r);
+}
+
+template <int T, int FF>
+__device__ __forceinline__ void load_x_all(int f_rt, const float* x, uint32_t ldx, uint32_t K,
+                                           float (&xr)[T][32], float (&sx)[T][4]) {
+    const int f = FF >= 0 ? FF : f_rt;
+    const uint32_t U = K >> 5;
+    const uint32_t unit = (threadIdx.x & 63) & (U - 1);
+#pragma unroll
+    for (int t = 0; t < T; t++) load_unit_x(f, x + (size_t)t * ldx, unit >> 3, (int)(unit & 7), xr[t], sx[t]);
 }
 
 // ---- single-matrix matvec --------------------------------------------------------
 
-template <int T>
+constexpr int kStepsMv = 4;
+
+template <int T, int FF>
 __global__ __launch_bounds__(kWG) void k_matvec(MatD W, const float* __restrict__ x,
                                                 float* __restrict__ y, uint32_t R,
-                                                uint32_t steps, uint32_t tmask) {
+                                                uint32_t tmask) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const uint32_t r0 = blockIdx.x * R;
     const uint32_t nv = min(R, W.rows - r0);
     const uint32_t toff = tab_bytes(tmask);
+    const uint32_t xoff = toff + align16(R * W.rb) + 16;
     stage_tables(smem, tmask);
     stage(smem + toff, W.p + (size_t)r0 * W.rb, nv * W.rb);
+    stage(smem + xoff, (const uint8_t*)x, T * W.cols * 4);
     stage_wait();
     const uint32_t* s = (const uint32_t*)smem;
-    tile_rows<T>(W.fmt, s, toff, W.rb, W.cols, x, W.cols, s, nv, steps,
-                 [&](uint32_t rl, const float(&acc)[T]) {
+    float xr[T][32], sx[T][4];
+    load_x_all<T, FF>(W.fmt, (const float*)(smem + xoff), W.cols, W.cols, xr, sx);
+    tile_rows<T, kStepsMv, FF>(W.fmt, s, toff, W.rb, W.cols, xr, sx, nv, threadIdx.x >> 6,
+                           [&](uint32_t rl, const float(&v)[T]) {
 #pragma unroll
-                     for (int t = 0; t < T; t++) y[(size_t)t * W.rows + r0 + rl] = acc[t];
-                 });
+                               for (int t = 0; t < T; t++) y[(size_t)t * W.rows + r0 + rl] = v[t];
+                           });
 }
 
 // Any K multiple of 256: one wave per row, lanes stride over the units, the
@@ -168,15 +204,10 @@ __global__ __launch_bounds__(64) void k_matvec_generic(MatD W, const float* __re
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const uint32_t r = blockIdx.x;
     const uint32_t toff = tab_bytes(tmask);
-    // 64-thread workgroup: reuse the 256-thread staging with idle upper chunks.
     const uint32_t lane = threadIdx.x;
-    const uint8_t* src = W.p + (size_t)r * W.rb;
-    const uint8_t* g = (const uint8_t*)&g_tabs;
-    for (uint32_t c = lane; c < toff / 16; c += 64)
-        ((uint4*)smem)[c] = ((const uint4*)g)[c];
-    for (uint32_t c = lane; c < W.rb / 2; c += 64)
-        ((uint16_t*)(smem + toff))[c] = ((const uint16_t*)src)[c];
-    __syncthreads();
+    stage_tables(smem, tmask);
+    stage(smem + toff, W.p + (size_t)r * W.rb, W.rb);
+    stage_wait();
     const uint32_t* s = (const uint32_t*)smem;
     const uint32_t U = W.cols >> 5, bb = fmt_block_bytes(W.fmt);
     float acc[T];
@@ -222,51 +253,68 @@ __global__ __launch_bounds__(64) void k_matvec_f32(const float* __restrict__ w,
 
 // ---- routing ---------------------------------------------------------------------
 
-// One wave: top_k rounds of (max value, lowest index), selected set to -inf,
-// then softmax over the selected values in selection order
-// (qw6_cpu_moe_route, qw6.c:2796-2827). Lane 0 writes idx/w.
-__device__ void wave_route(const float* logits, uint32_t n, uint32_t top_k, uint32_t* idx,
-                           float* w) {
+// Sortable 64-bit key of logit v at index e: the upper word maps the float
+// order onto unsigned order (-0 folded into +0, which compare equal), the
+// lower word is ~e so that equal values prefer the lower index.
+__device__ __forceinline__ uint64_t route_key(float v, uint32_t e) {
+    const uint32_t u = __float_as_uint(v + 0.0f);
+    const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t)k << 32) | (uint64_t)(~e);
+}
+
+// One wave: top_k rounds of (max value, lowest index), the winner set to
+// -inf, then softmax over the selected values in selection order
+// (qw6_cpu_moe_route, qw6.c:2796-2827). Branch-free: each round is a 64-bit
+// key maximum over the wave. Lane 0 writes idx/w (any memory). Inputs
+// without NaN reproduce qw6's indices exactly, including its ties and its
+// re-selection of an -inf entry once only -inf values remain.
+__device__ __forceinline__ void wave_route(const float* logits, uint32_t n, uint32_t top_k,
+                                           uint32_t* idx, float* w) {
     const uint32_t lane = threadIdx.x & 63;
-    float v[4];
+    uint64_t key[4];
+    const uint64_t none = 0;   // below every real key
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const uint32_t e = lane + 64u * i;
-        v[i] = e < n ? logits[e] : -INFINITY;
+        key[i] = e < n ? route_key(logits[e], e) : none;
     }
+    const uint64_t ninf = (uint64_t)(~0xff800000u & 0x7fffffffu) << 32;   // key(-inf) >> 32 << 32
     float sel[8];
     uint32_t sid[8];
-    for (uint32_t k = 0; k < top_k; k++) {
-        float bv = v[0];
-        uint32_t bi = lane < n ? lane : 0xffffffffu;
 #pragma unroll
-        for (int i = 1; i < 4; i++) {
-            const uint32_t e = lane + 64u * i;
-            if (e < n && (v[i] > bv || bi == 0xffffffffu)) { bv = v[i]; bi = e; }
-        }
-        for (int m = 32; m >= 1; m >>= 1) {
-            const float ov = __shfl_xor(bv, m, 64);
-            const uint32_t oi = (uint32_t)__shfl_xor((int)bi, m, 64);
-            if (oi != 0xffffffffu &&
-                (bi == 0xffffffffu || ov > bv || (ov == bv && oi < bi) ||
-                 (!(ov == ov) && !(bv == bv) && oi < bi))) {
-                bv = ov; bi = oi;
-            }
-        }
-        sel[k] = bv;
-        sid[k] = bi;
-        if ((bi & 63u) == lane) {
+    for (uint32_t k = 0; k < 8; k++) {
+        if (k >= top_k) break;
+        uint64_t best = key[0];
 #pragma unroll
-            for (int i = 0; i < 4; i++)
-                if (lane + 64u * i == bi) v[i] = -INFINITY;
+        for (int i = 1; i < 4; i++) best = key[i] > best ? key[i] : best;
+#pragma unroll
+        for (uint32_t m = 32; m >= 1; m >>= 1) {
+            const uint32_t lo = __float_as_uint(partner(__uint_as_float((uint32_t)best), m, lane));
+            const uint32_t hi = __float_as_uint(partner(__uint_as_float((uint32_t)(best >> 32)), m, lane));
+            const uint64_t o = ((uint64_t)hi << 32) | lo;
+            best = o > best ? o : best;
         }
+        const uint32_t e = ~(uint32_t)best;
+        const uint32_t ku = (uint32_t)(best >> 32);
+        const uint32_t fu = (ku & 0x80000000u) ? (ku & 0x7fffffffu) : ~ku;
+        sel[k] = __uint_as_float(fu);
+        sid[k] = e;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (lane + 64u * i == e) key[i] = ninf | (uint64_t)(~e);
     }
     if (lane == 0) {
         float mx = sel[0];
-        for (uint32_t k = 1; k < top_k; k++) mx = sel[k] > mx ? sel[k] : mx;
-        float e[8], sum = 0.f;
-        for (uint32_t k = 0; k < top_k; k++) { e[k] = expf(sel[k] - mx); sum += e[k]; }
-        for (uint32_t k = 0; k < top_k; k++) { idx[k] = sid[k]; w[k] = e[k] / sum; }
+#pragma unroll
+        for (uint32_t k = 1; k < 8; k++)
+            if (k < top_k) mx = sel[k] > mx ? sel[k] : mx;
+        float ex[8], sum = 0.f;
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++)
+            if (k < top_k) { ex[k] = expf(sel[k] - mx); sum += ex[k]; }
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++)
+            if (k < top_k) { idx[k] = sid[k]; w[k] = ex[k] / sum; }
     }
 }
 
@@ -284,74 +332,241 @@ struct ExpertEnt {            // device expert table entry
     uint32_t rb[3];
 };
 
+// Addressing of one matrix kind (gate / up / down) of the experts: a regular
+// pack (expert e at base + e * stride, one format; the GGUF expert pack of
+// bind_expert_pack, qw6.c:542-597) needs no memory round trip; otherwise the
+// per-expert table entry is loaded.
+struct PackRef {
+    const uint8_t* base;
+    uint64_t stride;
+    int32_t fmt;
+    uint32_t rb;
+    uint32_t regular;
+};
+
+constexpr int kStepsGu = 2;     // row steps per wave, gate/up
+constexpr int kStepsDn = 2;     // row steps per wave, down
+constexpr uint32_t kMaxSlots = kMaxTok * 8;
+constexpr uint32_t kSlotBytes = 2048;   // LDS slot of one step group (8 blocks <= 1680 B)
+
+// One selected expert ("slot"), resolved by the route kernel: its three
+// matrices and per-token gate weights. p[0] == nullptr marks an unused slot.
+struct SlotDesc {
+    const uint8_t* p[3];
+    int32_t fmt[3];
+    uint32_t rb[3];
+    float wt[kMaxTok];
+};
+
 struct MoeArgs {
     uint32_t hidden, inter, n_experts, top_k, T, max_u;
+    SlotDesc* slots;          // [max_u]
     const float* x;
     const float* router;
     const float* logits_in;
     const float* shared_router;
     const ExpertEnt* experts;
+    PackRef pk[3];
     MatD sg, su, sd;          // shared expert; sg.p == nullptr: none
     float* logits;            // [T][n_experts]
-    uint32_t* idx;            // [T][top_k]
-    float* w;                 // [T][top_k]
-    uint32_t* nslots;         // [1]
-    uint32_t* slot_e;         // [max_u] expert of each slot
-    float* wt;                // [max_u][T] gate weight of slot u for token t
     float* sw;                // [T] shared weight
     float* mid;               // [(max_u + 1)][T][inter], shared at max_u
-    uint32_t* counter;
     const float* residual;
     float* out;
     uint32_t* idx_out;
     float* w_out;
     uint32_t n_router_wg, rr_per_wg;     // router workgroups, rows per router WG
-    uint32_t rb_tile, rb_steps;          // gate/up tile rows and steps per wave
-    uint32_t rc_tile, rc_steps;          // down tile rows and steps per wave
+    uint32_t n_gu_waves;                 // waves per gate/up matrix pair
     uint32_t tmask_gu, tmask_dn;
 };
 
-// gate/up/silu for rows [r0, r0+R) of one expert -> mid[T][inter].
-template <int T>
-__device__ void gate_up_tile(const MatD& G, const MatD& Up, uint32_t r0, uint32_t R,
-                             uint32_t steps, const float* x, uint32_t hidden, float* mid,
-                             uint32_t inter, uint32_t tmask, uint8_t* smem) {
-    const uint32_t nv = min(R, G.rows - r0);
-    const uint32_t toff = tab_bytes(tmask);
-    const uint32_t gbytes = (nv * G.rb + 15u) & ~15u;
-    float* gv = (float*)(smem + toff + gbytes + ((nv * Up.rb + 15u) & ~15u) + 16);   // [R][T]
-    stage_tables(smem, tmask);
-    stage(smem + toff, G.p + (size_t)r0 * G.rb, nv * G.rb);
-    stage(smem + toff + gbytes, Up.p + (size_t)r0 * Up.rb, nv * Up.rb);
-    stage_wait();
-    const uint32_t* s = (const uint32_t*)smem;
-    tile_rows<T>(G.fmt, s, toff, G.rb, hidden, x, hidden, s, nv, steps,
-                 [&](uint32_t rl, const float(&acc)[T]) {
-#pragma unroll
-                     for (int t = 0; t < T; t++) gv[rl * T + t] = acc[t];
-                 });
-    __syncthreads();
-    tile_rows<T>(Up.fmt, s, toff + gbytes, Up.rb, hidden, x, hidden, s, nv, steps,
-                 [&](uint32_t rl, const float(&acc)[T]) {
-#pragma unroll
-                     for (int t = 0; t < T; t++) {
-                         const float g = gv[rl * T + t];
-                         mid[(size_t)t * inter + r0 + rl] = g / (1.0f + expf(-g)) * acc[t];
-                     }
-                 });
+__device__ __forceinline__ MatD expert_mat(const MoeArgs& a, uint32_t e, int k) {
+    const PackRef& P = a.pk[k];
+    const uint32_t rows = k < 2 ? a.inter : a.hidden, cols = k < 2 ? a.hidden : a.inter;
+    if (P.regular) return MatD{P.base + P.stride * e, P.fmt, rows, cols, P.rb};
+    const ExpertEnt& E = a.experts[e];
+    return MatD{E.p[k], E.fmt[k], rows, cols, E.rb[k]};
 }
 
+// Stage one step group (the rows one wave step covers: 8 GGUF blocks, a
+// multiple of 16 bytes, <= 1680 B) into a 2 KB LDS slot with exactly two
+// 16-byte direct-to-LDS loads per lane. Lanes past the group's end reload the
+// group's first chunk into the unused tail of the slot, so every wave issues
+// the same number of loads and the step waits below can use immediates.
+__device__ __forceinline__ void stage_group(uint8_t* slot, const uint8_t* src, uint32_t bytes) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t n16 = bytes >> 4;
+#pragma unroll
+    for (uint32_t i = 0; i < 2; i++) {
+        const uint32_t c = 64u * i + lane;
+        const uint32_t cc = c < n16 ? c : 0u;
+        __builtin_amdgcn_global_load_lds((glb_void_t*)(src + 16ull * cc),
+                                         (lds_void_t*)(slot + 1024u * i), 16, 0, 0);
+    }
+}
+
+// Wait until at most n of this wave's vector-memory loads are outstanding
+// (n a compile-time constant after unrolling: the switch folds away).
+__device__ __forceinline__ void wait_vm(uint32_t n) {
+    switch (n) {
+    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
+    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
+    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
+    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    }
+}
+
+// Routing of all T tokens from the router logits, recomputed by every
+// workgroup that needs it (a few hundred instructions from 1 KB per token)
+// instead of a serial "last workgroup" pass: waves route one token each, then
+// wave 0 numbers the distinct experts in first-use order. Leaves s_slot_e[u]
+// (expert of slot u), s_wt[u][t] (its gate weight for token t, 0 if unused)
+// and *s_n (number of slots) in LDS.
 template <int T>
+__device__ __forceinline__ void route_prologue(const MoeArgs& a, uint32_t* s_idx, float* s_w,
+                               uint32_t* s_slot_e, float* s_wt, uint32_t* s_n) {
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t nw = blockDim.x >> 6;
+    for (uint32_t i = threadIdx.x; i < kMaxSlots * kMaxTok; i += blockDim.x) s_wt[i] = 0.f;
+    for (uint32_t t = wave; t < T; t += nw)
+        wave_route(a.logits + (size_t)t * a.n_experts, a.n_experts, a.top_k,
+                   s_idx + t * a.top_k, s_w + t * a.top_k);
+    __syncthreads();
+    if (wave == 0) {
+        const uint32_t ne = T * a.top_k;
+        const uint32_t e = lane < ne ? s_idx[lane] : 0xffffffffu;
+        uint32_t first = lane;
+        if (T > 1)
+            for (uint32_t j = 0; j < lane && lane < ne; j++)
+                if (s_idx[j] == e) { first = j; break; }
+        const bool is_first = lane < ne && first == lane;
+        const uint64_t mask = __ballot(is_first);
+        const uint32_t slot = __popcll(mask & ((1ull << first) - 1ull));
+        if (is_first) s_slot_e[slot] = e;
+        if (lane < ne) s_wt[slot * kMaxTok + lane / a.top_k] = s_w[lane];
+        if (lane == 0) *s_n = (uint32_t)__popcll(mask);
+    }
+    __syncthreads();
+}
+
+// Routing of all T tokens, once per layer: route_prologue, then one
+// parallel round of expert lookups into the slot descriptors the expert
+// kernels read, plus the optional idx / w outputs.
+template <int T>
+__global__ __launch_bounds__(kWG) void k_moe_route(MoeArgs a) {
+    __shared__ uint32_t s_idx[kMaxSlots], s_slot_e[kMaxSlots], s_n;
+    __shared__ float s_w[kMaxSlots], s_wt[kMaxSlots * kMaxTok];
+    route_prologue<T>(a, s_idx, s_w, s_slot_e, s_wt, &s_n);
+    const uint32_t tid = threadIdx.x;
+    if (tid < a.max_u) {
+        SlotDesc d;
+        if (tid < s_n) {
+            const uint32_t e = s_slot_e[tid];
+#pragma unroll
+            for (int k = 0; k < 3; k++) {
+                const MatD m = expert_mat(a, e, k);
+                d.p[k] = m.p; d.fmt[k] = m.fmt; d.rb[k] = m.rb;
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 3; k++) { d.p[k] = nullptr; d.fmt[k] = 0; d.rb[k] = 0; }
+        }
+#pragma unroll
+        for (uint32_t t = 0; t < kMaxTok; t++) d.wt[t] = s_wt[tid * kMaxTok + t];
+        a.slots[tid] = d;
+    }
+    if (tid < T * a.top_k) {
+        if (a.idx_out) a.idx_out[tid] = s_idx[tid];
+        if (a.w_out) a.w_out[tid] = s_w[tid];
+    }
+}
+
+// gate/up/silu of one wave: S steps of rps rows starting at local row
+// (w*S)*rps of rows [r0, ...) of the pair (G, Up) -> mid[T][inter].
+// slots: 2*S LDS slots of kSlotBytes. Activations from global memory (L2).
+template <int T, int FF>
+__device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint32_t row0,
+                                             const float* x, uint32_t hidden, float* mid,
+                                             uint32_t inter, uint8_t* slots, const uint32_t* tab) {
+    constexpr int S = kStepsGu;
+    const int f = FF >= 0 ? FF : G.fmt;
+    const uint32_t U = hidden >> 5, rps = 64 / U;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t unit = lane & (U - 1), blk = unit >> 3, q = lane / U;
+    const int j = (int)(unit & 7);
+    const uint32_t bb = fmt_block_bytes(f);
+    const uint32_t gbytes = rps * G.rb;   // one step group (8 blocks)
+    float xr[T][32], sx[T][4];
+    load_x_all<T, FF>(f, x, hidden, hidden, xr, sx);
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const size_t r = row0 + (size_t)s * rps;
+        stage_group(slots + (2 * s) * kSlotBytes, G.p + r * G.rb, gbytes);
+        stage_group(slots + (2 * s + 1) * kSlotBytes, Up.p + r * Up.rb, gbytes);
+    }
+    const uint32_t* lds = (const uint32_t*)slots;
+    const uint32_t boff = q * G.rb + blk * bb;
+    float ag[T][S], au[T][S];
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        wait_vm(4u * (S - 1 - s));
+        float g[T], u[T];
+#pragma unroll
+        for (int t = 0; t < T; t++) { g[t] = 0.f; u[t] = 0.f; }
+        unit_dot<T>(f, lds, (2 * s) * kSlotBytes + boff, j, tab, xr, sx, g);
+        unit_dot<T>(f, lds, (2 * s + 1) * kSlotBytes + boff, j, tab, xr, sx, u);
+#pragma unroll
+        for (int t = 0; t < T; t++) { ag[t][s] = g[t]; au[t][s] = u[t]; }
+    }
+    float gv[T], uv[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        gv[t] = reduce_scatter<S>(ag[t], U);
+        uv[t] = reduce_scatter<S>(au[t], U);
+    }
+    if ((unit & (U / S - 1)) == 0) {
+        const uint32_t s = scatter_step<S>(lane, U);
+        const uint32_t r = row0 + s * rps + q;
+#pragma unroll
+        for (int t = 0; t < T; t++)
+            mid[(size_t)t * inter + r] = gv[t] / (1.0f + expf(-gv[t])) * uv[t];
+    }
+}
+
+// Router GEMV over all experts (one wave per row), plus the shared expert's
+// gate/up/SiLU (independent of routing) and the shared-expert weight.
+template <int T, int FG>
 __global__ __launch_bounds__(kWG) void k_moe_router(MoeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     const uint32_t b = blockIdx.x;
-    if (b >= a.n_router_wg) {   // shared expert gate/up
-        const uint32_t tile = b - a.n_router_wg;
-        gate_up_tile<T>(a.sg, a.su, tile * a.rb_tile, a.rb_tile, a.rb_steps, a.x, a.hidden,
-                        a.mid + (size_t)a.max_u * T * a.inter, a.inter, a.tmask_gu, smem);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (b >= a.n_router_wg) {   // shared expert gate/up, 4 waves x S steps per block
+        const uint32_t toff = tab_bytes(a.tmask_gu);
+        stage_tables(smem, a.tmask_gu);
+        if (a.tmask_gu) stage_wait();
+        const uint32_t U = a.hidden >> 5, rps = 64 / U;
+        const uint32_t row0 = ((b - a.n_router_wg) * 4 + wave) * kStepsGu * rps;
+        if (row0 < a.inter)
+            wave_gate_up<T, FG>(a.sg, a.su, row0, a.x, a.hidden,
+                                a.mid + (size_t)a.max_u * T * a.inter, a.inter,
+                                smem + toff + wave * 2 * kStepsGu * kSlotBytes,
+                                (const uint32_t*)smem);
         return;
     }
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (b == 0 && wave == 0) {   // shared-expert weight: sigmoid(shared_router . x) or 1
+        for (uint32_t t = 0; t < T; t++) {
+            float acc = 0.f;
+            if (a.shared_router)
+                for (uint32_t c = lane; c < a.hidden; c += 64)
+                    acc = fmaf(a.shared_router[c], a.x[(size_t)t * a.hidden + c], acc);
+            acc = group_sum(acc, 64);
+            if (lane == 0) a.sw[t] = a.shared_router ? 1.0f / (1.0f + expf(-acc)) : 1.0f;
+        }
+    }
     const uint32_t e0 = b * a.rr_per_wg, e1 = min(e0 + a.rr_per_wg, a.n_experts);
     if (a.router) {
         for (uint32_t e = e0 + wave; e < e1; e += 4) {
@@ -382,151 +597,106 @@ __global__ __launch_bounds__(kWG) void k_moe_router(MoeArgs a) {
             a.logits[(size_t)t * a.n_experts + e] = a.logits_in[(size_t)t * a.n_experts + e];
         }
     }
-    // Last router workgroup to finish routes every token.
-    __shared__ uint32_t s_last;
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) s_last = atomicAdd(a.counter, 1u) == a.n_router_wg - 1;
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    for (uint32_t t = wave; t < T; t += 4) {
-        wave_route(a.logits + (size_t)t * a.n_experts, a.n_experts, a.top_k,
-                   a.idx + t * a.top_k, a.w + t * a.top_k);
-        if (a.shared_router) {
-            float acc = 0.f;
-            for (uint32_t c = lane; c < a.hidden; c += 64)
-                acc = fmaf(a.shared_router[c], a.x[(size_t)t * a.hidden + c], acc);
-            acc = group_sum(acc, 64);
-            if (lane == 0) a.sw[t] = 1.0f / (1.0f + expf(-acc));
-        } else if (lane == 0) {
-            a.sw[t] = 1.0f;
-        }
-    }
+}
+
+// Routed gate/up/SiLU: workgroup (slot u, tile): 4 waves, each S steps.
+template <int T, int FG>
+__global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t U = a.hidden >> 5, rps = 64 / U;
+    const uint32_t rows_wg = 4 * kStepsGu * rps;
+    const uint32_t ntile = (a.inter + rows_wg - 1) / rows_wg;
+    const uint32_t u = blockIdx.x / ntile, tile = blockIdx.x % ntile;
+    const uint32_t toff = tab_bytes(a.tmask_gu);
+    stage_tables(smem, a.tmask_gu);
+    const SlotDesc& d = a.slots[u];
+    const uint8_t* pg = d.p[0];
+    if (!pg) return;
+    if (a.tmask_gu) stage_wait();
+    const MatD G = {pg, d.fmt[0], a.inter, a.hidden, d.rb[0]};
+    const MatD Up = {d.p[1], d.fmt[1], a.inter, a.hidden, d.rb[1]};
+    const uint32_t row0 = (tile * 4 + wave) * kStepsGu * rps;
+    if (row0 >= a.inter) return;
+    wave_gate_up<T, FG>(G, Up, row0, a.x, a.hidden, a.mid + (size_t)u * T * a.inter, a.inter,
+                        smem + toff + wave * 2 * kStepsGu * kSlotBytes, (const uint32_t*)smem);
+}
+
+// Down projection + combine for rows [r0, r0 + R), R = S * rps: wave w takes
+// slots w, w + nw, ... (routed slots in first-use order, the shared expert
+// last); per-slot row sums meet in LDS and are combined in slot order:
+// out = sum_u wt[u] * y[u] + sw * y[shared] (+ residual).
+constexpr uint32_t down_waves(int T) { return T == 1 ? 16u : 8u; }
+
+template <int T, int FD>
+__global__ __launch_bounds__(64 * down_waves(T)) void k_moe_down(MoeArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ SlotDesc s_d[kMaxSlots];
+    __shared__ uint32_t s_n;
+    constexpr int S = kStepsDn;
+    const uint32_t U = a.inter >> 5, rps = 64 / U;
+    const uint32_t R = S * rps;
+    const uint32_t r0 = blockIdx.x * R;
+    const uint32_t nw = blockDim.x >> 6;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const bool has_sh = a.sd.p != nullptr;
+    const uint32_t toff = tab_bytes(a.tmask_dn);
+    stage_tables(smem, a.tmask_dn);
+    if (threadIdx.x < a.max_u) s_d[threadIdx.x] = a.slots[threadIdx.x];
+    if (a.tmask_dn) wave_wait();
     __syncthreads();
     if (threadIdx.x == 0) {
         uint32_t n = 0;
-        for (uint32_t t = 0; t < T; t++)
-            for (uint32_t k = 0; k < a.top_k; k++) {
-                const uint32_t e = a.idx[t * a.top_k + k];
-                uint32_t u = 0;
-                while (u < n && a.slot_e[u] != e) u++;
-                if (u == n) {
-                    a.slot_e[n] = e;
-                    for (uint32_t tt = 0; tt < T; tt++) a.wt[n * T + tt] = 0.f;
-                    n++;
-                }
-                a.wt[u * T + t] = a.w[t * a.top_k + k];
-                if (a.idx_out) a.idx_out[t * a.top_k + k] = e;
-                if (a.w_out) a.w_out[t * a.top_k + k] = a.w[t * a.top_k + k];
-            }
-        *a.nslots = n;
-        *a.counter = 0u;
+        while (n < a.max_u && s_d[n].p[0]) n++;
+        s_n = n;
     }
-}
-
-template <int T>
-__global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const uint32_t ntile = (a.inter + a.rb_tile - 1) / a.rb_tile;
-    const uint32_t u = blockIdx.x / ntile, tile = blockIdx.x % ntile;
-    if (u >= *a.nslots) return;
-    const ExpertEnt& E = a.experts[a.slot_e[u]];
-    const MatD G = {E.p[0], E.fmt[0], a.inter, a.hidden, E.rb[0]};
-    const MatD Up = {E.p[1], E.fmt[1], a.inter, a.hidden, E.rb[1]};
-    gate_up_tile<T>(G, Up, tile * a.rb_tile, a.rb_tile, a.rb_steps, a.x, a.hidden,
-                    a.mid + (size_t)u * T * a.inter, a.inter, a.tmask_gu, smem);
-}
-
-constexpr uint32_t kMaxSteps = 4;
-
-template <int T>
-__global__ __launch_bounds__(kWG) void k_moe_down(MoeArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const uint32_t r0 = blockIdx.x * a.rc_tile;
-    const uint32_t nv = min(a.rc_tile, a.hidden - r0);
-    const uint32_t nslot = *a.nslots;
-    const bool has_sh = a.sd.p != nullptr;
-    const uint32_t ntot = nslot + (has_sh ? 1u : 0u);
-    const uint32_t toff = tab_bytes(a.tmask_dn);
-    const uint32_t* s = (const uint32_t*)smem;
-    const uint32_t U = a.inter >> 5, rps = 64 / U;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t unit = lane & (U - 1), blk = unit >> 3;
+    __syncthreads();
+    const uint32_t nslot = s_n, ntot = nslot + (has_sh ? 1u : 0u);
+    float* ybuf = (float*)(smem + toff + nw * S * kSlotBytes);   // [ntot][R][T]
+    uint8_t* slots = smem + toff + wave * S * kSlotBytes;
+    const uint32_t unit = lane & (U - 1), blk = unit >> 3, q = lane / U;
     const int j = (int)(unit & 7);
-    float acc_out[kMaxSteps][T], shv[kMaxSteps][T];
+    for (uint32_t u = wave; u < ntot; u += nw) {
+        const MatD D = u < nslot ? MatD{s_d[u].p[2], s_d[u].fmt[2], a.hidden, a.inter, s_d[u].rb[2]}
+                                 : a.sd;
+        const int f = FD >= 0 ? FD : D.fmt;
+        const float* xm = a.mid + (size_t)(u < nslot ? u : a.max_u) * T * a.inter;
+        float xr[T][32], sx[T][4];
+        load_x_all<T, FD>(f, xm, a.inter, a.inter, xr, sx);
 #pragma unroll
-    for (uint32_t q = 0; q < kMaxSteps; q++)
+        for (int s = 0; s < S; s++)
+            stage_group(slots + s * kSlotBytes, D.p + (size_t)(r0 + s * rps) * D.rb, rps * D.rb);
+        const uint32_t bb = fmt_block_bytes(f);
+        const uint32_t boff = q * D.rb + blk * bb;
+        float acc[T][S];
 #pragma unroll
-        for (int t = 0; t < T; t++) { acc_out[q][t] = 0.f; shv[q][t] = 0.f; }
-    // slot u < nslot: routed expert a.slot_e[u]; slot nslot: the shared expert
-    auto slot_mat = [&](uint32_t u) -> MatD {
-        if (u < nslot) {
-            const ExpertEnt& E = a.experts[a.slot_e[u]];
-            return MatD{E.p[2], E.fmt[2], a.hidden, a.inter, E.rb[2]};
+        for (int s = 0; s < S; s++) {
+            wait_vm(2u * (S - 1 - s));
+            float v[T];
+#pragma unroll
+            for (int t = 0; t < T; t++) v[t] = 0.f;
+            unit_dot<T>(f, (const uint32_t*)smem, (uint32_t)(slots - smem) + s * kSlotBytes + boff,
+                        j, (const uint32_t*)smem, xr, sx, v);
+#pragma unroll
+            for (int t = 0; t < T; t++) acc[t][s] = v[t];
         }
-        return a.sd;
-    };
-    stage_tables(smem, a.tmask_dn);
-    // Slots in batches that fit the LDS budget, all rows of a batch in flight.
-    uint32_t u0 = 0;
-    while (u0 < ntot) {
-        uint32_t off = toff, u1 = u0;
-        while (u1 < ntot) {
-            const MatD D = slot_mat(u1);
-            const uint32_t bytes = (nv * D.rb + 15u) & ~15u;
-            if (u1 > u0 && off + bytes + 16 > kLdsBudget) break;
-            stage(smem + off, D.p + (size_t)r0 * D.rb, nv * D.rb);
-            off += bytes;
-            u1++;
+        float r[T];
+#pragma unroll
+        for (int t = 0; t < T; t++) r[t] = reduce_scatter<S>(acc[t], U);
+        if ((unit & (U / S - 1)) == 0) {
+            const uint32_t rl = scatter_step<S>(lane, U) * rps + q;
+#pragma unroll
+            for (int t = 0; t < T; t++) ybuf[(u * R + rl) * T + t] = r[t];
         }
-        stage_wait();
-        off = toff;
-        for (uint32_t u = u0; u < u1; u++) {
-            const MatD D = slot_mat(u);
-            const bool shared = u >= nslot;
-            const float* xm = a.mid + (size_t)(shared ? a.max_u : u) * T * a.inter;
-            float wts[T];
-#pragma unroll
-            for (int t = 0; t < T; t++) wts[t] = shared ? 0.f : a.wt[u * T + t];
-            const uint32_t bb = fmt_block_bytes(D.fmt);
-            float xr[T][32], sx[T][4];
-#pragma unroll
-            for (int t = 0; t < T; t++)
-                load_unit_x(D.fmt, xm + (size_t)t * a.inter, blk, j, xr[t], sx[t]);
-#pragma unroll
-            for (uint32_t q = 0; q < kMaxSteps; q++) {
-                if (q >= a.rc_steps) break;
-                const uint32_t rl = (wave * a.rc_steps + q) * rps + lane / U;
-                float acc[T];
-#pragma unroll
-                for (int t = 0; t < T; t++) acc[t] = 0.f;
-                if (rl < nv) unit_dot<T>(D.fmt, s, off + rl * D.rb + blk * bb, j, s, xr, sx, acc);
-#pragma unroll
-                for (int t = 0; t < T; t++) {
-                    const float v = group_sum(acc[t], U);
-                    if (shared) shv[q][t] = v;
-                    else acc_out[q][t] = fmaf(wts[t], v, acc_out[q][t]);
-                }
-            }
-            off += (nv * D.rb + 15u) & ~15u;
-        }
-        __syncthreads();
-        u0 = u1;
     }
-    if (unit != 0) return;
-#pragma unroll
-    for (uint32_t q = 0; q < kMaxSteps; q++) {
-        if (q >= a.rc_steps) break;
-        const uint32_t rl = (wave * a.rc_steps + q) * rps + lane / U;
-        if (rl >= nv) continue;
-#pragma unroll
-        for (int t = 0; t < T; t++) {
-            float v = acc_out[q][t];
-            if (has_sh) v = fmaf(a.sw[t], shv[q][t], v);
-            if (a.residual) v += a.residual[(size_t)t * a.hidden + r0 + rl];
-            a.out[(size_t)t * a.hidden + r0 + rl] = v;
-        }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < R * T; i += blockDim.x) {
+        const uint32_t rl = i / T, t = i % T;
+        float v = 0.f;
+        for (uint32_t u = 0; u < nslot; u++) v = fmaf(s_d[u].wt[t], ybuf[(u * R + rl) * T + t], v);
+        if (has_sh) v = fmaf(a.sw[t], ybuf[(nslot * R + rl) * T + t], v);
+        if (a.residual) v += a.residual[(size_t)t * a.hidden + r0 + rl];
+        a.out[(size_t)t * a.hidden + r0 + rl] = v;
     }
 }
 
@@ -611,14 +781,9 @@ struct qw6_hip_ctx_s {
     std::vector<void*> owned;
     // decode workspace
     float* logits;
-    uint32_t* idx;
-    float* w;
-    uint32_t* nslots;
-    uint32_t* slot_e;
-    float* wt;
     float* sw;
+    SlotDesc* slots;
     float* mid;
-    uint32_t* counter;
     uint32_t ws_experts, ws_inter, ws_topk;
     // per-kernel timing (qw6_hip_profile)
     std::vector<hipEvent_t> prof_ev;
@@ -632,6 +797,10 @@ struct qw6_hip_experts_s {
     uint32_t hidden, inter;
     uint32_t tmask_gu, tmask_dn;
     uint32_t rb_gu_max;   // widest gate/up row in bytes
+    uint32_t rb_dn_max;   // widest down row in bytes
+    int fmt_gu, fmt_dn;   // the single gate/up (down) format, -1 if mixed
+    int gu_same;          // every expert's gate and up share a format
+    PackRef pk[3];        // regular-pack addressing per matrix kind
 };
 
 namespace {
@@ -664,6 +833,36 @@ uint32_t min_rows_align(uint32_t rb) {   // rows r such that r * rb % 16 == 0
     return r;
 }
 
+template <int V> using IC = std::integral_constant<int, V>;
+
+// Run fn(IC<T>, IC<F>) for the kernel instantiation of T tokens and format
+// f: format-specialised kernels for 1-2 tokens, the format switch otherwise
+// (or when f < 0: mixed formats).
+template <typename Fn>
+void launch_by_fmt(int f, uint32_t T, Fn fn) {
+    if (T <= 2 && f >= 0) {
+        auto by_f = [&](auto tc) {
+            switch (f) {
+            case F_Q4K: fn(tc, IC<F_Q4K>{}); break;
+            case F_Q5K: fn(tc, IC<F_Q5K>{}); break;
+            case F_Q6K: fn(tc, IC<F_Q6K>{}); break;
+            case F_IQ2XXS: fn(tc, IC<F_IQ2XXS>{}); break;
+            case F_IQ2S: fn(tc, IC<F_IQ2S>{}); break;
+            default: fn(tc, IC<F_IQ3S>{}); break;
+            }
+        };
+        if (T == 1) by_f(IC<1>{});
+        else by_f(IC<2>{});
+        return;
+    }
+    switch (T) {
+    case 1: fn(IC<1>{}, IC<-1>{}); break;
+    case 2: fn(IC<2>{}, IC<-1>{}); break;
+    case 3: fn(IC<3>{}, IC<-1>{}); break;
+    default: fn(IC<4>{}, IC<-1>{}); break;
+    }
+}
+
 // Launch y = W x for n_tok tokens on device data (W.fmt < 0: F32).
 int launch_matvec(const MatD& W, const float* x, float* y, uint32_t n_tok, hipStream_t st) {
     for (uint32_t t0 = 0; t0 < n_tok; t0 += kMaxTok) {
@@ -685,18 +884,14 @@ int launch_matvec(const MatD& W, const float* x, float* y, uint32_t n_tok, hipSt
                                 : tmask & 1u ? kTabOffIq2s : 0u;
             if (fast_k(W.cols)) {
                 const uint32_t U = W.cols / 32, rps = 64 / U;
-                uint32_t steps = 1;
-                while (steps < kMaxSteps && 4 * rps * steps * 2 * W.rb <= 32768) steps <<= 1;
-                uint32_t R = 4 * rps * steps;
-                while (R % min_rows_align(W.rb)) { steps <<= 1; R = 4 * rps * steps; }
-                const size_t lds = toff + R * W.rb + 32;
+                const uint32_t R = 4 * rps * kStepsMv;   // multiple of 16 bytes: 32*steps*bb
+                const size_t lds = toff + align16(R * W.rb) + 16 + T * W.cols * 4 + 16;
+                if (lds > kLdsBudget) return fail("matvec tile exceeds LDS budget");
                 const dim3 grid((W.rows + R - 1) / R);
-                switch (T) {
-                case 1: k_matvec<1><<<grid, kWG, lds, st>>>(W, xt, yt, R, steps, tmask); break;
-                case 2: k_matvec<2><<<grid, kWG, lds, st>>>(W, xt, yt, R, steps, tmask); break;
-                case 3: k_matvec<3><<<grid, kWG, lds, st>>>(W, xt, yt, R, steps, tmask); break;
-                default: k_matvec<4><<<grid, kWG, lds, st>>>(W, xt, yt, R, steps, tmask); break;
-                }
+                launch_by_fmt(W.fmt, T, [&](auto tc, auto fc) {
+                    k_matvec<decltype(tc)::value, decltype(fc)::value>
+                        <<<grid, kWG, lds, st>>>(W, xt, yt, R, tmask);
+                });
             } else {
                 const size_t lds = toff + W.rb + 32;
                 if (lds > kLdsBudget) return fail("row too large for the generic kernel (%u B)", W.rb);
@@ -929,7 +1124,7 @@ int qw6_hip_experts_create(qw6_hip_ctx_t* c, const qw6_hip_matrix_t* gate,
     if (n_experts == 0 || n_experts > 256) return fail("n_experts %u not in 1..256", n_experts);
     const uint32_t hidden = gate[0].cols, inter = gate[0].rows;
     std::vector<ExpertEnt> tab(n_experts);
-    uint32_t mgu = 0, mdn = 0, rb_gu = 0;
+    uint32_t mgu = 0, mdn = 0, rb_gu = 0, rb_dn = 0;
     for (uint32_t e = 0; e < n_experts; e++) {
         const qw6_hip_matrix_t* m[3] = {&gate[e], &up[e], &down[e]};
         for (int k = 0; k < 3; k++) {
@@ -947,11 +1142,33 @@ int qw6_hip_experts_create(qw6_hip_ctx_t* c, const qw6_hip_matrix_t* gate,
             tab[e].rb[k] = (m[k]->cols / 256) * fmt_block_bytes(f);
             (k < 2 ? mgu : mdn) |= fmt_table_mask(f);
             if (k < 2 && tab[e].rb[k] > rb_gu) rb_gu = tab[e].rb[k];
+            if (k == 2 && tab[e].rb[k] > rb_dn) rb_dn = tab[e].rb[k];
         }
     }
     DevGuard g(c->device);
     qw6_hip_experts_t* E = new qw6_hip_experts_t();
     E->rb_gu_max = rb_gu;
+    for (int k = 0; k < 3; k++) {   // expert e at base + e * stride, one format?
+        PackRef& P = E->pk[k];
+        P.base = tab[0].p[k];
+        P.fmt = tab[0].fmt[k];
+        P.rb = tab[0].rb[k];
+        P.stride = n_experts > 1 ? (uint64_t)(tab[1].p[k] - tab[0].p[k]) : 0;
+        P.regular = 1;
+        for (uint32_t e = 0; e < n_experts && P.regular; e++)
+            if (tab[e].fmt[k] != P.fmt ||
+                tab[e].p[k] != tab[0].p[k] + P.stride * e || (P.stride & 15u))
+                P.regular = 0;
+    }
+    E->fmt_gu = tab[0].fmt[0];
+    E->fmt_dn = tab[0].fmt[2];
+    E->gu_same = 1;
+    for (uint32_t e = 0; e < n_experts; e++) {
+        if (tab[e].fmt[0] != E->fmt_gu || tab[e].fmt[1] != E->fmt_gu) E->fmt_gu = -1;
+        if (tab[e].fmt[2] != E->fmt_dn) E->fmt_dn = -1;
+        if (tab[e].fmt[0] != tab[e].fmt[1]) E->gu_same = 0;
+    }
+    E->rb_dn_max = rb_dn;
     E->ctx = c;
     E->n = n_experts;
     E->hidden = hidden;
@@ -983,48 +1200,51 @@ namespace {
 int ensure_ws(qw6_hip_ctx_t* c, uint32_t n_experts, uint32_t inter, uint32_t top_k) {
     if (c->logits && c->ws_experts >= n_experts && c->ws_inter >= inter && c->ws_topk >= top_k)
         return 0;
-    const uint32_t T = kMaxTok, max_u = T * 8;
+    const uint32_t T = kMaxTok;
     n_experts = n_experts > 256 ? n_experts : 256;
     inter = inter > c->ws_inter ? inter : c->ws_inter;
     void* p;
     if (alloc_owned(c, (size_t)T * n_experts * 4, &p)) return -1;
     c->logits = (float*)p;
-    if (alloc_owned(c, (size_t)T * 8 * 4, &p)) return -1;
-    c->idx = (uint32_t*)p;
-    if (alloc_owned(c, (size_t)T * 8 * 4, &p)) return -1;
-    c->w = (float*)p;
-    if (alloc_owned(c, 16, &p)) return -1;
-    c->nslots = (uint32_t*)p;
-    if (alloc_owned(c, max_u * 4, &p)) return -1;
-    c->slot_e = (uint32_t*)p;
-    if (alloc_owned(c, (size_t)max_u * T * 4, &p)) return -1;
-    c->wt = (float*)p;
     if (alloc_owned(c, T * 4, &p)) return -1;
     c->sw = (float*)p;
-    if (alloc_owned(c, (size_t)(max_u + 1) * T * inter * 4, &p)) return -1;
+    if (alloc_owned(c, sizeof(SlotDesc) * kMaxSlots, &p)) return -1;
+    c->slots = (SlotDesc*)p;
+    if (alloc_owned(c, (size_t)(kMaxSlots + 1) * T * inter * 4, &p)) return -1;
     c->mid = (float*)p;
-    if (alloc_owned(c, 256, &p)) return -1;
-    c->counter = (uint32_t*)p;
     c->ws_experts = n_experts;
     c->ws_inter = inter;
     c->ws_topk = 8;
     return 0;
 }
 
-template <int T>
-int launch_moe_T(const MoeArgs& a, size_t lds_r, uint32_t grid_r, size_t lds_b,
-                        uint32_t grid_b, size_t lds_c, uint32_t grid_c, hipStream_t st,
-                        hipEvent_t* ev) {
+int launch_moe(const MoeArgs& a, int fs, int fg, int fd, size_t lds_r, uint32_t grid_r,
+               size_t lds_b, uint32_t grid_b, size_t lds_c, uint32_t grid_c, uint32_t nw_c,
+               hipStream_t st, hipEvent_t* ev) {
     if (ev) CK(hipEventRecord(ev[0], st));
-    k_moe_router<T><<<grid_r, kWG, lds_r, st>>>(a);
+    launch_by_fmt(fs, a.T, [&](auto tc, auto fc) {
+        k_moe_router<decltype(tc)::value, decltype(fc)::value><<<grid_r, kWG, lds_r, st>>>(a);
+    });
     CK(hipGetLastError());
     if (ev) CK(hipEventRecord(ev[1], st));
-    k_moe_gate_up<T><<<grid_b, kWG, lds_b, st>>>(a);
+    switch (a.T) {
+    case 1: k_moe_route<1><<<1, kWG, 0, st>>>(a); break;
+    case 2: k_moe_route<2><<<1, kWG, 0, st>>>(a); break;
+    case 3: k_moe_route<3><<<1, kWG, 0, st>>>(a); break;
+    default: k_moe_route<4><<<1, kWG, 0, st>>>(a); break;
+    }
     CK(hipGetLastError());
     if (ev) CK(hipEventRecord(ev[2], st));
-    k_moe_down<T><<<grid_c, kWG, lds_c, st>>>(a);
+    launch_by_fmt(fg, a.T, [&](auto tc, auto fc) {
+        k_moe_gate_up<decltype(tc)::value, decltype(fc)::value><<<grid_b, kWG, lds_b, st>>>(a);
+    });
     CK(hipGetLastError());
     if (ev) CK(hipEventRecord(ev[3], st));
+    launch_by_fmt(fd, a.T, [&](auto tc, auto fc) {
+        k_moe_down<decltype(tc)::value, decltype(fc)::value><<<grid_c, 64 * nw_c, lds_c, st>>>(a);
+    });
+    CK(hipGetLastError());
+    if (ev) CK(hipEventRecord(ev[4], st));
     return 0;
 }
 
@@ -1075,38 +1295,26 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
     a.inter = L->inter;
     a.n_experts = E->n;
     a.top_k = L->top_k;
-    a.router = L->router;
     a.shared_router = L->shared_router;
     a.experts = E->dev;
+    for (int k = 0; k < 3; k++) a.pk[k] = E->pk[k];
     a.sg = sg; a.su = su; a.sd = sd;
-    a.logits = c->logits; a.idx = c->idx; a.w = c->w; a.nslots = c->nslots;
-    a.slot_e = c->slot_e; a.wt = c->wt; a.sw = c->sw; a.mid = c->mid; a.counter = c->counter;
+    a.logits = c->logits; a.sw = c->sw; a.mid = c->mid; a.slots = c->slots;
     a.tmask_gu = mgu;
     a.tmask_dn = mdn;
-    // gate/up tiles: 4 waves x steps x (64/U) rows
-    const uint32_t Ug = L->hidden / 32, rpsg = 64 / Ug;
-    a.rb_steps = rpsg >= 4 ? 1 : 4 / rpsg;
-    a.rb_tile = 4 * rpsg * a.rb_steps;
-    const uint32_t Ud = L->inter / 32, rpsd = 64 / Ud;
-    a.rc_steps = rpsd >= 4 ? 1 : 4 / rpsd;
-    a.rc_tile = 4 * rpsd * a.rc_steps;
-    a.rr_per_wg = L->router ? 4 : E->n;
-    a.n_router_wg = (E->n + a.rr_per_wg - 1) / a.rr_per_wg;
-    uint32_t rb_max = E->rb_gu_max;
-    if (has_sh) rb_max = sg.rb > rb_max ? sg.rb : rb_max, rb_max = su.rb > rb_max ? su.rb : rb_max;
-    auto gu_lds = [&]() {
-        return (size_t)tab_bytes(mgu) + 2 * ((size_t)a.rb_tile * rb_max + 16) +
-               a.rb_tile * kMaxTok * 4 + 64;
-    };
-    while (gu_lds() > kLdsBudget && a.rb_steps > 1) {
-        a.rb_steps >>= 1;
-        a.rb_tile = 4 * rpsg * a.rb_steps;
-    }
-    const size_t lds_gu = gu_lds();
-    const uint32_t nsh_tiles = has_sh ? (L->inter + a.rb_tile - 1) / a.rb_tile : 0;
-    const uint32_t ntile_b = (L->inter + a.rb_tile - 1) / a.rb_tile;
-    const uint32_t grid_c = (L->hidden + a.rc_tile - 1) / a.rc_tile;
-    if (lds_gu > kLdsBudget) return fail("gate/up tile exceeds LDS budget");
+    // kernels specialised on one weight format where a matrix kind has one
+    if (!E->gu_same || (has_sh && sg.fmt != su.fmt))
+        return fail("gate and up of each expert must share a quant type");
+    const int fg = E->fmt_gu, fs = has_sh ? sg.fmt : fg;
+    int fd = E->fmt_dn;
+    if (has_sh && sd.fmt != fd) fd = -1;
+    const uint32_t rpsg = 64 / (L->hidden / 32), rpsd = 64 / (L->inter / 32);
+    const uint32_t rows_wg = 4 * kStepsGu * rpsg;          // gate/up rows per workgroup
+    const uint32_t ntile_b = (L->inter + rows_wg - 1) / rows_wg;
+    const uint32_t nsh_wg = has_sh ? ntile_b : 0;
+    const size_t lds_gu = (size_t)tab_bytes(mgu) + 4 * 2 * kStepsGu * kSlotBytes;
+    const uint32_t R_c = kStepsDn * rpsd;
+    const uint32_t grid_c = (L->hidden + R_c - 1) / R_c;
 
     for (uint32_t t0 = 0; t0 < n_tok; t0 += kMaxTok) {
         const uint32_t T = n_tok - t0 < kMaxTok ? n_tok - t0 : kMaxTok;
@@ -1121,17 +1329,18 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
         a.out = out + (size_t)t0 * L->hidden;
         a.idx_out = idx ? idx + (size_t)t0 * L->top_k : nullptr;
         a.w_out = w ? w + (size_t)t0 * L->top_k : nullptr;
-        const uint32_t grid_r = a.n_router_wg + nsh_tiles;
+        const uint32_t grid_r = a.n_router_wg + nsh_wg;
         const uint32_t grid_b = a.max_u * ntile_b;
+        const uint32_t ntot = a.max_u + (has_sh ? 1u : 0u);
+        const uint32_t nw_max = T == 1 ? down_waves(1) : down_waves(2);
+        const uint32_t nw_c = ntot < nw_max ? ntot : nw_max;
+        const size_t lds_c = (size_t)tab_bytes(mdn) + (size_t)nw_c * kStepsDn * kSlotBytes +
+                             (size_t)ntot * R_c * T * 4 + 16;
+        if (lds_c > kLdsBudget) return fail("down tile exceeds the LDS budget");
         hipEvent_t* ev = nullptr;
-        if (c->prof_calls < c->prof_cap) ev = &c->prof_ev[4 * c->prof_calls++];
-        int rc;
-        switch (T) {
-        case 1: rc = launch_moe_T<1>(a, lds_gu, grid_r, lds_gu, grid_b, kLdsBudget, grid_c, st, ev); break;
-        case 2: rc = launch_moe_T<2>(a, lds_gu, grid_r, lds_gu, grid_b, kLdsBudget, grid_c, st, ev); break;
-        case 3: rc = launch_moe_T<3>(a, lds_gu, grid_r, lds_gu, grid_b, kLdsBudget, grid_c, st, ev); break;
-        default: rc = launch_moe_T<4>(a, lds_gu, grid_r, lds_gu, grid_b, kLdsBudget, grid_c, st, ev); break;
-        }
+        if (c->prof_calls < c->prof_cap) ev = &c->prof_ev[kProfEv * c->prof_calls++];
+        const int rc = launch_moe(a, fs, fg, fd, lds_gu, grid_r, lds_gu, grid_b, lds_c,
+                                  grid_c, nw_c, st, ev);
         if (rc) return rc;
     }
     return 0;
@@ -1144,21 +1353,21 @@ int qw6_hip_profile(qw6_hip_ctx_t* c, uint32_t max_calls) {
     c->prof_ev.clear();
     c->prof_cap = c->prof_calls = 0;
     if (max_calls == 0) return 0;
-    c->prof_ev.resize(4 * (size_t)max_calls);
+    c->prof_ev.resize(kProfEv * (size_t)max_calls);
     for (auto& e : c->prof_ev) CK(hipEventCreate(&e));
     c->prof_cap = max_calls;
     return 0;
 }
 
-int qw6_hip_profile_read(qw6_hip_ctx_t* c, float ms[3], uint32_t* calls) {
+int qw6_hip_profile_read(qw6_hip_ctx_t* c, float ms[4], uint32_t* calls) {
     if (!c || !ms || !calls) return fail("null pointer");
     DevGuard g(c->device);
-    ms[0] = ms[1] = ms[2] = 0.f;
+    for (int k = 0; k < kProfEv - 1; k++) ms[k] = 0.f;
     for (uint32_t i = 0; i < c->prof_calls; i++) {
-        CK(hipEventSynchronize(c->prof_ev[4 * i + 3]));
-        for (int k = 0; k < 3; k++) {
+        CK(hipEventSynchronize(c->prof_ev[kProfEv * i + kProfEv - 1]));
+        for (int k = 0; k < kProfEv - 1; k++) {
             float t = 0.f;
-            CK(hipEventElapsedTime(&t, c->prof_ev[4 * i + k], c->prof_ev[4 * i + k + 1]));
+            CK(hipEventElapsedTime(&t, c->prof_ev[kProfEv * i + k], c->prof_ev[kProfEv * i + k + 1]));
             ms[k] += t;
         }
     }

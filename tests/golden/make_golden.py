@@ -33,25 +33,6 @@ def mv_case(q, rows, cols, seed):
     return w, x
 
 
-def route_cases():
-    rng_seed = 31
-    out = {}
-    z = S.f32_normal(rng_seed, S.stream_id(0, 20), 256, 1.0)
-    out["route_randn"] = (z, 8)
-    out["route_ties"] = (np.round(z * 2) / 2, 8)                   # many exact ties
-    out["route_small"] = (np.array([0.0, 2.0, 1.0, -1.0], np.float32), 2)  # qw6.c:3400-3412
-    i = np.arange(256, dtype=np.float32)
-    kat = (np.sin(i * np.float32(0.17)) + np.cos(i * np.float32(0.031))).astype(np.float32)
-    kat[7], kat[149] = 5.0, 4.5                                    # qw6_vk.c:1898-1920
-    out["route_vkkat"] = (kat, 8)
-    neg = z.copy()
-    neg[::3] = -np.inf
-    out["route_neginf"] = (neg, 8)
-    out["route_n7k3"] = (z[:7].copy(), 3)
-    out["route_allequal"] = (np.full(16, 0.5, np.float32), 8)
-    return out
-
-
 def main():
     R = O.ref()
     if R is None:
@@ -72,7 +53,7 @@ def main():
     x = S.f32_normal(1, S.stream_id(0, S.K_X), 2048, 1.0)
     g["cfg0_y"] = O.ref_matvec(S.Q_Q4_K_M, w, 512, 2048, x)
     # routing
-    for name, (lg, k) in route_cases().items():
+    for name, (lg, k) in cases.route_cases().items():
         idx, wt = O.ref_moe_route(lg, k)
         g[name + "_idx"], g[name + "_w"] = idx, wt
     # rmsnorm

@@ -229,8 +229,7 @@ def test_kat_matvec_f32():
 @pytest.mark.parametrize("name", ["route_randn", "route_ties", "route_small", "route_vkkat",
                                   "route_neginf", "route_n7k3", "route_allequal"])
 def test_route_golden(name):
-    import golden.make_golden as MG
-    lg, k = MG.route_cases()[name]
+    lg, k = cases.route_cases()[name]
     idx, w = O.moe_route(lg, k)
     assert np.array_equal(idx, G[name + "_idx"])
     assert np.array_equal(bits(w), bits(G[name + "_w"]))
