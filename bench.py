@@ -110,18 +110,22 @@ def main():
         step(k)
     torch.cuda.synchronize()
 
-    # bytes per step: router + 8 selected experts + shared + x/out/logits
+    # algorithmic bytes per step and per kernel: the router, the 8 selected
+    # experts' gate/up/down, the shared expert, activations in and out
     sel = idx.cpu().numpy()
-    step_bytes = []
-    gu_bytes = []
+    L0 = pool[0]
+    sh_gu = sum(S.row_bytes(m[1], m[3]) * m[2] for m in L0.shared[:2])
+    sh_dn = S.row_bytes(L0.shared[2][1], L0.shared[2][3]) * L0.shared[2][2]
+    r_b = N_EXPERTS * HIDDEN * 4 + HIDDEN * 4 + N_EXPERTS * 4
+    gu_bytes, dn_bytes = [], []
     for j in range(P):
         L = pool[j]
-        eb = sum(L.expert_bytes(int(e)) for e in sel[j])
         gub = sum(2 * S.row_bytes(L.quants[int(e)][0], HIDDEN) * INTER for e in sel[j])
-        step_bytes.append(N_EXPERTS * HIDDEN * 4 + eb + L.shared_bytes() + 2 * HIDDEN * 4
-                          + N_EXPERTS * 4)
-        gu_bytes.append(gub + HIDDEN * 4 + TOP_K * INTER * 4)
-    bytes_per_step = float(np.mean(step_bytes))
+        dnb = sum(S.row_bytes(L.quants[int(e)][2], INTER) * HIDDEN for e in sel[j])
+        gu_bytes.append(gub + sh_gu + HIDDEN * 4 + N_EXPERTS * 4 + (TOP_K + 1) * INTER * 4)
+        dn_bytes.append(dnb + sh_dn + (TOP_K + 1) * INTER * 4 + HIDDEN * 4)
+    gu_b, d_b = float(np.mean(gu_bytes)), float(np.mean(dn_bytes))
+    bytes_per_step = r_b + gu_b + d_b - N_EXPERTS * 4 - (TOP_K + 1) * INTER * 4
 
     K = args.steps
     # eager timing
@@ -154,7 +158,8 @@ def main():
     us_layer = 1e6 * graph_s / steps_graph
     eager_us = 1e6 * eager_s / K
 
-    # per-kernel durations with HIP events on the launch stream
+    # per-kernel durations: each kernel's own dispatch timestamps (HIP events
+    # recorded by hipExtLaunchKernel on the launch stream)
     nprof = min(K, 256)
     ctx.profile(nprof)
     for k in range(nprof):
@@ -162,20 +167,14 @@ def main():
     ms, calls = ctx.profile_read()
     ctx.profile(0)
     kus = [1e3 * m / calls for m in ms]
-    gu_b = float(np.mean(gu_bytes))
-    achieved = gu_b / (kus[2] * 1e-6) / 1e9
-    sh_gu = sum(S.row_bytes(m[1], m[3]) * m[2] for m in pool[0].shared[:2])
-    r_b = N_EXPERTS * HIDDEN * 4 + sh_gu + HIDDEN * 4 + N_EXPERTS * 4
-    rt_b = N_EXPERTS * 4
-    d_b = bytes_per_step - r_b - gu_b
+    achieved = gu_b / (kus[1] * 1e-6) / 1e9
     kernels = {
         "moe_router": {"us": round(kus[0], 2), "bytes": int(r_b),
                        "GBps": round(r_b / kus[0] / 1e3, 1)},
-        "moe_route": {"us": round(kus[1], 2), "bytes": int(rt_b)},
-        "moe_gate_up": {"us": round(kus[2], 2), "bytes": int(gu_b),
+        "moe_gate_up": {"us": round(kus[1], 2), "bytes": int(gu_b),
                         "GBps": round(achieved, 1)},
-        "moe_down": {"us": round(kus[3], 2), "bytes": int(d_b),
-                     "GBps": round(d_b / kus[3] / 1e3, 1)},
+        "moe_down": {"us": round(kus[2], 2), "bytes": int(d_b),
+                     "GBps": round(d_b / kus[2] / 1e3, 1)},
     }
     log("graph %.2f us/layer, eager %.2f us/layer, kernels %s" % (us_layer, eager_us, kernels))
 

@@ -129,6 +129,12 @@ typedef struct {
     qw6_hip_matrix_t shared_gate; /* shared expert; data == NULL: none */
     qw6_hip_matrix_t shared_up;
     qw6_hip_matrix_t shared_down;
+    const float *norm_w;          /* F32 [hidden]: the layer input is first
+                                     RMSNorm'd with this weight (the MoE
+                                     block's post-attention norm,
+                                     qw6_vk.c:3351-3354; qw6.c:2476-2478), or
+                                     NULL: the input is used as given */
+    float norm_eps;               /* RMSNorm epsilon (qw6.h QW6_RMS_EPS) */
 } qw6_hip_moe_layer_t;
 
 /* out[t] = MoE(x[t]) for n_tok tokens (device pointers, row-major [n_tok x
@@ -147,13 +153,15 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t *ctx, const qw6_hip_moe_layer_t *layer,
  * 1 = always the fp32 decode kernels, 2 = always the grouped MFMA kernels. */
 int qw6_hip_set_mode(qw6_hip_ctx_t *ctx, int mode);
 
-/* Per-kernel timing of qw6_hip_moe_forward with HIP events on its launch
- * stream (eager calls only, not under graph capture). max_calls > 0 starts
- * recording for up to that many calls (events between the four decode
- * kernels), 0 stops. qw6_hip_profile_read synchronizes and returns the summed
- * elapsed ms of [router, route, gate_up, down] over the recorded calls. */
+/* Per-kernel timing of qw6_hip_moe_forward on its launch stream (eager calls
+ * only, not under graph capture). max_calls > 0 starts recording for up to
+ * that many calls, 0 stops. Each of the three decode kernels (router,
+ * gate/up, down) is launched with start/stop events that the dispatch itself
+ * timestamps (hipExtLaunchKernel), so the durations carry no extra queue
+ * packets. qw6_hip_profile_read synchronizes and returns the summed elapsed
+ * ms of [router, gate_up, down] over the recorded calls. */
 int qw6_hip_profile(qw6_hip_ctx_t *ctx, uint32_t max_calls);
-int qw6_hip_profile_read(qw6_hip_ctx_t *ctx, float ms[4], uint32_t *calls);
+int qw6_hip_profile_read(qw6_hip_ctx_t *ctx, float ms[3], uint32_t *calls);
 
 /* y = rmsnorm(x) * w per token (qw6_cpu_rmsnorm, qw6.c:2503-2513). */
 int qw6_hip_rmsnorm(qw6_hip_ctx_t *ctx, const float *x, const float *w,

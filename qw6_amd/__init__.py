@@ -39,7 +39,8 @@ class MoeLayer(C.Structure):
     _fields_ = [("hidden", C.c_uint32), ("inter", C.c_uint32), ("top_k", C.c_uint32),
                 ("router", C.c_void_p), ("shared_router", C.c_void_p),
                 ("experts", C.c_void_p), ("shared_gate", Matrix),
-                ("shared_up", Matrix), ("shared_down", Matrix)]
+                ("shared_up", Matrix), ("shared_down", Matrix),
+                ("norm_w", C.c_void_p), ("norm_eps", C.c_float)]
 
 
 _lib = None
@@ -244,7 +245,8 @@ class Context:
         _check(lib().qw6_hip_profile(self.handle, max_calls))
 
     def profile_read(self):
-        ms = (C.c_float * 4)()
+        """Summed ms of [router, gate_up, down] over the recorded calls."""
+        ms = (C.c_float * 3)()
         n = C.c_uint32()
         _check(lib().qw6_hip_profile_read(self.handle, ms, C.byref(n)))
         return list(ms), n.value
@@ -255,11 +257,13 @@ class Context:
 
 
 def make_layer(hidden: int, inter: int, top_k: int, experts: Experts, router=None,
-               shared=None, shared_router=None) -> MoeLayer:
+               shared=None, shared_router=None, norm_w=None, norm_eps: float = 1e-6) -> MoeLayer:
     L = MoeLayer()
     L.hidden, L.inter, L.top_k = hidden, inter, top_k
     L.router = _addr(router)
     L.shared_router = _addr(shared_router)
+    L.norm_w = _addr(norm_w)
+    L.norm_eps = norm_eps
     L.experts = experts.handle
     if shared is not None:
         L.shared_gate = Matrix(*shared[0])

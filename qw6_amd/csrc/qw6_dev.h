@@ -186,11 +186,13 @@ __device__ __forceinline__ void load_unit_x(int f, const float* __restrict__ x, 
             for (int i = 0; i < 8; i++) s += xr[8 * k + i];
             sx[k] = s;
         }
-    } else {
+    } else if (f == F_Q4K || f == F_Q5K) {
         float s0 = 0.f, s1 = 0.f;
 #pragma unroll
         for (int i = 0; i < 16; i++) { s0 += xr[i]; s1 += xr[16 + i]; }
         sx[0] = s0; sx[1] = s1; sx[2] = 0.f; sx[3] = 0.f;
+    } else {   // the IQ decoders use no activation sums
+        sx[0] = sx[1] = sx[2] = sx[3] = 0.f;
     }
 }
 
@@ -484,37 +486,57 @@ __device__ __forceinline__ float partner(float v, uint32_t m, uint32_t lane) {
     }
 }
 
-// Sum over aligned groups of g lanes (g a power of two <= 64); every lane of
-// a group receives the sum.
-__device__ __forceinline__ float group_sum(float v, uint32_t g) {
+// log2 of a power of two that is a compile-time constant after inlining.
+__host__ __device__ constexpr int ilog2(uint32_t v) { return v <= 1 ? 0 : 1 + ilog2(v >> 1); }
+
+// Sum over aligned groups of G lanes (G a power of two <= 64); every lane of
+// a group receives the sum. The loops below run a constant number of times so
+// they unroll into fixed DPP / permlane exchanges.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
     const uint32_t lane = threadIdx.x & 63u;
-    for (uint32_t m = g >> 1; m >= 1; m >>= 1) v += partner(v, m, lane);
+#pragma unroll
+    for (int i = 1; i <= ilog2(G); i++) v += partner(v, (uint32_t)G >> i, lane);
     return v;
 }
 
 // Reduce-scatter: each lane holds S partial sums v[0..S) (one per row step)
-// of a group of g lanes (S <= g). Returns the full group sum of step
-// s = (lane & (g-1)) >> log2(g/S); all lanes of each g/S sub-group get it.
-template <int S>
-__device__ __forceinline__ float reduce_scatter(float (&v)[S], uint32_t g) {
+// of a group of G lanes (S <= G). Returns the full group sum of step
+// s = (lane & (G-1)) >> log2(G/S); all lanes of each G/S sub-group get it.
+// G is a compile-time constant so every lane exchange is a fixed DPP /
+// permlane instruction.
+template <int S, int G>
+__device__ __forceinline__ float reduce_scatter_k(float (&v)[S]) {
     const uint32_t lane = threadIdx.x & 63u;
     float w[S];
 #pragma unroll
     for (int i = 0; i < S; i++) w[i] = v[i];
-    uint32_t m = g >> 1;
 #pragma unroll
-    for (int n = S / 2; n >= 1; n /= 2) {
+    for (int st = 1; st <= ilog2(S); st++) {   // S/2, S/4, .. values remain
+        const uint32_t m = (uint32_t)G >> st;
+        const int n = S >> st;
         const bool up = (lane & m) != 0;
 #pragma unroll
         for (int i = 0; i < n; i++) {
             const float a = w[i], b = w[i + n];
             w[i] = (up ? b : a) + partner(up ? a : b, m, lane);
         }
-        m >>= 1;
     }
     float r = w[0];
-    for (; m >= 1; m >>= 1) r += partner(r, m, lane);
+#pragma unroll
+    for (int st = ilog2(S) + 1; st <= ilog2(G); st++) r += partner(r, (uint32_t)G >> st, lane);
     return r;
+}
+
+// The same for a run-time group size g in {8, 16, 32, 64}.
+template <int S>
+__device__ __forceinline__ float reduce_scatter_c(float (&v)[S], uint32_t g) {
+    switch (g) {
+    case 64: return reduce_scatter_k<S, 64>(v);
+    case 32: return reduce_scatter_k<S, 32>(v);
+    case 16: return reduce_scatter_k<S, 16>(v);
+    default: return reduce_scatter_k<S, 8>(v);
+    }
 }
 
 template <int S>

@@ -23,6 +23,7 @@
 // fixed, so each lane keeps its unit's activations in registers across rows,
 // and the rows of one step are always 8 GGUF blocks (<= 1680 bytes).
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdarg.h>
 #include <stdint.h>
@@ -43,10 +44,46 @@ __device__ const IqTables g_tabs = make_tables();
 
 constexpr int kWG = 256;           // threads per workgroup (4 waves)
 constexpr uint32_t kMaxTok = 4;    // tokens per decode launch
-constexpr uint32_t kLdsBudget = 64 * 1024;
-constexpr int kProfEv = 5;         // events per profiled MoE call (4 kernels)
+constexpr uint32_t kLdsBudget = 64 * 1024;   // dynamic LDS per workgroup
+constexpr int kProfEv = 6;         // events per profiled MoE call (3 kernels x start/stop)
 
 thread_local char g_err[512];
+#ifdef QW6_TRACE
+// Per-workgroup wall-clock spans of the MoE kernels (instrumented builds
+// only): g_trace[kernel][block] = {start, end} of wave 0, 100 MHz ticks.
+__device__ unsigned long long g_trace[4][4096][2];
+struct TraceScope {
+    int k;
+    __device__ explicit TraceScope(int k_) : k(k_) {
+        if (threadIdx.x == 0 && blockIdx.x < 4096) g_trace[k][blockIdx.x][0] = wall_clock64();
+    }
+    __device__ ~TraceScope() {
+        if (threadIdx.x == 0 && blockIdx.x < 4096) g_trace[k][blockIdx.x][1] = wall_clock64();
+    }
+};
+#define TRACE_SCOPE(k) TraceScope trace_scope_(k)
+__device__ unsigned long long g_mark[4][4096][6];
+#ifdef QW6_TRACE_MARKS
+// Phase marks: wave 0's clock after its outstanding memory operations have
+// completed (the wait changes the kernel's timing; diagnostic builds only).
+#define TRACE_MARK(k, i)                                                            \
+    do {                                                                            \
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");                 \
+        if (threadIdx.x == 0 && blockIdx.x < 4096) g_mark[k][blockIdx.x][i] = wall_clock64(); \
+    } while (0)
+#else
+#define TRACE_MARK(k, i) do {} while (0)
+#endif
+#define TRACE_MARK_IF(c, k, i) \
+    do {                       \
+        if (c) TRACE_MARK(k, i); \
+    } while (0)
+#else
+#define TRACE_SCOPE(k)
+#define TRACE_MARK(k, i)
+#define TRACE_MARK_IF(c, k, i)
+#endif
+
 
 int fail(const char* fmt, ...) {
     va_list ap;
@@ -153,7 +190,7 @@ __device__ __forceinline__ void tile_rows(int f_rt, const uint32_t* lds, uint32_
     }
     float r[T];
 #pragma unroll
-    for (int t = 0; t < T; t++) r[t] = reduce_scatter<S>(acc[t], U);
+    for (int t = 0; t < T; t++) r[t] = reduce_scatter_c<S>(acc[t], U);
     const uint32_t s = scatter_step<S>(lane, U);
     const uint32_t rl = (wave * S + s) * rps + q;
     if ((unit & (U / S - 1)) == 0 && rl < rows_valid) emit(rl, r);
@@ -223,7 +260,7 @@ __global__ __launch_bounds__(64) void k_matvec_generic(MatD W, const float* __re
     }
 #pragma unroll
     for (int t = 0; t < T; t++) {
-        const float v = group_sum(acc[t], 64);
+        const float v = group_sum<64>(acc[t]);
         if (lane == 0) y[(size_t)t * W.rows + r] = v;
     }
 }
@@ -246,85 +283,134 @@ __global__ __launch_bounds__(64) void k_matvec_f32(const float* __restrict__ w,
     }
 #pragma unroll
     for (int t = 0; t < T; t++) {
-        const float v = group_sum(acc[t], 64);
+        const float v = group_sum<64>(acc[t]);
         if (lane == 0) y[(size_t)t * rows + r] = v;
     }
 }
 
 // ---- routing ---------------------------------------------------------------------
 
-// Sortable 64-bit key of logit v at index e: the upper word maps the float
-// order onto unsigned order (-0 folded into +0, which compare equal), the
-// lower word is ~e so that equal values prefer the lower index.
-__device__ __forceinline__ uint64_t route_key(float v, uint32_t e) {
+// Order-preserving 32-bit key of a logit: unsigned key order equals float
+// order (-0 folded into +0, which compare equal). Ties between equal logits
+// are broken by index separately (lowest index wins).
+__device__ __forceinline__ uint32_t route_key(float v) {
     const uint32_t u = __float_as_uint(v + 0.0f);
-    const uint32_t k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-    return ((uint64_t)k << 32) | (uint64_t)(~e);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+constexpr uint32_t kKeyNegInf = 0x007fffffu;   // route_key(-inf)
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+    for (int i = 0; i < 6; i++) {
+        const uint32_t o = __float_as_uint(partner(__uint_as_float(v), 32u >> i, lane));
+        v = o > v ? o : v;
+    }
+    return v;
 }
 
-// One wave: top_k rounds of (max value, lowest index), the winner set to
-// -inf, then softmax over the selected values in selection order
-// (qw6_cpu_moe_route, qw6.c:2796-2827). Branch-free: each round is a 64-bit
-// key maximum over the wave. Lane 0 writes idx/w (any memory). Inputs
-// without NaN reproduce qw6's indices exactly, including its ties and its
-// re-selection of an -inf entry once only -inf values remain.
-__device__ __forceinline__ void wave_route(const float* logits, uint32_t n, uint32_t top_k,
-                                           uint32_t* idx, float* w) {
-    const uint32_t lane = threadIdx.x & 63;
-    uint64_t key[4];
-    const uint64_t none = 0;   // below every real key
+// The routing of one token: selected experts in selection order and their
+// gate weights (wave-uniform values).
+struct Route {
+    uint32_t e[8];
+    float w[8];
+};
+
+// One wave routes one token (qw6_cpu_moe_route, qw6.c:2796-2827): top_k
+// rounds of (largest logit, lowest index among equal ones), the winner set to
+// -inf, then a softmax over the selected logits in selection order.
+// Lane l holds experts 4l .. 4l+3, sorted by key (stable, so equal keys keep
+// index order). A round is one 32-bit wave maximum over the lane heads; the
+// lowest lane whose head equals it holds the lowest index with that logit,
+// and pops its head. Once only -inf logits remain, qw6's scan (start at
+// index 0, strict >) picks index 0 every round; so does this one. Logits
+// without NaN give qw6's indices exactly.
+__device__ __forceinline__ void wave_route(const float* __restrict__ logits, uint32_t n,
+                                           uint32_t top_k, Route& r) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t k[4], id[4];
+    if ((((uintptr_t)logits & 15u) == 0) && 4 * lane + 3 < n) {
+        const float4 v = *(const float4*)(logits + 4 * lane);
+        k[0] = route_key(v.x); k[1] = route_key(v.y); k[2] = route_key(v.z); k[3] = route_key(v.w);
+    } else {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const uint32_t e = lane + 64u * i;
-        key[i] = e < n ? route_key(logits[e], e) : none;
+        for (int i = 0; i < 4; i++) k[i] = 4 * lane + i < n ? route_key(logits[4 * lane + i]) : 0u;
     }
-    const uint64_t ninf = (uint64_t)(~0xff800000u & 0x7fffffffu) << 32;   // key(-inf) >> 32 << 32
+#pragma unroll
+    for (int i = 0; i < 4; i++) id[i] = (uint32_t)i;
+    // stable descending sort of the lane's 4 keys (adjacent exchanges only)
+    auto cx = [&](int p) {
+        const bool sw = k[p + 1] > k[p];
+        const uint32_t k0 = k[p], k1 = k[p + 1], i0 = id[p], i1 = id[p + 1];
+        k[p] = sw ? k1 : k0; k[p + 1] = sw ? k0 : k1;
+        id[p] = sw ? i1 : i0; id[p + 1] = sw ? i0 : i1;
+    };
+    cx(0); cx(1); cx(2); cx(0); cx(1); cx(0);
     float sel[8];
-    uint32_t sid[8];
 #pragma unroll
-    for (uint32_t k = 0; k < 8; k++) {
-        if (k >= top_k) break;
-        uint64_t best = key[0];
-#pragma unroll
-        for (int i = 1; i < 4; i++) best = key[i] > best ? key[i] : best;
-#pragma unroll
-        for (uint32_t m = 32; m >= 1; m >>= 1) {
-            const uint32_t lo = __float_as_uint(partner(__uint_as_float((uint32_t)best), m, lane));
-            const uint32_t hi = __float_as_uint(partner(__uint_as_float((uint32_t)(best >> 32)), m, lane));
-            const uint64_t o = ((uint64_t)hi << 32) | lo;
-            best = o > best ? o : best;
+    for (uint32_t kk = 0; kk < 8; kk++) {
+        if (kk >= top_k) break;
+        const uint32_t m = wave_max_u32(k[0]);
+        if (m <= kKeyNegInf) {   // nothing above -inf left
+            r.e[kk] = 0;
+            sel[kk] = -INFINITY;
+            continue;
         }
-        const uint32_t e = ~(uint32_t)best;
-        const uint32_t ku = (uint32_t)(best >> 32);
-        const uint32_t fu = (ku & 0x80000000u) ? (ku & 0x7fffffffu) : ~ku;
-        sel[k] = __uint_as_float(fu);
-        sid[k] = e;
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            if (lane + 64u * i == e) key[i] = ninf | (uint64_t)(~e);
+        const uint64_t b = __ballot(k[0] == m);
+        const uint32_t w = (uint32_t)__ffsll((unsigned long long)b) - 1u;
+        r.e[kk] = 4 * w + (uint32_t)__builtin_amdgcn_readlane((int)id[0], (int)w);
+        sel[kk] = key_value(m);
+        if (lane == w) {
+            k[0] = k[1]; k[1] = k[2]; k[2] = k[3]; k[3] = 0u;
+            id[0] = id[1]; id[1] = id[2]; id[2] = id[3];
+        }
     }
-    if (lane == 0) {
-        float mx = sel[0];
+    float mx = sel[0];
 #pragma unroll
-        for (uint32_t k = 1; k < 8; k++)
-            if (k < top_k) mx = sel[k] > mx ? sel[k] : mx;
-        float ex[8], sum = 0.f;
+    for (uint32_t kk = 1; kk < 8; kk++)
+        if (kk < top_k) mx = sel[kk] > mx ? sel[kk] : mx;
+    float sum = 0.f;
 #pragma unroll
-        for (uint32_t k = 0; k < 8; k++)
-            if (k < top_k) { ex[k] = expf(sel[k] - mx); sum += ex[k]; }
+    for (uint32_t kk = 0; kk < 8; kk++)
+        if (kk < top_k) { r.w[kk] = expf(sel[kk] - mx); sum += r.w[kk]; }
 #pragma unroll
-        for (uint32_t k = 0; k < 8; k++)
-            if (k < top_k) { idx[k] = sid[k]; w[k] = ex[k] / sum; }
-    }
+    for (uint32_t kk = 0; kk < 8; kk++)
+        if (kk < top_k) r.w[kk] = r.w[kk] / sum;
 }
 
 __global__ __launch_bounds__(64) void k_route(const float* __restrict__ logits, uint32_t n,
                                               uint32_t top_k, uint32_t* idx, float* w) {
     const uint32_t t = blockIdx.x;
-    wave_route(logits + (size_t)t * n, n, top_k, idx + t * top_k, w + t * top_k);
+    Route r;
+    wave_route(logits + (size_t)t * n, n, top_k, r);
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (uint32_t k = 0; k < 8; k++)
+            if (k < top_k) {
+                idx[t * top_k + k] = r.e[k];
+                w[t * top_k + k] = r.w[k];
+            }
+    }
 }
 
 // ---- MoE decode kernels --------------------------------------------------------------
+//
+// Three kernels per layer (a kernel boundary is the cheapest grid-wide
+// dependency on this GPU; in-kernel grid barriers cost several times more):
+//   k_moe_router : router GEMV, one wave per expert row (+ optional RMSNorm of
+//                  the input, + the shared-expert gate weight).
+//   k_moe_gate_up: workgroups of the shared expert start streaming at once;
+//                  the routed ones route the tokens themselves from the logits
+//                  (1 KB per token), then stream gate/up rows of one selected
+//                  expert; silu(gate) * up -> mid. Workgroup 0 also publishes
+//                  the slot table (selected experts resolved to matrices).
+//   k_moe_down   : one workgroup per tile of output rows, one wave per
+//                  selected expert (the shared one first, it needs no routing);
+//                  row sums meet in LDS and are combined in a fixed order with
+//                  the residual -- no atomics, deterministic.
 
 struct ExpertEnt {            // device expert table entry
     const uint8_t* p[3];      // gate, up, down
@@ -349,34 +435,39 @@ constexpr int kStepsDn = 2;     // row steps per wave, down
 constexpr uint32_t kMaxSlots = kMaxTok * 8;
 constexpr uint32_t kSlotBytes = 2048;   // LDS slot of one step group (8 blocks <= 1680 B)
 
-// One selected expert ("slot"), resolved by the route kernel: its three
-// matrices and per-token gate weights. p[0] == nullptr marks an unused slot.
-struct SlotDesc {
-    const uint8_t* p[3];
-    int32_t fmt[3];
-    uint32_t rb[3];
-    float wt[kMaxTok];
+// The slot table k_moe_gate_up publishes for k_moe_down: distinct selected
+// experts in first-use order with their down matrix and per-token weights.
+struct SlotTable {
+    uint32_t n;                    // number of slots in use
+    uint32_t pad[3];
+    const uint8_t* p[kMaxSlots];   // down matrix of slot u
+    int32_t fmt[kMaxSlots];
+    uint32_t rb[kMaxSlots];
+    float wt[kMaxSlots][kMaxTok];  // gate weight of slot u for token t (0: unused)
 };
 
 struct MoeArgs {
     uint32_t hidden, inter, n_experts, top_k, T, max_u;
-    SlotDesc* slots;          // [max_u]
-    const float* x;
-    const float* router;
-    const float* logits_in;
-    const float* shared_router;
+    const float* x;               // layer input [T][hidden]
+    const float* xin;             // input of the expert matvecs (x or its RMSNorm)
+    const float* router;          // F32 router or nullptr
+    const float* route_logits;    // logits the routing reads (workspace or given)
+    const float* shared_router;   // nullptr: shared weight 1
+    const float* norm_w;          // RMSNorm weight or nullptr
+    float norm_eps;
+    uint32_t n_sh_wg;             // shared-expert workgroups in k_moe_gate_up
     const ExpertEnt* experts;
     PackRef pk[3];
-    MatD sg, su, sd;          // shared expert; sg.p == nullptr: none
-    float* logits;            // [T][n_experts]
-    float* sw;                // [T] shared weight
-    float* mid;               // [(max_u + 1)][T][inter], shared at max_u
+    MatD sg, su, sd;              // shared expert; sg.p == nullptr: none
+    float* logits;                // [T][n_experts] workspace
+    float* xn;                    // [T][hidden] normalised input (norm_w set)
+    float* sw;                    // [T] shared weight (written when shared_router)
+    SlotTable* slots;
+    float* mid;                   // [(max_u + 1)][T][inter], shared expert at max_u
     const float* residual;
     float* out;
     uint32_t* idx_out;
     float* w_out;
-    uint32_t n_router_wg, rr_per_wg;     // router workgroups, rows per router WG
-    uint32_t n_gu_waves;                 // waves per gate/up matrix pair
     uint32_t tmask_gu, tmask_dn;
 };
 
@@ -416,25 +507,33 @@ __device__ __forceinline__ void wait_vm(uint32_t n) {
     case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
     case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
     case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
+    case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+    case 32: asm volatile("s_waitcnt vmcnt(32)" ::: "memory"); break;
     default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
     }
 }
 
-// Routing of all T tokens from the router logits, recomputed by every
-// workgroup that needs it (a few hundred instructions from 1 KB per token)
-// instead of a serial "last workgroup" pass: waves route one token each, then
-// wave 0 numbers the distinct experts in first-use order. Leaves s_slot_e[u]
-// (expert of slot u), s_wt[u][t] (its gate weight for token t, 0 if unused)
-// and *s_n (number of slots) in LDS.
+// Routing of all T tokens inside one workgroup: wave t routes token t; the
+// distinct selected experts are numbered in first-use order ("slots").
+// Leaves s_slot_e[u] (expert of slot u), s_wt[u][t] (gate weight of slot u
+// for token t, 0 if unused), s_idx / s_w (per-token selection) and *s_n.
 template <int T>
 __device__ __forceinline__ void route_prologue(const MoeArgs& a, uint32_t* s_idx, float* s_w,
-                               uint32_t* s_slot_e, float* s_wt, uint32_t* s_n) {
+                                               uint32_t* s_slot_e, float* s_wt, uint32_t* s_n) {
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    const uint32_t nw = blockDim.x >> 6;
-    for (uint32_t i = threadIdx.x; i < kMaxSlots * kMaxTok; i += blockDim.x) s_wt[i] = 0.f;
-    for (uint32_t t = wave; t < T; t += nw)
-        wave_route(a.logits + (size_t)t * a.n_experts, a.n_experts, a.top_k,
-                   s_idx + t * a.top_k, s_w + t * a.top_k);
+    if (wave < (uint32_t)T) {
+        Route r;
+        wave_route(a.route_logits + (size_t)wave * a.n_experts, a.n_experts, a.top_k, r);
+        if (lane == 0) {
+#pragma unroll
+            for (uint32_t k = 0; k < 8; k++)
+                if (k < a.top_k) {
+                    s_idx[wave * a.top_k + k] = r.e[k];
+                    s_w[wave * a.top_k + k] = r.w[k];
+                }
+        }
+    }
     __syncthreads();
     if (wave == 0) {
         const uint32_t ne = T * a.top_k;
@@ -446,74 +545,116 @@ __device__ __forceinline__ void route_prologue(const MoeArgs& a, uint32_t* s_idx
         const bool is_first = lane < ne && first == lane;
         const uint64_t mask = __ballot(is_first);
         const uint32_t slot = __popcll(mask & ((1ull << first) - 1ull));
+        for (uint32_t i = lane; i < kMaxSlots * kMaxTok; i += 64) s_wt[i] = 0.f;
         if (is_first) s_slot_e[slot] = e;
-        if (lane < ne) s_wt[slot * kMaxTok + lane / a.top_k] = s_w[lane];
         if (lane == 0) *s_n = (uint32_t)__popcll(mask);
+        __builtin_amdgcn_wave_barrier();
+        if (lane < ne) s_wt[slot * kMaxTok + lane / a.top_k] = s_w[lane];
     }
     __syncthreads();
 }
 
-// Routing of all T tokens, once per layer: route_prologue, then one
-// parallel round of expert lookups into the slot descriptors the expert
-// kernels read, plus the optional idx / w outputs.
+// x (T tokens) -> optional RMSNorm (qw6_cpu_rmsnorm, qw6.c:2503-2513) ->
+// router logits; one wave per expert row. Each wave holds the whole input
+// in registers, so with norm_w set every wave computes the norm scale itself
+// and wave e writes its slice of the normalised input for the expert kernels.
+// Block n_experts (when present) computes the shared-expert gate weight
+// sigmoid(shared_router . x) (qw6.c:2267-2285).
 template <int T>
-__global__ __launch_bounds__(kWG) void k_moe_route(MoeArgs a) {
-    __shared__ uint32_t s_idx[kMaxSlots], s_slot_e[kMaxSlots], s_n;
-    __shared__ float s_w[kMaxSlots], s_wt[kMaxSlots * kMaxTok];
-    route_prologue<T>(a, s_idx, s_w, s_slot_e, s_wt, &s_n);
-    const uint32_t tid = threadIdx.x;
-    if (tid < a.max_u) {
-        SlotDesc d;
-        if (tid < s_n) {
-            const uint32_t e = s_slot_e[tid];
+__global__ __launch_bounds__(64) void k_moe_router(MoeArgs a) {
+    TRACE_SCOPE(0);
+    const uint32_t lane = threadIdx.x, e = blockIdx.x;
+    const uint32_t H = a.hidden, n4 = H / 256;   // float4 per lane (H multiple of 256)
+    float4 xv[T][8];
 #pragma unroll
-            for (int k = 0; k < 3; k++) {
-                const MatD m = expert_mat(a, e, k);
-                d.p[k] = m.p; d.fmt[k] = m.fmt; d.rb[k] = m.rb;
+    for (int t = 0; t < T; t++)
+#pragma unroll
+        for (uint32_t i = 0; i < 8; i++)
+            if (i < n4) xv[t][i] = ((const float4*)(a.x + (size_t)t * H))[64 * i + lane];
+    float4 wv[8];
+    const float* wrow = e < a.n_experts ? a.router + (size_t)e * H : a.shared_router;
+#pragma unroll
+    for (uint32_t i = 0; i < 8; i++)
+        if (i < n4) wv[i] = ((const float4*)wrow)[64 * i + lane];
+    if (a.norm_w) {
+        float4 nw[8];
+#pragma unroll
+        for (uint32_t i = 0; i < 8; i++)
+            if (i < n4) nw[i] = ((const float4*)a.norm_w)[64 * i + lane];
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            float ss = 0.f;
+#pragma unroll
+            for (uint32_t i = 0; i < 8; i++)
+                if (i < n4) {
+                    ss = fmaf(xv[t][i].x, xv[t][i].x, ss); ss = fmaf(xv[t][i].y, xv[t][i].y, ss);
+                    ss = fmaf(xv[t][i].z, xv[t][i].z, ss); ss = fmaf(xv[t][i].w, xv[t][i].w, ss);
+                }
+            ss = group_sum<64>(ss);
+            const float sc = 1.0f / sqrtf(ss / (float)H + a.norm_eps);
+#pragma unroll
+            for (uint32_t i = 0; i < 8; i++)
+                if (i < n4) {
+                    xv[t][i].x = xv[t][i].x * sc * nw[i].x; xv[t][i].y = xv[t][i].y * sc * nw[i].y;
+                    xv[t][i].z = xv[t][i].z * sc * nw[i].z; xv[t][i].w = xv[t][i].w * sc * nw[i].w;
+                }
+            // wave e writes float4s [e * per, (e + 1) * per) of the normalised input
+            const uint32_t nq = H / 4, nwv = a.n_experts + (a.shared_router ? 1u : 0u);
+            const uint32_t per = (nq + nwv - 1) / nwv;
+#pragma unroll
+            for (uint32_t i = 0; i < 8; i++) {
+                const uint32_t q = 64 * i + lane;
+                if (i < n4 && q >= e * per && q < (e + 1) * per)
+                    ((float4*)(a.xn + (size_t)t * H))[q] = xv[t][i];
             }
-        } else {
-#pragma unroll
-            for (int k = 0; k < 3; k++) { d.p[k] = nullptr; d.fmt[k] = 0; d.rb[k] = 0; }
         }
-#pragma unroll
-        for (uint32_t t = 0; t < kMaxTok; t++) d.wt[t] = s_wt[tid * kMaxTok + t];
-        a.slots[tid] = d;
     }
-    if (tid < T * a.top_k) {
-        if (a.idx_out) a.idx_out[tid] = s_idx[tid];
-        if (a.w_out) a.w_out[tid] = s_w[tid];
+#pragma unroll
+    for (int t = 0; t < T; t++) {
+        float acc = 0.f;
+#pragma unroll
+        for (uint32_t i = 0; i < 8; i++)
+            if (i < n4) {
+                acc = fmaf(wv[i].x, xv[t][i].x, acc); acc = fmaf(wv[i].y, xv[t][i].y, acc);
+                acc = fmaf(wv[i].z, xv[t][i].z, acc); acc = fmaf(wv[i].w, xv[t][i].w, acc);
+            }
+        acc = group_sum<64>(acc);
+        if (lane == 0) {
+            if (e < a.n_experts) a.logits[(size_t)t * a.n_experts + e] = acc;
+            else a.sw[t] = 1.0f / (1.0f + expf(-acc));
+        }
     }
 }
 
-// gate/up/silu of one wave: S steps of rps rows starting at local row
-// (w*S)*rps of rows [r0, ...) of the pair (G, Up) -> mid[T][inter].
-// slots: 2*S LDS slots of kSlotBytes. Activations from global memory (L2).
-template <int T, int FF>
+// gate/up/silu of one wave: S steps of rps rows starting at row0 of the pair
+// (G, Up) -> mid[T][inter]. slots: 2*S LDS slots of kSlotBytes. xr/sx: this
+// lane's activations, loaded before the weights' addresses were known.
+template <int T, int FF, int KU>
 __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint32_t row0,
-                                             const float* x, uint32_t hidden, float* mid,
-                                             uint32_t inter, uint8_t* slots, const uint32_t* tab) {
+                                             const float (&xr)[T][32], const float (&sx)[T][4],
+                                             float* mid, uint32_t inter, uint8_t* slots,
+                                             const uint32_t* lds, uint32_t slot_off,
+                                             const uint32_t* tab) {
     constexpr int S = kStepsGu;
     const int f = FF >= 0 ? FF : G.fmt;
-    const uint32_t U = hidden >> 5, rps = 64 / U;
+    constexpr uint32_t U = KU, rps = 64 / KU;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t unit = lane & (U - 1), blk = unit >> 3, q = lane / U;
     const int j = (int)(unit & 7);
     const uint32_t bb = fmt_block_bytes(f);
     const uint32_t gbytes = rps * G.rb;   // one step group (8 blocks)
-    float xr[T][32], sx[T][4];
-    load_x_all<T, FF>(f, x, hidden, hidden, xr, sx);
 #pragma unroll
     for (int s = 0; s < S; s++) {
         const size_t r = row0 + (size_t)s * rps;
         stage_group(slots + (2 * s) * kSlotBytes, G.p + r * G.rb, gbytes);
         stage_group(slots + (2 * s + 1) * kSlotBytes, Up.p + r * Up.rb, gbytes);
     }
-    const uint32_t* lds = (const uint32_t*)slots;
-    const uint32_t boff = q * G.rb + blk * bb;
+    const uint32_t boff = slot_off + q * G.rb + blk * bb;
     float ag[T][S], au[T][S];
 #pragma unroll
     for (int s = 0; s < S; s++) {
         wait_vm(4u * (S - 1 - s));
+        TRACE_MARK_IF(s == 0, 2, 1);
         float g[T], u[T];
 #pragma unroll
         for (int t = 0; t < T; t++) { g[t] = 0.f; u[t] = 0.f; }
@@ -522,11 +663,12 @@ __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint
 #pragma unroll
         for (int t = 0; t < T; t++) { ag[t][s] = g[t]; au[t][s] = u[t]; }
     }
+    TRACE_MARK(2, 2);
     float gv[T], uv[T];
 #pragma unroll
     for (int t = 0; t < T; t++) {
-        gv[t] = reduce_scatter<S>(ag[t], U);
-        uv[t] = reduce_scatter<S>(au[t], U);
+        gv[t] = reduce_scatter_k<S, KU>(ag[t]);
+        uv[t] = reduce_scatter_k<S, KU>(au[t]);
     }
     if ((unit & (U / S - 1)) == 0) {
         const uint32_t s = scatter_step<S>(lane, U);
@@ -535,166 +677,165 @@ __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint
         for (int t = 0; t < T; t++)
             mid[(size_t)t * inter + r] = gv[t] / (1.0f + expf(-gv[t])) * uv[t];
     }
+    TRACE_MARK(2, 3);
 }
 
-// Router GEMV over all experts (one wave per row), plus the shared expert's
-// gate/up/SiLU (independent of routing) and the shared-expert weight.
-template <int T, int FG>
-__global__ __launch_bounds__(kWG) void k_moe_router(MoeArgs a) {
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    const uint32_t b = blockIdx.x;
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (b >= a.n_router_wg) {   // shared expert gate/up, 4 waves x S steps per block
-        const uint32_t toff = tab_bytes(a.tmask_gu);
-        stage_tables(smem, a.tmask_gu);
-        if (a.tmask_gu) stage_wait();
-        const uint32_t U = a.hidden >> 5, rps = 64 / U;
-        const uint32_t row0 = ((b - a.n_router_wg) * 4 + wave) * kStepsGu * rps;
-        if (row0 < a.inter)
-            wave_gate_up<T, FG>(a.sg, a.su, row0, a.x, a.hidden,
-                                a.mid + (size_t)a.max_u * T * a.inter, a.inter,
-                                smem + toff + wave * 2 * kStepsGu * kSlotBytes,
-                                (const uint32_t*)smem);
-        return;
-    }
-    if (b == 0 && wave == 0) {   // shared-expert weight: sigmoid(shared_router . x) or 1
-        for (uint32_t t = 0; t < T; t++) {
-            float acc = 0.f;
-            if (a.shared_router)
-                for (uint32_t c = lane; c < a.hidden; c += 64)
-                    acc = fmaf(a.shared_router[c], a.x[(size_t)t * a.hidden + c], acc);
-            acc = group_sum(acc, 64);
-            if (lane == 0) a.sw[t] = a.shared_router ? 1.0f / (1.0f + expf(-acc)) : 1.0f;
-        }
-    }
-    const uint32_t e0 = b * a.rr_per_wg, e1 = min(e0 + a.rr_per_wg, a.n_experts);
-    if (a.router) {
-        for (uint32_t e = e0 + wave; e < e1; e += 4) {
-            const float4* wr = (const float4*)(a.router + (size_t)e * a.hidden);
-            float acc[T];
-#pragma unroll
-            for (int t = 0; t < T; t++) acc[t] = 0.f;
-            for (uint32_t c = lane; c < a.hidden / 4; c += 64) {
-                const float4 wv = wr[c];
-#pragma unroll
-                for (int t = 0; t < T; t++) {
-                    const float4 xv = ((const float4*)(a.x + (size_t)t * a.hidden))[c];
-                    acc[t] = fmaf(wv.x, xv.x, acc[t]);
-                    acc[t] = fmaf(wv.y, xv.y, acc[t]);
-                    acc[t] = fmaf(wv.z, xv.z, acc[t]);
-                    acc[t] = fmaf(wv.w, xv.w, acc[t]);
-                }
-            }
-#pragma unroll
-            for (int t = 0; t < T; t++) {
-                const float v = group_sum(acc[t], 64);
-                if (lane == 0) a.logits[(size_t)t * a.n_experts + e] = v;
-            }
-        }
-    } else {
-        for (uint32_t i = threadIdx.x; i < (e1 - e0) * T; i += kWG) {
-            const uint32_t t = i / (e1 - e0), e = e0 + i % (e1 - e0);
-            a.logits[(size_t)t * a.n_experts + e] = a.logits_in[(size_t)t * a.n_experts + e];
-        }
-    }
-}
-
-// Routed gate/up/SiLU: workgroup (slot u, tile): 4 waves, each S steps.
-template <int T, int FG>
+// Routed + shared gate/up/SiLU. Blocks [0, n_sh_wg) stream the shared
+// expert right away; the others route the tokens (each workgroup on its
+// own), then take (slot u, row tile). 4 waves x S steps per block.
+template <int T, int FG, int KU>
 __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
+    TRACE_SCOPE(2);
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ uint32_t s_idx[kMaxSlots], s_slot_e[kMaxSlots], s_n;
+    __shared__ float s_w[kMaxSlots], s_wt[kMaxSlots * kMaxTok];
     const uint32_t wave = threadIdx.x >> 6;
-    const uint32_t U = a.hidden >> 5, rps = 64 / U;
-    const uint32_t rows_wg = 4 * kStepsGu * rps;
+    constexpr uint32_t rps = 64 / KU;
+    constexpr uint32_t rows_wg = 4 * kStepsGu * rps;
     const uint32_t ntile = (a.inter + rows_wg - 1) / rows_wg;
-    const uint32_t u = blockIdx.x / ntile, tile = blockIdx.x % ntile;
     const uint32_t toff = tab_bytes(a.tmask_gu);
+    uint8_t* wslots = smem + toff + wave * 2 * kStepsGu * kSlotBytes;
+    const uint32_t slot_off = toff + wave * 2 * kStepsGu * kSlotBytes;
     stage_tables(smem, a.tmask_gu);
-    const SlotDesc& d = a.slots[u];
-    const uint8_t* pg = d.p[0];
-    if (!pg) return;
-    if (a.tmask_gu) stage_wait();
-    const MatD G = {pg, d.fmt[0], a.inter, a.hidden, d.rb[0]};
-    const MatD Up = {d.p[1], d.fmt[1], a.inter, a.hidden, d.rb[1]};
-    const uint32_t row0 = (tile * 4 + wave) * kStepsGu * rps;
+    const bool shared_wg = blockIdx.x < a.n_sh_wg;
+    // Activations first when their unit layout is known before the routing
+    // (one gate/up format): their loads then overlap the logits round trip.
+    const bool early = FG >= 0 || shared_wg || a.pk[0].regular;
+    const int fx = FG >= 0 ? FG : shared_wg ? a.sg.fmt : a.pk[0].fmt;
+    float xr[T][32], sx[T][4];
+    if (early) load_x_all<T, FG>(fx, a.xin, a.hidden, a.hidden, xr, sx);
+    if (a.tmask_gu) {   // the lattice tables are in LDS before any wave reads them
+        if (early) wait_vm(8u * T);
+        else wait_vm(0);
+        __syncthreads();
+    }
+    MatD G, Up;
+    uint32_t row0;
+    float* midp;
+    if (shared_wg) {
+        G = a.sg;
+        Up = a.su;
+        row0 = (blockIdx.x * 4 + wave) * kStepsGu * rps;
+        midp = a.mid + (size_t)a.max_u * T * a.inter;
+    } else {
+        route_prologue<T>(a, s_idx, s_w, s_slot_e, s_wt, &s_n);   // ends with a barrier
+        TRACE_MARK(2, 0);
+        const uint32_t b = blockIdx.x - a.n_sh_wg;
+        const uint32_t u = b / ntile, tile = b % ntile;
+        const uint32_t nslot = s_n;
+        if (b == 0) {   // publish the routing and the slot table for k_moe_down
+            const uint32_t tid = threadIdx.x;
+            if (tid < T * a.top_k) {
+                if (a.idx_out) a.idx_out[tid] = s_idx[tid];
+                if (a.w_out) a.w_out[tid] = s_w[tid];
+            }
+            if (tid < a.max_u) {
+                SlotTable* st = a.slots;
+                if (tid < nslot) {
+                    const MatD D = expert_mat(a, s_slot_e[tid], 2);
+                    st->p[tid] = D.p; st->fmt[tid] = D.fmt; st->rb[tid] = D.rb;
+                } else {
+                    st->p[tid] = nullptr; st->fmt[tid] = 0; st->rb[tid] = 0;
+                }
+#pragma unroll
+                for (uint32_t t = 0; t < kMaxTok; t++) st->wt[tid][t] = s_wt[tid * kMaxTok + t];
+            }
+            if (tid == 0) a.slots->n = nslot;
+        }
+        if (u >= nslot) return;
+        const uint32_t e = s_slot_e[u];
+        G = expert_mat(a, e, 0);
+        Up = expert_mat(a, e, 1);
+        row0 = (tile * 4 + wave) * kStepsGu * rps;
+        midp = a.mid + (size_t)u * T * a.inter;
+        if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr, sx);
+    }
     if (row0 >= a.inter) return;
-    wave_gate_up<T, FG>(G, Up, row0, a.x, a.hidden, a.mid + (size_t)u * T * a.inter, a.inter,
-                        smem + toff + wave * 2 * kStepsGu * kSlotBytes, (const uint32_t*)smem);
+    wave_gate_up<T, FG, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, (const uint32_t*)smem,
+                            slot_off, (const uint32_t*)smem);
 }
 
-// Down projection + combine for rows [r0, r0 + R), R = S * rps: wave w takes
-// slots w, w + nw, ... (routed slots in first-use order, the shared expert
-// last); per-slot row sums meet in LDS and are combined in slot order:
-// out = sum_u wt[u] * y[u] + sw * y[shared] (+ residual).
-constexpr uint32_t down_waves(int T) { return T == 1 ? 16u : 8u; }
+// Down projection + combine for rows [r0, r0 + R), R = S * rps. Matrix m of
+// the block: m = 0 the shared expert (when present; no routing needed, so
+// its wave starts streaming at once), then the slots in first-use order.
+// Wave w takes matrices w, w + nw, ...; row sums meet in LDS and are
+// combined as out = sum_u wt[u] * y[u] + sw * y[shared] (+ residual).
+template <int T>
+__host__ __device__ constexpr uint32_t down_waves() { return T == 1 ? 9u : 8u; }
 
-template <int T, int FD>
-__global__ __launch_bounds__(64 * down_waves(T)) void k_moe_down(MoeArgs a) {
+template <int T, int FD, int KU>
+__global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
+    TRACE_SCOPE(3);
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ SlotDesc s_d[kMaxSlots];
-    __shared__ uint32_t s_n;
+    __shared__ float s_wt[kMaxSlots * kMaxTok];
     constexpr int S = kStepsDn;
-    const uint32_t U = a.inter >> 5, rps = 64 / U;
-    const uint32_t R = S * rps;
+    constexpr uint32_t U = KU, rps = 64 / KU;
+    constexpr uint32_t R = S * rps;
     const uint32_t r0 = blockIdx.x * R;
     const uint32_t nw = blockDim.x >> 6;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const bool has_sh = a.sd.p != nullptr;
+    const uint32_t has_sh = a.sd.p != nullptr ? 1u : 0u;
     const uint32_t toff = tab_bytes(a.tmask_dn);
     stage_tables(smem, a.tmask_dn);
-    if (threadIdx.x < a.max_u) s_d[threadIdx.x] = a.slots[threadIdx.x];
-    if (a.tmask_dn) wave_wait();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint32_t n = 0;
-        while (n < a.max_u && s_d[n].p[0]) n++;
-        s_n = n;
-    }
-    __syncthreads();
-    const uint32_t nslot = s_n, ntot = nslot + (has_sh ? 1u : 0u);
-    float* ybuf = (float*)(smem + toff + nw * S * kSlotBytes);   // [ntot][R][T]
+    float* ybuf = (float*)(smem + toff + nw * S * kSlotBytes);   // [m][R][T]
     uint8_t* slots = smem + toff + wave * S * kSlotBytes;
+    const uint32_t slot_off = toff + wave * S * kSlotBytes;
     const uint32_t unit = lane & (U - 1), blk = unit >> 3, q = lane / U;
     const int j = (int)(unit & 7);
-    for (uint32_t u = wave; u < ntot; u += nw) {
-        const MatD D = u < nslot ? MatD{s_d[u].p[2], s_d[u].fmt[2], a.hidden, a.inter, s_d[u].rb[2]}
-                                 : a.sd;
-        const int f = FD >= 0 ? FD : D.fmt;
-        const float* xm = a.mid + (size_t)(u < nslot ? u : a.max_u) * T * a.inter;
+    const uint32_t nslot = a.slots->n;   // one scalar load, shared by every wave
+    if (threadIdx.x < kMaxSlots * kMaxTok)
+        s_wt[threadIdx.x] = a.slots->wt[threadIdx.x / kMaxTok][threadIdx.x % kMaxTok];
+    const uint32_t ntot = nslot + has_sh;
+    if (a.tmask_dn) {   // the lattice tables are in LDS before any wave reads them
+        wave_wait();
+        __syncthreads();
+    }
+    for (uint32_t m = wave; m < ntot; m += nw) {
+        const bool sh = has_sh && m == 0;
+        const uint32_t u = m - has_sh;
+        const float* xm = a.mid + (size_t)(sh ? a.max_u : u) * T * a.inter;
         float xr[T][32], sx[T][4];
-        load_x_all<T, FD>(f, xm, a.inter, a.inter, xr, sx);
+        // activations (independent of the slot table) before the weights
+        if (FD >= 0) load_x_all<T, FD>(FD, xm, a.inter, a.inter, xr, sx);
+        const MatD D = sh ? a.sd : MatD{a.slots->p[u], a.slots->fmt[u], a.hidden, a.inter,
+                                        a.slots->rb[u]};
+        const int f = FD >= 0 ? FD : D.fmt;
+        if (FD < 0) load_x_all<T, FD>(f, xm, a.inter, a.inter, xr, sx);
 #pragma unroll
         for (int s = 0; s < S; s++)
             stage_group(slots + s * kSlotBytes, D.p + (size_t)(r0 + s * rps) * D.rb, rps * D.rb);
         const uint32_t bb = fmt_block_bytes(f);
-        const uint32_t boff = q * D.rb + blk * bb;
+        const uint32_t boff = slot_off + q * D.rb + blk * bb;
         float acc[T][S];
 #pragma unroll
         for (int s = 0; s < S; s++) {
             wait_vm(2u * (S - 1 - s));
+            TRACE_MARK_IF(s == 0 && m == wave, 3, 1);
             float v[T];
 #pragma unroll
             for (int t = 0; t < T; t++) v[t] = 0.f;
-            unit_dot<T>(f, (const uint32_t*)smem, (uint32_t)(slots - smem) + s * kSlotBytes + boff,
-                        j, (const uint32_t*)smem, xr, sx, v);
+            unit_dot<T>(f, (const uint32_t*)smem, s * kSlotBytes + boff, j, (const uint32_t*)smem,
+                        xr, sx, v);
 #pragma unroll
             for (int t = 0; t < T; t++) acc[t][s] = v[t];
         }
         float r[T];
 #pragma unroll
-        for (int t = 0; t < T; t++) r[t] = reduce_scatter<S>(acc[t], U);
+        for (int t = 0; t < T; t++) r[t] = reduce_scatter_k<S, KU>(acc[t]);
         if ((unit & (U / S - 1)) == 0) {
             const uint32_t rl = scatter_step<S>(lane, U) * rps + q;
 #pragma unroll
-            for (int t = 0; t < T; t++) ybuf[(u * R + rl) * T + t] = r[t];
+            for (int t = 0; t < T; t++) ybuf[(m * R + rl) * T + t] = r[t];
         }
     }
+    TRACE_MARK(3, 2);
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < R * T; i += blockDim.x) {
         const uint32_t rl = i / T, t = i % T;
         float v = 0.f;
-        for (uint32_t u = 0; u < nslot; u++) v = fmaf(s_d[u].wt[t], ybuf[(u * R + rl) * T + t], v);
-        if (has_sh) v = fmaf(a.sw[t], ybuf[(nslot * R + rl) * T + t], v);
+        for (uint32_t u = 0; u < nslot; u++)
+            v = fmaf(s_wt[u * kMaxTok + t], ybuf[((u + has_sh) * R + rl) * T + t], v);
+        if (has_sh) v = fmaf(a.shared_router ? a.sw[t] : 1.0f, ybuf[rl * T + t], v);
         if (a.residual) v += a.residual[(size_t)t * a.hidden + r0 + rl];
         a.out[(size_t)t * a.hidden + r0 + rl] = v;
     }
@@ -724,7 +865,7 @@ __global__ __launch_bounds__(kWG) void k_rmsnorm(const float* x, const float* w,
     float* yr = y + (size_t)blockIdx.x * n;
     float ss = 0.f;
     for (uint32_t i = threadIdx.x; i < n; i += kWG) ss = fmaf(xr[i], xr[i], ss);
-    ss = group_sum(ss, 64);
+    ss = group_sum<64>(ss);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
     __syncthreads();
     const float tot = red[0] + red[1] + red[2] + red[3];
@@ -782,9 +923,10 @@ struct qw6_hip_ctx_s {
     // decode workspace
     float* logits;
     float* sw;
-    SlotDesc* slots;
+    float* xn;
+    SlotTable* slots;
     float* mid;
-    uint32_t ws_experts, ws_inter, ws_topk;
+    uint32_t ws_hidden, ws_inter;
     // per-kernel timing (qw6_hip_profile)
     std::vector<hipEvent_t> prof_ev;
     uint32_t prof_cap, prof_calls;
@@ -946,6 +1088,22 @@ int alloc_owned(qw6_hip_ctx_t* c, size_t bytes, void** p) {
 extern "C" {
 
 const char* qw6_hip_last_error(void) { return g_err; }
+
+#ifdef QW6_TRACE
+int qw6_hip_trace_read(void* host) {
+    CK(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_trace), sizeof(g_trace)));
+    return 0;
+}
+int qw6_hip_mark_read(void* host) {
+    CK(hipMemcpyFromSymbol(host, HIP_SYMBOL(g_mark), sizeof(g_mark)));
+    return 0;
+}
+int qw6_hip_trace_clear(void) {
+    static unsigned long long z[4][4096][2];
+    CK(hipMemcpyToSymbol(HIP_SYMBOL(g_trace), z, sizeof(z)));
+    return 0;
+}
+#endif
 
 int qw6_hip_matvec_f32_host(const float* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols) {
@@ -1197,55 +1355,101 @@ void qw6_hip_experts_free(qw6_hip_experts_t* e) {
 
 namespace {
 
-int ensure_ws(qw6_hip_ctx_t* c, uint32_t n_experts, uint32_t inter, uint32_t top_k) {
-    if (c->logits && c->ws_experts >= n_experts && c->ws_inter >= inter && c->ws_topk >= top_k)
-        return 0;
-    const uint32_t T = kMaxTok;
-    n_experts = n_experts > 256 ? n_experts : 256;
+int ensure_ws(qw6_hip_ctx_t* c, uint32_t hidden, uint32_t inter) {
+    if (c->logits && c->ws_hidden >= hidden && c->ws_inter >= inter) return 0;
+    hidden = hidden > c->ws_hidden ? hidden : c->ws_hidden;
     inter = inter > c->ws_inter ? inter : c->ws_inter;
     void* p;
-    if (alloc_owned(c, (size_t)T * n_experts * 4, &p)) return -1;
+    if (alloc_owned(c, (size_t)kMaxTok * 256 * 4, &p)) return -1;
     c->logits = (float*)p;
-    if (alloc_owned(c, T * 4, &p)) return -1;
+    if (alloc_owned(c, kMaxTok * 4, &p)) return -1;
     c->sw = (float*)p;
-    if (alloc_owned(c, sizeof(SlotDesc) * kMaxSlots, &p)) return -1;
-    c->slots = (SlotDesc*)p;
-    if (alloc_owned(c, (size_t)(kMaxSlots + 1) * T * inter * 4, &p)) return -1;
+    if (alloc_owned(c, (size_t)kMaxTok * hidden * 4, &p)) return -1;
+    c->xn = (float*)p;
+    if (alloc_owned(c, sizeof(SlotTable), &p)) return -1;
+    c->slots = (SlotTable*)p;
+    if (alloc_owned(c, (size_t)(kMaxSlots + 1) * kMaxTok * inter * 4, &p)) return -1;
     c->mid = (float*)p;
-    c->ws_experts = n_experts;
+    c->ws_hidden = hidden;
     c->ws_inter = inter;
-    c->ws_topk = 8;
     return 0;
 }
 
-int launch_moe(const MoeArgs& a, int fs, int fg, int fd, size_t lds_r, uint32_t grid_r,
-               size_t lds_b, uint32_t grid_b, size_t lds_c, uint32_t grid_c, uint32_t nw_c,
-               hipStream_t st, hipEvent_t* ev) {
-    if (ev) CK(hipEventRecord(ev[0], st));
-    launch_by_fmt(fs, a.T, [&](auto tc, auto fc) {
-        k_moe_router<decltype(tc)::value, decltype(fc)::value><<<grid_r, kWG, lds_r, st>>>(a);
-    });
-    CK(hipGetLastError());
-    if (ev) CK(hipEventRecord(ev[1], st));
-    switch (a.T) {
-    case 1: k_moe_route<1><<<1, kWG, 0, st>>>(a); break;
-    case 2: k_moe_route<2><<<1, kWG, 0, st>>>(a); break;
-    case 3: k_moe_route<3><<<1, kWG, 0, st>>>(a); break;
-    default: k_moe_route<4><<<1, kWG, 0, st>>>(a); break;
+// A kernel launch, timed by its own dispatch (hipExtLaunchKernel start/stop
+// events, no extra queue packets) when ev is given.
+template <typename... Args>
+int launch_k(void (*kern)(Args...), uint32_t grid, uint32_t block, size_t lds, hipStream_t st,
+             hipEvent_t* ev, const MoeArgs& a) {
+    if (ev) {
+        void* args[] = {(void*)&a};
+        CK(hipExtLaunchKernel((const void*)kern, dim3(grid), dim3(block), args, lds, st, ev[0],
+                              ev[1], 0));
+    } else {
+        kern<<<grid, block, lds, st>>>(a);
+        CK(hipGetLastError());
     }
-    CK(hipGetLastError());
-    if (ev) CK(hipEventRecord(ev[2], st));
-    launch_by_fmt(fg, a.T, [&](auto tc, auto fc) {
-        k_moe_gate_up<decltype(tc)::value, decltype(fc)::value><<<grid_b, kWG, lds_b, st>>>(a);
-    });
-    CK(hipGetLastError());
-    if (ev) CK(hipEventRecord(ev[3], st));
-    launch_by_fmt(fd, a.T, [&](auto tc, auto fc) {
-        k_moe_down<decltype(tc)::value, decltype(fc)::value><<<grid_c, 64 * nw_c, lds_c, st>>>(a);
-    });
-    CK(hipGetLastError());
-    if (ev) CK(hipEventRecord(ev[4], st));
     return 0;
+}
+
+struct MoeLaunch {
+    bool router;             // k_moe_router runs
+    uint32_t grid_r;
+    int fg, fd;              // format of the gate/up (down) kernels, -1: mixed
+    size_t lds_b, lds_c;
+    uint32_t grid_b, grid_c, nw_c;
+};
+
+// Run fn(IC<T>, IC<F>, IC<KU>) for the expert-kernel instantiation of T
+// tokens, format f and KU = K/32 units per row: format- and size-specialised
+// kernels for 1-2 tokens at the model's row length KU_fast, the generic
+// (format switch) kernel otherwise.
+template <int KU_fast, typename Fn>
+void launch_expert_kernel(int f, uint32_t T, uint32_t KU, Fn fn) {
+    if (T <= 2 && f >= 0 && KU == (uint32_t)KU_fast) {
+        launch_by_fmt(f, T, [&](auto tc, auto fc) { fn(tc, fc, IC<KU_fast>{}); });
+        return;
+    }
+    auto by_ku = [&](auto tc) {
+        switch (KU) {
+        case 8: fn(tc, IC<-1>{}, IC<8>{}); break;
+        case 16: fn(tc, IC<-1>{}, IC<16>{}); break;
+        case 32: fn(tc, IC<-1>{}, IC<32>{}); break;
+        default: fn(tc, IC<-1>{}, IC<64>{}); break;
+        }
+    };
+    switch (T) {
+    case 1: by_ku(IC<1>{}); break;
+    case 2: by_ku(IC<2>{}); break;
+    case 3: by_ku(IC<3>{}); break;
+    default: by_ku(IC<4>{}); break;
+    }
+}
+
+int launch_moe(const MoeArgs& a, const MoeLaunch& m, hipStream_t st, hipEvent_t* ev) {
+    if (m.router) {
+        int rc = 0;
+        switch (a.T) {
+        case 1: rc = launch_k(k_moe_router<1>, m.grid_r, 64, 0, st, ev, a); break;
+        case 2: rc = launch_k(k_moe_router<2>, m.grid_r, 64, 0, st, ev, a); break;
+        case 3: rc = launch_k(k_moe_router<3>, m.grid_r, 64, 0, st, ev, a); break;
+        default: rc = launch_k(k_moe_router<4>, m.grid_r, 64, 0, st, ev, a); break;
+        }
+        if (rc) return rc;
+    } else if (ev) {
+        CK(hipEventRecord(ev[0], st));
+        CK(hipEventRecord(ev[1], st));
+    }
+    int rc = 0;
+    launch_expert_kernel<64>(m.fg, a.T, a.hidden / 32, [&](auto tc, auto fc, auto kc) {
+        rc = launch_k(k_moe_gate_up<decltype(tc)::value, decltype(fc)::value, decltype(kc)::value>,
+                      m.grid_b, kWG, m.lds_b, st, ev ? ev + 2 : nullptr, a);
+    });
+    if (rc) return rc;
+    launch_expert_kernel<16>(m.fd, a.T, a.inter / 32, [&](auto tc, auto fc, auto kc) {
+        rc = launch_k(k_moe_down<decltype(tc)::value, decltype(fc)::value, decltype(kc)::value>,
+                      m.grid_c, 64 * m.nw_c, m.lds_c, st, ev ? ev + 4 : nullptr, a);
+    });
+    return rc;
 }
 
 }  // namespace
@@ -1266,8 +1470,9 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
         return fail("decode MoE kernels need hidden and inter in {256, 512, 1024, 2048}");
     if (L->top_k == 0 || L->top_k > 8 || L->top_k > E->n) return fail("top_k %u out of range", L->top_k);
     if (!L->router && !logits) return fail("neither router nor logits given");
-    if (((uintptr_t)L->router | (uintptr_t)x | (uintptr_t)out) & 15u)
-        return fail("router, x and out must be 16-byte aligned");
+    if (((uintptr_t)L->router | (uintptr_t)x | (uintptr_t)out | (uintptr_t)L->shared_router |
+         (uintptr_t)L->norm_w) & 15u)
+        return fail("router, shared_router, norm_w, x and out must be 16-byte aligned");
     const bool has_sh = L->shared_gate.data != nullptr;
     MatD sg = {nullptr, 0, 0, 0, 0}, su = sg, sd = sg;
     uint32_t mgu = E->tmask_gu, mdn = E->tmask_dn;
@@ -1281,12 +1486,18 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
             if (f < 0) return fail("F32 shared expert not supported");
             const uint32_t wr = k < 2 ? L->inter : L->hidden, wc = k < 2 ? L->hidden : L->inter;
             if (m[k]->rows != wr || m[k]->cols != wc) return fail("shared matrix %d shape", k);
+            if ((uintptr_t)m[k]->data & 15u) return fail("shared matrix %d not 16-B aligned", k);
             *d[k] = {(const uint8_t*)m[k]->data, f, wr, wc, (wc / 256) * fmt_block_bytes(f)};
             (k < 2 ? mgu : mdn) |= fmt_table_mask(f);
         }
+    } else if (L->shared_router) {
+        return fail("shared_router given without a shared expert");
     }
+    // every expert's gate and up share a format, so one unit layout serves both
+    if (!E->gu_same || (has_sh && sg.fmt != su.fmt))
+        return fail("gate and up of each expert must share a quant type");
     DevGuard g(c->device);
-    if (ensure_ws(c, E->n, L->inter, L->top_k)) return -1;
+    if (ensure_ws(c, L->hidden, L->inter)) return -1;
     hipStream_t st = (hipStream_t)stream;
 
     MoeArgs a;
@@ -1296,51 +1507,51 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
     a.n_experts = E->n;
     a.top_k = L->top_k;
     a.shared_router = L->shared_router;
+    a.norm_w = L->norm_w;
+    a.norm_eps = L->norm_eps;
     a.experts = E->dev;
     for (int k = 0; k < 3; k++) a.pk[k] = E->pk[k];
     a.sg = sg; a.su = su; a.sd = sd;
-    a.logits = c->logits; a.sw = c->sw; a.mid = c->mid; a.slots = c->slots;
+    a.logits = c->logits; a.sw = c->sw; a.xn = c->xn; a.mid = c->mid; a.slots = c->slots;
     a.tmask_gu = mgu;
     a.tmask_dn = mdn;
-    // kernels specialised on one weight format where a matrix kind has one
-    if (!E->gu_same || (has_sh && sg.fmt != su.fmt))
-        return fail("gate and up of each expert must share a quant type");
-    const int fg = E->fmt_gu, fs = has_sh ? sg.fmt : fg;
-    int fd = E->fmt_dn;
-    if (has_sh && sd.fmt != fd) fd = -1;
+
+    MoeLaunch m;
+    m.fg = (has_sh && sg.fmt != E->fmt_gu) ? -1 : E->fmt_gu;
+    m.fd = (has_sh && sd.fmt != E->fmt_dn) ? -1 : E->fmt_dn;
     const uint32_t rpsg = 64 / (L->hidden / 32), rpsd = 64 / (L->inter / 32);
     const uint32_t rows_wg = 4 * kStepsGu * rpsg;          // gate/up rows per workgroup
     const uint32_t ntile_b = (L->inter + rows_wg - 1) / rows_wg;
-    const uint32_t nsh_wg = has_sh ? ntile_b : 0;
-    const size_t lds_gu = (size_t)tab_bytes(mgu) + 4 * 2 * kStepsGu * kSlotBytes;
+    a.n_sh_wg = has_sh ? ntile_b : 0;
+    m.lds_b = (size_t)tab_bytes(mgu) + 4 * 2 * kStepsGu * kSlotBytes;
     const uint32_t R_c = kStepsDn * rpsd;
-    const uint32_t grid_c = (L->hidden + R_c - 1) / R_c;
+    m.grid_c = (L->hidden + R_c - 1) / R_c;
+    m.router = L->router != nullptr || L->shared_router != nullptr || L->norm_w != nullptr;
+    m.grid_r = E->n + (L->shared_router ? 1u : 0u);
+    if (m.lds_b > kLdsBudget) return fail("gate/up tile exceeds the LDS budget");
 
     for (uint32_t t0 = 0; t0 < n_tok; t0 += kMaxTok) {
         const uint32_t T = n_tok - t0 < kMaxTok ? n_tok - t0 : kMaxTok;
         a.T = T;
         a.max_u = T * L->top_k;
         a.x = x + (size_t)t0 * L->hidden;
-        a.logits_in = logits ? logits + (size_t)t0 * E->n : nullptr;
+        a.xin = L->norm_w ? c->xn : a.x;
         a.router = logits ? nullptr : L->router;
-        a.rr_per_wg = a.router ? 4 : E->n;
-        a.n_router_wg = (E->n + a.rr_per_wg - 1) / a.rr_per_wg;
+        a.route_logits = logits ? logits + (size_t)t0 * E->n : c->logits;
         a.residual = residual ? residual + (size_t)t0 * L->hidden : nullptr;
         a.out = out + (size_t)t0 * L->hidden;
         a.idx_out = idx ? idx + (size_t)t0 * L->top_k : nullptr;
         a.w_out = w ? w + (size_t)t0 * L->top_k : nullptr;
-        const uint32_t grid_r = a.n_router_wg + nsh_wg;
-        const uint32_t grid_b = a.max_u * ntile_b;
+        m.grid_b = a.n_sh_wg + a.max_u * ntile_b;
         const uint32_t ntot = a.max_u + (has_sh ? 1u : 0u);
-        const uint32_t nw_max = T == 1 ? down_waves(1) : down_waves(2);
-        const uint32_t nw_c = ntot < nw_max ? ntot : nw_max;
-        const size_t lds_c = (size_t)tab_bytes(mdn) + (size_t)nw_c * kStepsDn * kSlotBytes +
-                             (size_t)ntot * R_c * T * 4 + 16;
-        if (lds_c > kLdsBudget) return fail("down tile exceeds the LDS budget");
+        const uint32_t nw_max = T == 1 ? down_waves<1>() : T == 2 ? down_waves<2>() : down_waves<3>();
+        m.nw_c = ntot < nw_max ? ntot : nw_max;
+        m.lds_c = (size_t)tab_bytes(mdn) + (size_t)m.nw_c * kStepsDn * kSlotBytes +
+                  (size_t)ntot * R_c * T * 4 + 16;
+        if (m.lds_c > kLdsBudget) return fail("down tile exceeds the LDS budget");
         hipEvent_t* ev = nullptr;
         if (c->prof_calls < c->prof_cap) ev = &c->prof_ev[kProfEv * c->prof_calls++];
-        const int rc = launch_moe(a, fs, fg, fd, lds_gu, grid_r, lds_gu, grid_b, lds_c,
-                                  grid_c, nw_c, st, ev);
+        const int rc = launch_moe(a, m, st, ev);
         if (rc) return rc;
     }
     return 0;
@@ -1359,15 +1570,16 @@ int qw6_hip_profile(qw6_hip_ctx_t* c, uint32_t max_calls) {
     return 0;
 }
 
-int qw6_hip_profile_read(qw6_hip_ctx_t* c, float ms[4], uint32_t* calls) {
+int qw6_hip_profile_read(qw6_hip_ctx_t* c, float ms[3], uint32_t* calls) {
     if (!c || !ms || !calls) return fail("null pointer");
     DevGuard g(c->device);
-    for (int k = 0; k < kProfEv - 1; k++) ms[k] = 0.f;
+    for (int k = 0; k < 3; k++) ms[k] = 0.f;
     for (uint32_t i = 0; i < c->prof_calls; i++) {
         CK(hipEventSynchronize(c->prof_ev[kProfEv * i + kProfEv - 1]));
-        for (int k = 0; k < kProfEv - 1; k++) {
+        for (int k = 0; k < 3; k++) {
             float t = 0.f;
-            CK(hipEventElapsedTime(&t, c->prof_ev[kProfEv * i + k], c->prof_ev[kProfEv * i + k + 1]));
+            CK(hipEventElapsedTime(&t, c->prof_ev[kProfEv * i + 2 * k],
+                                   c->prof_ev[kProfEv * i + 2 * k + 1]));
             ms[k] += t;
         }
     }
