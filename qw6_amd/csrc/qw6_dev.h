@@ -86,16 +86,11 @@ constexpr IqTables make_tables() {
 
 // ---- scalar helpers ------------------------------------------------------------
 
-// Exact binary16 -> binary32 in integer arithmetic (independent of the fp16
-// denormal mode): subnormal halves are m * 2^-24, exact in fp32.
+// Exact binary16 -> binary32: v_cvt_f32_f16. The kernels run with f16 and
+// f32 denormals preserved (denorm mode 3 in every kernel descriptor), so
+// subnormal halves convert to their exact normal f32 values (qw6.c:1448-1471).
 __device__ __forceinline__ float h2f(uint32_t h) {
-    const uint32_t sign = (h & 0x8000u) << 16;
-    const uint32_t e = (h >> 10) & 0x1fu;
-    const uint32_t m = h & 0x3ffu;
-    uint32_t bits = sign | ((e + 112u) << 23) | (m << 13);
-    if (e == 0x1f) bits = sign | 0x7f800000u | (m << 13);
-    if (e == 0) bits = sign | __float_as_uint((float)m * 0x1p-24f);
-    return __uint_as_float(bits);
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
 // float -> binary16, round to nearest even, subnormals kept (synthetic data).
@@ -139,7 +134,18 @@ __device__ __forceinline__ uint64_t lds64_tab(const uint32_t* s, uint32_t off) {
     return (uint64_t)v.x | ((uint64_t)v.y << 32);
 }
 
-__device__ __forceinline__ float ub(uint32_t w, int n) { return (float)((w >> (8 * n)) & 0xffu); }
+// Byte n of w as a float: one v_cvt_f32_ubyteN (the compiler would otherwise
+// emit a bit-field extract plus a conversion).
+__device__ __forceinline__ float ub(uint32_t w, int n) {
+    float r;
+    switch (n) {
+    case 0: asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w)); break;
+    case 1: asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w)); break;
+    case 2: asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(w)); break;
+    default: asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(w)); break;
+    }
+    return r;
+}
 // ±v where bit n of `signs` set means negative.
 __device__ __forceinline__ float sgn(float v, uint32_t signs, int n) {
     return __uint_as_float(__float_as_uint(v) ^ (((signs >> n) & 1u) << 31));
@@ -200,105 +206,95 @@ __device__ __forceinline__ void load_unit_x(int f, const float* __restrict__ x, 
 // s: LDS words; bo: byte offset of the block in LDS; tab: LDS words of the
 // lattice tables (IqTables layout at offset 0).
 
-// Q4_K (qw6.c:1492-1516): w = (d*sc)*q - dmin*m per 32-run.
+// Q4_K / Q5_K block scales (qw6_get_scale_min_k4, qw6.c:1480-1490). The 8
+// lanes of a block hold units j = 0..7 (lane & 7); lane j decodes sub-block
+// j's 6-bit (scale, min) and two quad permutes hand every lane the pair of
+// its own unit, sub-blocks 2(j/2) (low nibbles) and 2(j/2)+1 (high nibbles).
+// hdr = the block's first 16 bytes {d|dmin, scales[0..3], [4..7], [8..11]}.
+struct KScales {
+    float da, ma, db, mb;   // d*sc and dmin*m of the low / high sub-block
+};
+__device__ __forceinline__ KScales k_scales(const uint4& hdr, int j) {
+    const float d = h2f(hdr.x & 0xffffu), dmin = h2f(hdr.x >> 16);
+    const uint32_t sh = 8u * (uint32_t)(j & 3);
+    const uint32_t sc_lo = __builtin_amdgcn_ubfe(hdr.y, sh, 6);
+    const uint32_t m_lo = __builtin_amdgcn_ubfe(hdr.z, sh, 6);
+    const uint32_t sc_hi = __builtin_amdgcn_ubfe(hdr.w, sh, 4) | (__builtin_amdgcn_ubfe(hdr.y, sh + 6, 2) << 4);
+    const uint32_t m_hi = __builtin_amdgcn_ubfe(hdr.w, sh + 4, 4) | (__builtin_amdgcn_ubfe(hdr.z, sh + 6, 2) << 4);
+    const float fd = d * (float)(j < 4 ? sc_lo : sc_hi);
+    const float fm = dmin * (float)(j < 4 ? m_lo : m_hi);
+    const uint32_t ud = __float_as_uint(fd), um = __float_as_uint(fm);
+    KScales k;
+    k.da = __uint_as_float(__builtin_amdgcn_update_dpp(0u, ud, 0xA0, 0xf, 0xf, false));  // [0,0,2,2]
+    k.db = __uint_as_float(__builtin_amdgcn_update_dpp(0u, ud, 0xF5, 0xf, 0xf, false));  // [1,1,3,3]
+    k.ma = __uint_as_float(__builtin_amdgcn_update_dpp(0u, um, 0xA0, 0xf, 0xf, false));
+    k.mb = __uint_as_float(__builtin_amdgcn_update_dpp(0u, um, 0xF5, 0xf, 0xf, false));
+    return k;
+}
+
+// Q4_K (qw6.c:1492-1516): w = (d*sc)*q - dmin*m per 32-run. Blocks are 144 B,
+// so bo is 16-byte aligned.
 template <int T>
 __device__ __forceinline__ void unit_q4k(const uint32_t* s, uint32_t bo, int j,
                                          const float (&xr)[T][32], const float (&sx)[T][4],
                                          float (&acc)[T]) {
-    const uint32_t dm = s[bo >> 2];
-    const float d = h2f(dm & 0xffffu), dmin = h2f(dm >> 16);
-    const uint64_t sl = (uint64_t)s[(bo + 4) >> 2] | ((uint64_t)s[(bo + 8) >> 2] << 32);
-    const uint32_t sh = s[(bo + 12) >> 2];
-    auto byte = [&](int k) -> uint32_t {
-        return k < 8 ? (uint32_t)(sl >> (8 * k)) & 0xffu : (sh >> (8 * (k - 8))) & 0xffu;
-    };
-    const int p = j >> 1;
-    const int sa = 2 * p, sb = 2 * p + 1;
-    uint32_t sca, ma, scb, mb;
-    if (p < 2) {
-        sca = byte(sa) & 63; ma = byte(sa + 4) & 63;
-        scb = byte(sb) & 63; mb = byte(sb + 4) & 63;
-    } else {
-        sca = (byte(sa + 4) & 0xf) | ((byte(sa - 4) >> 6) << 4);
-        ma = (byte(sa + 4) >> 4) | ((byte(sa) >> 6) << 4);
-        scb = (byte(sb + 4) & 0xf) | ((byte(sb - 4) >> 6) << 4);
-        mb = (byte(sb + 4) >> 4) | ((byte(sb) >> 6) << 4);
-    }
+    const uint4 hdr = *(const uint4*)(s + (bo >> 2));
     const uint4 q = *(const uint4*)(s + ((bo + 16 + 16 * j) >> 2));
+    const KScales k = k_scales(hdr, j);
     const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
     float lo[T], hi[T];
 #pragma unroll
     for (int t = 0; t < T; t++) { lo[t] = 0.f; hi[t] = 0.f; }
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const uint32_t l4 = qw[k] & 0x0f0f0f0fu, h4 = (qw[k] >> 4) & 0x0f0f0f0fu;
+    for (int i = 0; i < 4; i++) {
+        const uint32_t l4 = qw[i] & 0x0f0f0f0fu, h4 = (qw[i] >> 4) & 0x0f0f0f0fu;
 #pragma unroll
         for (int n = 0; n < 4; n++) {
             const float fl = ub(l4, n), fh = ub(h4, n);
 #pragma unroll
             for (int t = 0; t < T; t++) {
-                lo[t] = fmaf(fl, xr[t][4 * k + n], lo[t]);
-                hi[t] = fmaf(fh, xr[t][16 + 4 * k + n], hi[t]);
+                lo[t] = fmaf(fl, xr[t][4 * i + n], lo[t]);
+                hi[t] = fmaf(fh, xr[t][16 + 4 * i + n], hi[t]);
             }
         }
     }
-    const float da = d * (float)sca, mma = dmin * (float)ma;
-    const float db = d * (float)scb, mmb = dmin * (float)mb;
 #pragma unroll
     for (int t = 0; t < T; t++)
-        acc[t] += (da * lo[t] - mma * sx[t][0]) + (db * hi[t] - mmb * sx[t][1]);
+        acc[t] += (k.da * lo[t] - k.ma * sx[t][0]) + (k.db * hi[t] - k.mb * sx[t][1]);
 }
 
-// Q5_K (qw6.c:1518-1548): as Q4_K with a fifth bit from qh.
+// Q5_K (qw6.c:1518-1548): as Q4_K with a fifth bit from qh. Blocks are 176 B.
 template <int T>
 __device__ __forceinline__ void unit_q5k(const uint32_t* s, uint32_t bo, int j,
                                          const float (&xr)[T][32], const float (&sx)[T][4],
                                          float (&acc)[T]) {
-    const uint32_t dm = s[bo >> 2];
-    const float d = h2f(dm & 0xffffu), dmin = h2f(dm >> 16);
-    const uint64_t sl = (uint64_t)s[(bo + 4) >> 2] | ((uint64_t)s[(bo + 8) >> 2] << 32);
-    const uint32_t sh = s[(bo + 12) >> 2];
-    auto byte = [&](int k) -> uint32_t {
-        return k < 8 ? (uint32_t)(sl >> (8 * k)) & 0xffu : (sh >> (8 * (k - 8))) & 0xffu;
-    };
-    const int p = j >> 1;
-    const int sa = 2 * p, sb = 2 * p + 1;
-    uint32_t sca, ma, scb, mb;
-    if (p < 2) {
-        sca = byte(sa) & 63; ma = byte(sa + 4) & 63;
-        scb = byte(sb) & 63; mb = byte(sb + 4) & 63;
-    } else {
-        sca = (byte(sa + 4) & 0xf) | ((byte(sa - 4) >> 6) << 4);
-        ma = (byte(sa + 4) >> 4) | ((byte(sa) >> 6) << 4);
-        scb = (byte(sb + 4) & 0xf) | ((byte(sb - 4) >> 6) << 4);
-        mb = (byte(sb + 4) >> 4) | ((byte(sb) >> 6) << 4);
-    }
+    const uint4 hdr = *(const uint4*)(s + (bo >> 2));
     const uint4 q = *(const uint4*)(s + ((bo + 48 + 16 * j) >> 2));
     const uint4 h = *(const uint4*)(s + ((bo + 16 + 16 * (j & 1)) >> 2));
+    const KScales k = k_scales(hdr, j);
+    const uint32_t sa = 2u * (uint32_t)(j >> 1), sb = sa + 1;
     const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
     const uint32_t hw[4] = {h.x, h.y, h.z, h.w};
     float lo[T], hi[T];
 #pragma unroll
     for (int t = 0; t < T; t++) { lo[t] = 0.f; hi[t] = 0.f; }
 #pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const uint32_t l5 = (qw[k] & 0x0f0f0f0fu) | (((hw[k] >> sa) & 0x01010101u) << 4);
-        const uint32_t h5 = ((qw[k] >> 4) & 0x0f0f0f0fu) | (((hw[k] >> sb) & 0x01010101u) << 4);
+    for (int i = 0; i < 4; i++) {
+        const uint32_t l5 = (qw[i] & 0x0f0f0f0fu) | (((hw[i] >> sa) & 0x01010101u) << 4);
+        const uint32_t h5 = ((qw[i] >> 4) & 0x0f0f0f0fu) | (((hw[i] >> sb) & 0x01010101u) << 4);
 #pragma unroll
         for (int n = 0; n < 4; n++) {
             const float fl = ub(l5, n), fh = ub(h5, n);
 #pragma unroll
             for (int t = 0; t < T; t++) {
-                lo[t] = fmaf(fl, xr[t][4 * k + n], lo[t]);
-                hi[t] = fmaf(fh, xr[t][16 + 4 * k + n], hi[t]);
+                lo[t] = fmaf(fl, xr[t][4 * i + n], lo[t]);
+                hi[t] = fmaf(fh, xr[t][16 + 4 * i + n], hi[t]);
             }
         }
     }
-    const float da = d * (float)sca, mma = dmin * (float)ma;
-    const float db = d * (float)scb, mmb = dmin * (float)mb;
 #pragma unroll
     for (int t = 0; t < T; t++)
-        acc[t] += (da * lo[t] - mma * sx[t][0]) + (db * hi[t] - mmb * sx[t][1]);
+        acc[t] += (k.da * lo[t] - k.ma * sx[t][0]) + (k.db * hi[t] - k.mb * sx[t][1]);
 }
 
 // Q6_K (qw6.c:1550-1578), qw6's even-scale rule: the 32-run k of half h uses

@@ -312,26 +312,17 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return v;
 }
 
-// The routing of one token: selected experts in selection order and their
-// gate weights (wave-uniform values).
-struct Route {
-    uint32_t e[8];
-    float w[8];
-};
+// qw6's routing (qw6_cpu_moe_route, qw6.c:2796-2827) runs top_k rounds of
+// argmax (strict >, scan from index 0, winner set to -inf): it takes the
+// top_k logits ordered by (value desc, index asc), then a softmax over them
+// in that order. Once only -inf is left, its scan picks index 0 for every
+// remaining round. Logits without NaN give qw6's indices exactly here too.
+// Lane l holds experts 4l .. 4l+3 as order-preserving keys.
 
-// One wave routes one token (qw6_cpu_moe_route, qw6.c:2796-2827): top_k
-// rounds of (largest logit, lowest index among equal ones), the winner set to
-// -inf, then a softmax over the selected logits in selection order.
-// Lane l holds experts 4l .. 4l+3, sorted by key (stable, so equal keys keep
-// index order). A round is one 32-bit wave maximum over the lane heads; the
-// lowest lane whose head equals it holds the lowest index with that logit,
-// and pops its head. Once only -inf logits remain, qw6's scan (start at
-// index 0, strict >) picks index 0 every round; so does this one. Logits
-// without NaN give qw6's indices exactly.
-__device__ __forceinline__ void wave_route(const float* __restrict__ logits, uint32_t n,
-                                           uint32_t top_k, Route& r) {
+// Keys of one token's logits (0 for the lanes past n: below every real key).
+__device__ __forceinline__ void route_keys(const float* __restrict__ logits, uint32_t n,
+                                           uint32_t (&k)[4]) {
     const uint32_t lane = threadIdx.x & 63u;
-    uint32_t k[4], id[4];
     if ((((uintptr_t)logits & 15u) == 0) && 4 * lane + 3 < n) {
         const float4 v = *(const float4*)(logits + 4 * lane);
         k[0] = route_key(v.x); k[1] = route_key(v.y); k[2] = route_key(v.z); k[3] = route_key(v.w);
@@ -339,9 +330,15 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ logits, uin
 #pragma unroll
         for (int i = 0; i < 4; i++) k[i] = 4 * lane + i < n ? route_key(logits[4 * lane + i]) : 0u;
     }
-#pragma unroll
-    for (int i = 0; i < 4; i++) id[i] = (uint32_t)i;
-    // stable descending sort of the lane's 4 keys (adjacent exchanges only)
+}
+
+// Ranked selection, slow path: top_k rounds of a wave maximum over the lane
+// heads (each lane's keys sorted, stable); the lowest lane whose head equals
+// the maximum holds the lowest index with that logit and pops its head.
+// Writes the (key, index) of rank r to scr[32 + r] for r < top_k.
+__device__ __forceinline__ void route_rounds(uint32_t (&k)[4], uint32_t top_k, uint2* scr) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t id[4] = {0, 1, 2, 3};
     auto cx = [&](int p) {
         const bool sw = k[p + 1] > k[p];
         const uint32_t k0 = k[p], k1 = k[p + 1], i0 = id[p], i1 = id[p + 1];
@@ -349,51 +346,100 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ logits, uin
         id[p] = sw ? i1 : i0; id[p + 1] = sw ? i0 : i1;
     };
     cx(0); cx(1); cx(2); cx(0); cx(1); cx(0);
-    float sel[8];
-#pragma unroll
-    for (uint32_t kk = 0; kk < 8; kk++) {
-        if (kk >= top_k) break;
+    for (uint32_t r = 0; r < top_k; r++) {
         const uint32_t m = wave_max_u32(k[0]);
-        if (m <= kKeyNegInf) {   // nothing above -inf left
-            r.e[kk] = 0;
-            sel[kk] = -INFINITY;
-            continue;
-        }
         const uint64_t b = __ballot(k[0] == m);
         const uint32_t w = (uint32_t)__ffsll((unsigned long long)b) - 1u;
-        r.e[kk] = 4 * w + (uint32_t)__builtin_amdgcn_readlane((int)id[0], (int)w);
-        sel[kk] = key_value(m);
+        const uint32_t e = 4 * w + (uint32_t)__builtin_amdgcn_readlane((int)id[0], (int)w);
         if (lane == w) {
+            scr[32 + r] = make_uint2(~e, m);
             k[0] = k[1]; k[1] = k[2]; k[2] = k[3]; k[3] = 0u;
             id[0] = id[1]; id[1] = id[2]; id[2] = id[3];
         }
     }
-    float mx = sel[0];
+}
+
+// One wave routes one token. Fast path: T = the minimum over 8 groups of 8
+// lanes of each group's largest key is at most the 8th-largest key (8
+// distinct keys are >= T), so the top_k <= 8 winners are among the keys >= T
+// -- about 20 of 256 for router logits. Those candidates are compacted into
+// LDS and each is ranked against all of them at once with one 64-bit compare
+// of (key, ~index) per pair; more than 32 candidates take route_rounds.
+// scr: 40 uint2 of LDS private to the wave. Lanes j < top_k leave the j-th
+// selected expert and its gate weight in out_e[j] / out_w[j] (any memory).
+__device__ __forceinline__ void wave_route(const float* __restrict__ logits, uint32_t n,
+                                           uint32_t top_k, uint2* scr, uint32_t* out_e,
+                                           float* out_w) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t k[4];
+    route_keys(logits, n, k);
+    uint32_t g = max(max(k[0], k[1]), max(k[2], k[3]));
 #pragma unroll
-    for (uint32_t kk = 1; kk < 8; kk++)
-        if (kk < top_k) mx = sel[kk] > mx ? sel[kk] : mx;
-    float sum = 0.f;
+    for (int i = 0; i < 3; i++) {   // group maxima over lanes 8q .. 8q+7
+        const uint32_t o = __float_as_uint(partner(__uint_as_float(g), 1u << i, lane));
+        g = o > g ? o : g;
+    }
 #pragma unroll
-    for (uint32_t kk = 0; kk < 8; kk++)
-        if (kk < top_k) { r.w[kk] = expf(sel[kk] - mx); sum += r.w[kk]; }
+    for (int i = 3; i < 6; i++) {   // minimum over the 8 groups
+        const uint32_t o = __float_as_uint(partner(__uint_as_float(g), 1u << i, lane));
+        g = o < g ? o : g;
+    }
+    const uint32_t t = (uint32_t)__builtin_amdgcn_readfirstlane((int)g);
+    bool c[4];
+    uint32_t ncand = 0, pos = 0;
 #pragma unroll
-    for (uint32_t kk = 0; kk < 8; kk++)
-        if (kk < top_k) r.w[kk] = r.w[kk] / sum;
+    for (int i = 0; i < 4; i++) {
+        c[i] = k[i] >= t && k[i] != 0u;
+        const uint64_t b = __ballot(c[i]);
+        ncand += __popcll(b);
+        pos += __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+    }
+    if (ncand <= 32) {
+        // candidates of lower lanes first, then this lane's in index order
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (c[i]) scr[pos++] = make_uint2(~(4 * lane + (uint32_t)i), k[i]);
+        __builtin_amdgcn_wave_barrier();
+        if (lane < ncand) {
+            const uint2 me2 = scr[lane];
+            const uint64_t me = ((uint64_t)me2.y << 32) | me2.x;
+            uint32_t rank = 0;
+#pragma unroll
+            for (uint32_t m = 0; m < 32; m++) {
+                const uint2 o2 = scr[m];
+                const uint64_t o = ((uint64_t)o2.y << 32) | o2.x;
+                rank += (m < ncand && o > me) ? 1u : 0u;
+            }
+            if (rank < top_k) scr[32 + rank] = me2;
+        }
+    } else {
+        route_rounds(k, top_k, scr);
+    }
+    __builtin_amdgcn_wave_barrier();
+    uint32_t e = 0;
+    float v = -INFINITY;
+    if (lane < top_k) {
+        const uint2 me = scr[32 + lane];
+        v = key_value(me.y);
+        e = me.y > kKeyNegInf ? ~me.x : 0u;   // only -inf left: qw6 picks index 0
+    }
+    const float mx = key_value(scr[32].y);   // rank 0 holds the maximum
+    const float ex = lane < top_k ? expf(v - mx) : 0.f;
+    float sum = ex;
+    sum += partner(sum, 1, lane);
+    sum += partner(sum, 2, lane);
+    sum += partner(sum, 4, lane);
+    if (lane < top_k) {
+        out_e[lane] = e;
+        out_w[lane] = ex / sum;
+    }
 }
 
 __global__ __launch_bounds__(64) void k_route(const float* __restrict__ logits, uint32_t n,
                                               uint32_t top_k, uint32_t* idx, float* w) {
+    __shared__ uint2 scr[40];
     const uint32_t t = blockIdx.x;
-    Route r;
-    wave_route(logits + (size_t)t * n, n, top_k, r);
-    if (threadIdx.x == 0) {
-#pragma unroll
-        for (uint32_t k = 0; k < 8; k++)
-            if (k < top_k) {
-                idx[t * top_k + k] = r.e[k];
-                w[t * top_k + k] = r.w[k];
-            }
-    }
+    wave_route(logits + (size_t)t * n, n, top_k, scr, idx + t * top_k, w + t * top_k);
 }
 
 // ---- MoE decode kernels --------------------------------------------------------------
@@ -522,18 +568,25 @@ template <int T>
 __device__ __forceinline__ void route_prologue(const MoeArgs& a, uint32_t* s_idx, float* s_w,
                                                uint32_t* s_slot_e, float* s_wt, uint32_t* s_n) {
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    if (wave < (uint32_t)T) {
-        Route r;
-        wave_route(a.route_logits + (size_t)wave * a.n_experts, a.n_experts, a.top_k, r);
-        if (lane == 0) {
+    __shared__ uint2 s_rt[4][40];
+    if (T == 1) {   // one token: the slots are the selection itself
+        if (wave == 0) {
+            wave_route(a.route_logits, a.n_experts, a.top_k, s_rt[0], s_idx, s_w);
+            __builtin_amdgcn_wave_barrier();
+            if (lane < a.top_k) {
+                s_slot_e[lane] = s_idx[lane];
+                s_wt[lane * kMaxTok] = s_w[lane];
 #pragma unroll
-            for (uint32_t k = 0; k < 8; k++)
-                if (k < a.top_k) {
-                    s_idx[wave * a.top_k + k] = r.e[k];
-                    s_w[wave * a.top_k + k] = r.w[k];
-                }
+                for (uint32_t t = 1; t < kMaxTok; t++) s_wt[lane * kMaxTok + t] = 0.f;
+            }
+            if (lane == 0) *s_n = a.top_k;
         }
+        __syncthreads();
+        return;
     }
+    if (wave < (uint32_t)T)
+        wave_route(a.route_logits + (size_t)wave * a.n_experts, a.n_experts, a.top_k, s_rt[wave],
+                   s_idx + wave * a.top_k, s_w + wave * a.top_k);
     __syncthreads();
     if (wave == 0) {
         const uint32_t ne = T * a.top_k;
