@@ -38,7 +38,7 @@ __host__ __device__ inline int fmt_of_quant(int q) {
     }
 }
 
-__host__ __device__ inline uint32_t fmt_block_bytes(int f) {
+__host__ __device__ constexpr uint32_t fmt_block_bytes(int f) {
     switch (f) {
     case F_Q4K: return 144;
     case F_Q5K: return 176;
@@ -538,6 +538,153 @@ __device__ __forceinline__ float reduce_scatter_c(float (&v)[S], uint32_t g) {
 template <int S>
 __device__ __forceinline__ uint32_t scatter_step(uint32_t lane, uint32_t g) {
     return S == 1 ? 0u : (lane & (g - 1)) / (g / S);
+}
+
+// ---- routing ---------------------------------------------------------------------
+
+// Order-preserving 32-bit key of a logit: unsigned key order equals float
+// order (-0 folded into +0, which compare equal). Ties between equal logits
+// are broken by index separately (lowest index wins).
+__device__ __forceinline__ uint32_t route_key(float v) {
+    const uint32_t u = __float_as_uint(v + 0.0f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+__device__ __forceinline__ float key_value(uint32_t k) {
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+constexpr uint32_t kKeyNegInf = 0x007fffffu;   // route_key(-inf)
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+    for (int i = 0; i < 6; i++) {
+        const uint32_t o = __float_as_uint(partner(__uint_as_float(v), 32u >> i, lane));
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// qw6's routing (qw6_cpu_moe_route, qw6.c:2796-2827) runs top_k rounds of
+// argmax (strict >, scan from index 0, winner set to -inf): it takes the
+// top_k logits ordered by (value desc, index asc), then a softmax over them
+// in that order. Once only -inf is left, its scan picks index 0 for every
+// remaining round. Logits without NaN give qw6's indices exactly here too.
+// Lane l holds experts 4l .. 4l+3 as order-preserving keys.
+
+// Keys of one token's logits (0 for the lanes past n: below every real key).
+__device__ __forceinline__ void route_keys(const float* __restrict__ logits, uint32_t n,
+                                           uint32_t (&k)[4]) {
+    const uint32_t lane = threadIdx.x & 63u;
+    if ((((uintptr_t)logits & 15u) == 0) && 4 * lane + 3 < n) {
+        const float4 v = *(const float4*)(logits + 4 * lane);
+        k[0] = route_key(v.x); k[1] = route_key(v.y); k[2] = route_key(v.z); k[3] = route_key(v.w);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; i++) k[i] = 4 * lane + i < n ? route_key(logits[4 * lane + i]) : 0u;
+    }
+}
+
+// Ranked selection, slow path: top_k rounds of a wave maximum over the lane
+// heads (each lane's keys sorted, stable); the lowest lane whose head equals
+// the maximum holds the lowest index with that logit and pops its head.
+// Writes the (key, index) of rank r to scr[32 + r] for r < top_k.
+__device__ __forceinline__ void route_rounds(uint32_t (&k)[4], uint32_t top_k, uint2* scr) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t id[4] = {0, 1, 2, 3};
+    auto cx = [&](int p) {
+        const bool sw = k[p + 1] > k[p];
+        const uint32_t k0 = k[p], k1 = k[p + 1], i0 = id[p], i1 = id[p + 1];
+        k[p] = sw ? k1 : k0; k[p + 1] = sw ? k0 : k1;
+        id[p] = sw ? i1 : i0; id[p + 1] = sw ? i0 : i1;
+    };
+    cx(0); cx(1); cx(2); cx(0); cx(1); cx(0);
+    for (uint32_t r = 0; r < top_k; r++) {
+        const uint32_t m = wave_max_u32(k[0]);
+        const uint64_t b = __ballot(k[0] == m);
+        const uint32_t w = (uint32_t)__ffsll((unsigned long long)b) - 1u;
+        const uint32_t e = 4 * w + (uint32_t)__builtin_amdgcn_readlane((int)id[0], (int)w);
+        if (lane == w) {
+            scr[32 + r] = make_uint2(~e, m);
+            k[0] = k[1]; k[1] = k[2]; k[2] = k[3]; k[3] = 0u;
+            id[0] = id[1]; id[1] = id[2]; id[2] = id[3];
+        }
+    }
+}
+
+// One wave routes one token. Fast path: T = the minimum over 8 groups of 8
+// lanes of each group's largest key is at most the 8th-largest key (8
+// distinct keys are >= T), so the top_k <= 8 winners are among the keys >= T
+// -- about 20 of 256 for router logits. Those candidates are compacted into
+// LDS and each is ranked against all of them at once with one 64-bit compare
+// of (key, ~index) per pair; more than 32 candidates take route_rounds.
+// scr: 40 uint2 of LDS private to the wave. Lanes j < top_k leave the j-th
+// selected expert and its gate weight in out_e[j] / out_w[j] (any memory).
+__device__ __forceinline__ void wave_route(const float* __restrict__ logits, uint32_t n,
+                                           uint32_t top_k, uint2* scr, uint32_t* out_e,
+                                           float* out_w) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint32_t k[4];
+    route_keys(logits, n, k);
+    uint32_t g = max(max(k[0], k[1]), max(k[2], k[3]));
+#pragma unroll
+    for (int i = 0; i < 3; i++) {   // group maxima over lanes 8q .. 8q+7
+        const uint32_t o = __float_as_uint(partner(__uint_as_float(g), 1u << i, lane));
+        g = o > g ? o : g;
+    }
+#pragma unroll
+    for (int i = 3; i < 6; i++) {   // minimum over the 8 groups
+        const uint32_t o = __float_as_uint(partner(__uint_as_float(g), 1u << i, lane));
+        g = o < g ? o : g;
+    }
+    const uint32_t t = (uint32_t)__builtin_amdgcn_readfirstlane((int)g);
+    bool c[4];
+    uint32_t ncand = 0, pos = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        c[i] = k[i] >= t && k[i] != 0u;
+        const uint64_t b = __ballot(c[i]);
+        ncand += __popcll(b);
+        pos += __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+    }
+    if (ncand <= 32) {
+        // candidates of lower lanes first, then this lane's in index order
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (c[i]) scr[pos++] = make_uint2(~(4 * lane + (uint32_t)i), k[i]);
+        __builtin_amdgcn_wave_barrier();
+        if (lane < ncand) {
+            const uint2 me2 = scr[lane];
+            const uint64_t me = ((uint64_t)me2.y << 32) | me2.x;
+            uint32_t rank = 0;
+#pragma unroll
+            for (uint32_t m = 0; m < 32; m++) {
+                const uint2 o2 = scr[m];
+                const uint64_t o = ((uint64_t)o2.y << 32) | o2.x;
+                rank += (m < ncand && o > me) ? 1u : 0u;
+            }
+            if (rank < top_k) scr[32 + rank] = me2;
+        }
+    } else {
+        route_rounds(k, top_k, scr);
+    }
+    __builtin_amdgcn_wave_barrier();
+    uint32_t e = 0;
+    float v = -INFINITY;
+    if (lane < top_k) {
+        const uint2 me = scr[32 + lane];
+        v = key_value(me.y);
+        e = me.y > kKeyNegInf ? ~me.x : 0u;   // only -inf left: qw6 picks index 0
+    }
+    const float mx = key_value(scr[32].y);   // rank 0 holds the maximum
+    const float ex = lane < top_k ? expf(v - mx) : 0.f;
+    float sum = ex;
+    sum += partner(sum, 1, lane);
+    sum += partner(sum, 2, lane);
+    sum += partner(sum, 4, lane);
+    if (lane < top_k) {
+        out_e[lane] = e;
+        out_w[lane] = ex / sum;
+    }
 }
 
 // ---- synthetic data hash (twin of qw6_amd/synth.py) ------------------------------

@@ -35,6 +35,7 @@
 
 #include "../../include/qw6_hip.h"
 #include "qw6_dev.h"
+#include "qw6_moe.h"
 
 using namespace qw6;
 
@@ -44,6 +45,7 @@ __device__ const IqTables g_tabs = make_tables();
 
 constexpr int kWG = 256;           // threads per workgroup (4 waves)
 constexpr uint32_t kMaxTok = 4;    // tokens per decode launch
+constexpr uint32_t kGroupedMinTokens = 32;   // automatic switch to the grouped MFMA path
 constexpr uint32_t kLdsBudget = 64 * 1024;   // dynamic LDS per workgroup
 constexpr int kProfEv = 6;         // events per profiled MoE call (3 kernels x start/stop)
 
@@ -85,13 +87,18 @@ __device__ unsigned long long g_mark[4][4096][6];
 #endif
 
 
+int vfail(const char* fmt, va_list ap) {
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    fprintf(stderr, "qw6_hip: %s\n", g_err);
+    return -1;
+}
+
 int fail(const char* fmt, ...) {
     va_list ap;
     va_start(ap, fmt);
-    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    const int r = vfail(fmt, ap);
     va_end(ap);
-    fprintf(stderr, "qw6_hip: %s\n", g_err);
-    return -1;
+    return r;
 }
 
 #define CK(expr)                                                                   \
@@ -102,8 +109,6 @@ int fail(const char* fmt, ...) {
                         __FILE__, __LINE__);                                       \
     } while (0)
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
 
 // ---- staging: global bytes -> LDS ----------------------------------------------
 
@@ -154,11 +159,6 @@ __host__ __device__ inline uint32_t align16(uint32_t n) { return (n + 15u) & ~15
 
 // ---- one matrix tile: per-row dot products --------------------------------------
 
-struct MatD {
-    const uint8_t* p;
-    int32_t fmt;
-    uint32_t rows, cols, rb;   // rb: bytes per row
-};
 
 // Row tile staged in LDS at byte offset tile_off (rows [0, rows_valid)).
 // Wave `wave` owns S steps of rps = 64/U rows: local row of step s for lane
@@ -288,152 +288,7 @@ __global__ __launch_bounds__(64) void k_matvec_f32(const float* __restrict__ w,
     }
 }
 
-// ---- routing ---------------------------------------------------------------------
-
-// Order-preserving 32-bit key of a logit: unsigned key order equals float
-// order (-0 folded into +0, which compare equal). Ties between equal logits
-// are broken by index separately (lowest index wins).
-__device__ __forceinline__ uint32_t route_key(float v) {
-    const uint32_t u = __float_as_uint(v + 0.0f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-__device__ __forceinline__ float key_value(uint32_t k) {
-    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-}
-constexpr uint32_t kKeyNegInf = 0x007fffffu;   // route_key(-inf)
-
-__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    const uint32_t lane = threadIdx.x & 63u;
-#pragma unroll
-    for (int i = 0; i < 6; i++) {
-        const uint32_t o = __float_as_uint(partner(__uint_as_float(v), 32u >> i, lane));
-        v = o > v ? o : v;
-    }
-    return v;
-}
-
-// qw6's routing (qw6_cpu_moe_route, qw6.c:2796-2827) runs top_k rounds of
-// argmax (strict >, scan from index 0, winner set to -inf): it takes the
-// top_k logits ordered by (value desc, index asc), then a softmax over them
-// in that order. Once only -inf is left, its scan picks index 0 for every
-// remaining round. Logits without NaN give qw6's indices exactly here too.
-// Lane l holds experts 4l .. 4l+3 as order-preserving keys.
-
-// Keys of one token's logits (0 for the lanes past n: below every real key).
-__device__ __forceinline__ void route_keys(const float* __restrict__ logits, uint32_t n,
-                                           uint32_t (&k)[4]) {
-    const uint32_t lane = threadIdx.x & 63u;
-    if ((((uintptr_t)logits & 15u) == 0) && 4 * lane + 3 < n) {
-        const float4 v = *(const float4*)(logits + 4 * lane);
-        k[0] = route_key(v.x); k[1] = route_key(v.y); k[2] = route_key(v.z); k[3] = route_key(v.w);
-    } else {
-#pragma unroll
-        for (int i = 0; i < 4; i++) k[i] = 4 * lane + i < n ? route_key(logits[4 * lane + i]) : 0u;
-    }
-}
-
-// Ranked selection, slow path: top_k rounds of a wave maximum over the lane
-// heads (each lane's keys sorted, stable); the lowest lane whose head equals
-// the maximum holds the lowest index with that logit and pops its head.
-// Writes the (key, index) of rank r to scr[32 + r] for r < top_k.
-__device__ __forceinline__ void route_rounds(uint32_t (&k)[4], uint32_t top_k, uint2* scr) {
-    const uint32_t lane = threadIdx.x & 63u;
-    uint32_t id[4] = {0, 1, 2, 3};
-    auto cx = [&](int p) {
-        const bool sw = k[p + 1] > k[p];
-        const uint32_t k0 = k[p], k1 = k[p + 1], i0 = id[p], i1 = id[p + 1];
-        k[p] = sw ? k1 : k0; k[p + 1] = sw ? k0 : k1;
-        id[p] = sw ? i1 : i0; id[p + 1] = sw ? i0 : i1;
-    };
-    cx(0); cx(1); cx(2); cx(0); cx(1); cx(0);
-    for (uint32_t r = 0; r < top_k; r++) {
-        const uint32_t m = wave_max_u32(k[0]);
-        const uint64_t b = __ballot(k[0] == m);
-        const uint32_t w = (uint32_t)__ffsll((unsigned long long)b) - 1u;
-        const uint32_t e = 4 * w + (uint32_t)__builtin_amdgcn_readlane((int)id[0], (int)w);
-        if (lane == w) {
-            scr[32 + r] = make_uint2(~e, m);
-            k[0] = k[1]; k[1] = k[2]; k[2] = k[3]; k[3] = 0u;
-            id[0] = id[1]; id[1] = id[2]; id[2] = id[3];
-        }
-    }
-}
-
-// One wave routes one token. Fast path: T = the minimum over 8 groups of 8
-// lanes of each group's largest key is at most the 8th-largest key (8
-// distinct keys are >= T), so the top_k <= 8 winners are among the keys >= T
-// -- about 20 of 256 for router logits. Those candidates are compacted into
-// LDS and each is ranked against all of them at once with one 64-bit compare
-// of (key, ~index) per pair; more than 32 candidates take route_rounds.
-// scr: 40 uint2 of LDS private to the wave. Lanes j < top_k leave the j-th
-// selected expert and its gate weight in out_e[j] / out_w[j] (any memory).
-__device__ __forceinline__ void wave_route(const float* __restrict__ logits, uint32_t n,
-                                           uint32_t top_k, uint2* scr, uint32_t* out_e,
-                                           float* out_w) {
-    const uint32_t lane = threadIdx.x & 63u;
-    uint32_t k[4];
-    route_keys(logits, n, k);
-    uint32_t g = max(max(k[0], k[1]), max(k[2], k[3]));
-#pragma unroll
-    for (int i = 0; i < 3; i++) {   // group maxima over lanes 8q .. 8q+7
-        const uint32_t o = __float_as_uint(partner(__uint_as_float(g), 1u << i, lane));
-        g = o > g ? o : g;
-    }
-#pragma unroll
-    for (int i = 3; i < 6; i++) {   // minimum over the 8 groups
-        const uint32_t o = __float_as_uint(partner(__uint_as_float(g), 1u << i, lane));
-        g = o < g ? o : g;
-    }
-    const uint32_t t = (uint32_t)__builtin_amdgcn_readfirstlane((int)g);
-    bool c[4];
-    uint32_t ncand = 0, pos = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        c[i] = k[i] >= t && k[i] != 0u;
-        const uint64_t b = __ballot(c[i]);
-        ncand += __popcll(b);
-        pos += __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
-    }
-    if (ncand <= 32) {
-        // candidates of lower lanes first, then this lane's in index order
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            if (c[i]) scr[pos++] = make_uint2(~(4 * lane + (uint32_t)i), k[i]);
-        __builtin_amdgcn_wave_barrier();
-        if (lane < ncand) {
-            const uint2 me2 = scr[lane];
-            const uint64_t me = ((uint64_t)me2.y << 32) | me2.x;
-            uint32_t rank = 0;
-#pragma unroll
-            for (uint32_t m = 0; m < 32; m++) {
-                const uint2 o2 = scr[m];
-                const uint64_t o = ((uint64_t)o2.y << 32) | o2.x;
-                rank += (m < ncand && o > me) ? 1u : 0u;
-            }
-            if (rank < top_k) scr[32 + rank] = me2;
-        }
-    } else {
-        route_rounds(k, top_k, scr);
-    }
-    __builtin_amdgcn_wave_barrier();
-    uint32_t e = 0;
-    float v = -INFINITY;
-    if (lane < top_k) {
-        const uint2 me = scr[32 + lane];
-        v = key_value(me.y);
-        e = me.y > kKeyNegInf ? ~me.x : 0u;   // only -inf left: qw6 picks index 0
-    }
-    const float mx = key_value(scr[32].y);   // rank 0 holds the maximum
-    const float ex = lane < top_k ? expf(v - mx) : 0.f;
-    float sum = ex;
-    sum += partner(sum, 1, lane);
-    sum += partner(sum, 2, lane);
-    sum += partner(sum, 4, lane);
-    if (lane < top_k) {
-        out_e[lane] = e;
-        out_w[lane] = ex / sum;
-    }
-}
+// ---- routing (wave_route: qw6_dev.h) -----------------------------------------------
 
 __global__ __launch_bounds__(64) void k_route(const float* __restrict__ logits, uint32_t n,
                                               uint32_t top_k, uint32_t* idx, float* w) {
@@ -457,24 +312,6 @@ __global__ __launch_bounds__(64) void k_route(const float* __restrict__ logits, 
 //                  selected expert (the shared one first, it needs no routing);
 //                  row sums meet in LDS and are combined in a fixed order with
 //                  the residual -- no atomics, deterministic.
-
-struct ExpertEnt {            // device expert table entry
-    const uint8_t* p[3];      // gate, up, down
-    int32_t fmt[3];
-    uint32_t rb[3];
-};
-
-// Addressing of one matrix kind (gate / up / down) of the experts: a regular
-// pack (expert e at base + e * stride, one format; the GGUF expert pack of
-// bind_expert_pack, qw6.c:542-597) needs no memory round trip; otherwise the
-// per-expert table entry is loaded.
-struct PackRef {
-    const uint8_t* base;
-    uint64_t stride;
-    int32_t fmt;
-    uint32_t rb;
-    uint32_t regular;
-};
 
 constexpr int kStepsGu = 2;     // row steps per wave, gate/up
 constexpr int kStepsDn = 2;     // row steps per wave, down
@@ -624,11 +461,14 @@ __global__ __launch_bounds__(64) void k_moe_router(MoeArgs a) {
 #pragma unroll
         for (uint32_t i = 0; i < 8; i++)
             if (i < n4) xv[t][i] = ((const float4*)(a.x + (size_t)t * H))[64 * i + lane];
+    // the router row of expert e (or the shared-expert router); none when the
+    // logits are given and this launch only normalises the input
+    const float* wrow = e < a.n_experts ? a.router : a.shared_router;
+    if (wrow && e < a.n_experts) wrow += (size_t)e * H;
     float4 wv[8];
-    const float* wrow = e < a.n_experts ? a.router + (size_t)e * H : a.shared_router;
 #pragma unroll
     for (uint32_t i = 0; i < 8; i++)
-        if (i < n4) wv[i] = ((const float4*)wrow)[64 * i + lane];
+        if (wrow && i < n4) wv[i] = ((const float4*)wrow)[64 * i + lane];
     if (a.norm_w) {
         float4 nw[8];
 #pragma unroll
@@ -662,6 +502,7 @@ __global__ __launch_bounds__(64) void k_moe_router(MoeArgs a) {
             }
         }
     }
+    if (!wrow) return;
 #pragma unroll
     for (int t = 0; t < T; t++) {
         float acc = 0.f;
@@ -964,6 +805,14 @@ __global__ void k_synth_normal(float* dst, uint64_t n, float mean, float sd, uin
 
 }  // namespace
 
+int qw6::qw6_fail(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    const int r = vfail(fmt, ap);
+    va_end(ap);
+    return r;
+}
+
 // ==================================================================================
 // Host side
 // ==================================================================================
@@ -980,6 +829,9 @@ struct qw6_hip_ctx_s {
     SlotTable* slots;
     float* mid;
     uint32_t ws_hidden, ws_inter;
+    // batched (grouped MFMA) workspace, sized for max_tokens
+    PrefillWs pre;
+    uint32_t pre_hidden, pre_inter, pre_experts;
     // per-kernel timing (qw6_hip_profile)
     std::vector<hipEvent_t> prof_ev;
     uint32_t prof_cap, prof_calls;
@@ -1428,6 +1280,44 @@ int ensure_ws(qw6_hip_ctx_t* c, uint32_t hidden, uint32_t inter) {
     return 0;
 }
 
+int ensure_prefill_ws(qw6_hip_ctx_t* c, uint32_t hidden, uint32_t inter, uint32_t n_experts,
+                      uint32_t top_k) {
+    (void)top_k;
+    if (c->pre.mid && c->pre_hidden >= hidden && c->pre_inter >= inter &&
+        c->pre_experts >= n_experts)
+        return 0;
+    const uint32_t T = c->max_tokens, K8 = 8;
+    const size_t E = prefill_entries(T, K8);
+    void* p;
+    PrefillWs& w = c->pre;
+    if (alloc_owned(c, (size_t)T * K8 * 4, &p)) return -1;
+    w.pidx = (uint32_t*)p;
+    if (alloc_owned(c, (size_t)T * K8 * 4, &p)) return -1;
+    w.pw = (float*)p;
+    if (alloc_owned(c, E * 4, &p)) return -1;
+    w.ent_tok = (uint32_t*)p;
+    if (alloc_owned(c, E * 4, &p)) return -1;
+    w.ent_w = (float*)p;
+    if (alloc_owned(c, (size_t)T * K8 * 4, &p)) return -1;
+    w.ent_pos = (uint32_t*)p;
+    if (alloc_owned(c, (size_t)prefill_tiles_max(T, K8, 256) * sizeof(uint4), &p)) return -1;
+    w.tiles = (uint4*)p;
+    if (alloc_owned(c, 16, &p)) return -1;
+    w.n_tiles = (uint32_t*)p;
+    if (alloc_owned(c, (size_t)T * 256 * 4, &p)) return -1;
+    w.logits = (float*)p;
+    if (alloc_owned(c, (size_t)T * hidden * 4, &p)) return -1;
+    w.xn = (float*)p;
+    if (alloc_owned(c, E * inter * 4, &p)) return -1;
+    w.mid = (float*)p;
+    if (alloc_owned(c, E * hidden * 4, &p)) return -1;
+    w.ybuf = (float*)p;
+    c->pre_hidden = hidden;
+    c->pre_inter = inter;
+    c->pre_experts = n_experts;
+    return 0;
+}
+
 // A kernel launch, timed by its own dispatch (hipExtLaunchKernel start/stop
 // events, no extra queue packets) when ev is given.
 template <typename... Args>
@@ -1550,8 +1440,31 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
     if (!E->gu_same || (has_sh && sg.fmt != su.fmt))
         return fail("gate and up of each expert must share a quant type");
     DevGuard g(c->device);
-    if (ensure_ws(c, L->hidden, L->inter)) return -1;
     hipStream_t st = (hipStream_t)stream;
+    // batched tokens: grouped MFMA contraction when every matrix kind has one
+    // supported format (qw6_hip_set_mode: 0 automatic, 1 per-token, 2 grouped)
+    const int fgu = (has_sh && sg.fmt != E->fmt_gu) ? -1 : E->fmt_gu;
+    const int fdn = (has_sh && sd.fmt != E->fmt_dn) ? -1 : E->fmt_dn;
+    const bool grouped_ok = prefill_supports(fgu) && prefill_supports(fdn) &&
+                            L->hidden % 256 == 0 && L->inter % 256 == 0;
+    if (c->mode == 2 && !grouped_ok)
+        return fail("grouped MFMA path needs one Q4_K / Q5_K / Q6_K format per matrix kind");
+    if (grouped_ok && (c->mode == 2 || (c->mode == 0 && n_tok >= kGroupedMinTokens))) {
+        if (ensure_prefill_ws(c, L->hidden, L->inter, E->n, L->top_k)) return -1;
+        PrefillLayer P;
+        memset(&P, 0, sizeof P);
+        P.hidden = L->hidden; P.inter = L->inter; P.n_experts = E->n; P.top_k = L->top_k;
+        P.T = n_tok;
+        P.x = x; P.logits = logits; P.router = logits ? nullptr : L->router;
+        P.shared_router = L->shared_router; P.norm_w = L->norm_w; P.norm_eps = L->norm_eps;
+        P.residual = residual; P.out = out; P.idx_out = idx; P.w_out = w;
+        P.experts = E->dev;
+        for (int k = 0; k < 3; k++) P.pk[k] = E->pk[k];
+        P.fmt_gu = fgu; P.fmt_dn = fdn;
+        P.sg = sg; P.su = su; P.sd = sd;
+        return prefill_forward(P, c->pre, st);
+    }
+    if (ensure_ws(c, L->hidden, L->inter)) return -1;
 
     MoeArgs a;
     memset(&a, 0, sizeof a);
@@ -1579,7 +1492,9 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
     m.lds_b = (size_t)tab_bytes(mgu) + 4 * 2 * kStepsGu * kSlotBytes;
     const uint32_t R_c = kStepsDn * rpsd;
     m.grid_c = (L->hidden + R_c - 1) / R_c;
-    m.router = L->router != nullptr || L->shared_router != nullptr || L->norm_w != nullptr;
+    // the router kernel runs when it has work: the router GEMV (no logits
+    // given), the shared-expert weight, or the input RMSNorm
+    m.router = (!logits && L->router) || L->shared_router != nullptr || L->norm_w != nullptr;
     m.grid_r = E->n + (L->shared_router ? 1u : 0u);
     if (m.lds_b > kLdsBudget) return fail("gate/up tile exceeds the LDS budget");
 

@@ -326,3 +326,17 @@ def test_error_paths(torch_dev, ctx, layers):
     shp[1] = (shp[1][0], shp[1][1], 1024, shp[1][3])
     with pytest.raises(Q.Qw6HipError, match="shape"):
         ctx.experts(L.mats[0], L.mats[1], shp)
+
+
+def test_given_logits_on_a_layer_with_router(torch_dev, ctx, layers):
+    """Router logits passed in for a layer that also has a router (the logits
+    win, the router is not read) on the per-token kernels, T = 1 and 3."""
+    L = layers[("q4k", 11)]
+    for T in (1, 3):
+        lg = S.zipf_logits(81 + T, T)
+        xs = np.stack([cases.token_x(81, 7, t) for t in range(T)])
+        out, idx, _ = run_layer(torch_dev, ctx, L, xs, logits=lg)
+        for t in range(T):
+            (oo, oi, _), _ = oracle_for(L, xs[t], logits=lg[t])
+            assert np.array_equal(idx[t], oi)
+            assert cases.rel_l2(out[t], oo) <= TOL

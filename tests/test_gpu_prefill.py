@@ -1,0 +1,209 @@
+"""The batched (grouped bf16-MFMA) MoE path against the oracle, through the
+C ABI. Bars: expert indices exact for given router logits; outputs rel-L2
+<= 2e-3 per token (the bf16-MFMA bar; the construction -- exact integer codes,
+hi/lo activations, fp32 scales -- lands near 1e-5, which the tighter assert
+on the mean pins). The full T = 512 batch is checked against the per-token
+fp32 kernels of the same library (a size-independent consistency check) and
+on a sample of tokens against the oracle.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import cases
+import oracle as O
+import qw6_amd as Q
+from qw6_amd import synth as S
+
+pytestmark = pytest.mark.gpu
+
+TOL_BF16 = 2e-3
+TOL_MEAN = 1e-4
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "no GPU visible"
+    return torch
+
+
+@pytest.fixture(scope="module")
+def ctx(torch_dev):
+    c = Q.Context(0, max_tokens=512)
+    yield c
+    c.close()
+
+
+@pytest.fixture(scope="module")
+def layer(torch_dev, ctx):
+    from qw6_amd.workload import SynthLayer
+    L = SynthLayer(ctx, 61, 0, "q4k")
+    yield L
+    L.free()
+
+
+def run(torch, ctx, L, xs, logits=None, residual=None, mode=2):
+    T = xs.shape[0]
+    dx = torch.from_numpy(np.ascontiguousarray(xs)).cuda()
+    dout = torch.zeros(T, L.hidden, dtype=torch.float32, device="cuda")
+    didx = torch.zeros(T, L.top_k, dtype=torch.int32, device="cuda")
+    dw = torch.zeros(T, L.top_k, dtype=torch.float32, device="cuda")
+    dl = None if logits is None else torch.from_numpy(np.ascontiguousarray(logits)).cuda()
+    dr = None if residual is None else torch.from_numpy(np.ascontiguousarray(residual)).cuda()
+    ctx.set_mode(mode)
+    try:
+        ctx.moe_forward(L.desc, dx, dout, n_tok=T, logits=dl, residual=dr, idx=didx, w=dw)
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_mode(0)
+    return dout.cpu().numpy(), didx.cpu().numpy(), dw.cpu().numpy()
+
+
+def oracle_tokens(L, xs, lg, tokens, router=None):
+    need = set()
+    for t in tokens:
+        idx, _ = O.moe_route(lg[t], L.top_k)
+        need.update(int(i) for i in idx)
+    ex = [L.expert_host(e) if e in need else None for e in range(L.n_experts)]
+    ol = O.Layer(L.hidden, L.inter, L.n_experts, L.top_k, router, ex, L.shared_host())
+    return {t: O.moe_layer(ol, xs[t], logits=None if router is not None else lg[t], nthreads=8)
+            for t in tokens}
+
+
+def test_grouped_given_logits_vs_oracle(torch_dev, ctx, layer):
+    """T = 64 tokens, Zipf(1.1)-skewed given logits, shared expert, residual."""
+    T = 64
+    lg = S.zipf_logits(61, T)
+    xs = np.stack([cases.token_x(61, 3, t) for t in range(T)])
+    res = np.stack([cases.token_x(62, 3, t) for t in range(T)])
+    say("grouped T=%d" % T)
+    out, idx, w = run(torch_dev, ctx, layer, xs, logits=lg, residual=res)
+    want = oracle_tokens(layer, xs, lg, range(T))
+    rels = []
+    for t in range(T):
+        oo, oi, ow = want[t]
+        assert np.array_equal(idx[t], oi), t
+        assert np.abs(w[t] - ow).max() <= 2e-5
+        rels.append(cases.rel_l2(out[t] - res[t], oo))
+    say("rel-L2 max %.2e mean %.2e" % (max(rels), np.mean(rels)))
+    assert max(rels) <= TOL_BF16
+    assert np.mean(rels) <= TOL_MEAN
+
+
+def test_grouped_router_and_norm_vs_oracle(torch_dev, ctx):
+    """Router GEMV and the fused RMSNorm on the batched path (T = 40)."""
+    torch = torch_dev
+    from qw6_amd.workload import SynthLayer
+    L = SynthLayer(ctx, 71, 0, "q4k")
+    try:
+        T = 40
+        nw = cases.norm_w(71, 0)
+        dnw = torch.from_numpy(nw).cuda()
+        desc = Q.make_layer(L.hidden, L.inter, L.top_k, L.experts, router=L.router,
+                            shared=L.shared, norm_w=dnw, norm_eps=1e-6)
+        xs = np.stack([cases.token_x(71, 4, t) for t in range(T)])
+        dx = torch.from_numpy(xs).cuda()
+        dout = torch.zeros(T, L.hidden, dtype=torch.float32, device="cuda")
+        didx = torch.zeros(T, L.top_k, dtype=torch.int32, device="cuda")
+        ctx.set_mode(2)
+        try:
+            ctx.moe_forward(desc, dx, dout, n_tok=T, idx=didx)
+            torch.cuda.synchronize()
+        finally:
+            ctx.set_mode(0)
+        out, idx = dout.cpu().numpy(), didx.cpu().numpy()
+        router = L.router_host()
+        xn = np.stack([O.rmsnorm(xs[t], nw) for t in range(T)])
+        lg = np.stack([O.matvec(0, router, L.n_experts, L.hidden, xn[t]) for t in range(T)])
+        want = oracle_tokens(L, xn, lg, range(T), router=router)
+        ties, rels = 0, []
+        for t in range(T):
+            oo, oi, _ = want[t]
+            if cases.route_gap(lg[t]) < 1e-4:
+                ties += 1
+                continue
+            assert np.array_equal(idx[t], oi), t
+            rels.append(cases.rel_l2(out[t], oo))
+        assert ties <= 1
+        assert max(rels) <= TOL_BF16 and np.mean(rels) <= TOL_MEAN, (max(rels), np.mean(rels))
+    finally:
+        L.free()
+
+
+def test_grouped_full_batch_vs_per_token_kernels_and_oracle(torch_dev, ctx, layer):
+    """T = 512 (the prefill workload): grouped result vs the fp32 per-token
+    kernels for every token, and vs the oracle on a sample of tokens."""
+    T = 512
+    lg = S.zipf_logits(63, T)
+    xs = np.stack([cases.token_x(63, 5, t) for t in range(T)])
+    g_out, g_idx, _ = run(torch_dev, ctx, layer, xs, logits=lg, mode=2)
+    d_out, d_idx, _ = run(torch_dev, ctx, layer, xs, logits=lg, mode=1)
+    assert np.array_equal(g_idx, d_idx)
+    rels = [cases.rel_l2(g_out[t], d_out[t]) for t in range(T)]
+    say("T=512 grouped vs per-token: max %.2e mean %.2e" % (max(rels), np.mean(rels)))
+    assert max(rels) <= TOL_BF16 and np.mean(rels) <= TOL_MEAN
+    sample = [0, 1, 2, 77, 255, 256, 400, 511]
+    want = oracle_tokens(layer, xs, lg, sample)
+    for t in sample:
+        oo, oi, _ = want[t]
+        assert np.array_equal(g_idx[t], oi)
+        assert cases.rel_l2(g_out[t], oo) <= TOL_BF16
+        assert cases.rel_l2(d_out[t], oo) <= 1e-5
+
+
+def test_grouped_small_batch_vs_golden(torch_dev, ctx):
+    """The 4-token golden fixture (qw6's own layer on Zipf logits, with a
+    residual) through the grouped kernels."""
+    import test_gpu as TG
+    from qw6_amd.workload import SynthLayer
+    L = SynthLayer(ctx, 51, 0, "q4k", router=False)
+    try:
+        lg = S.zipf_logits(51, 4)
+        xs = np.stack([cases.token_x(51, 0, t) for t in range(4)])
+        res = np.stack([cases.token_x(52, 0, t) for t in range(4)])
+        out, idx, _ = run(torch_dev, ctx, L, xs, logits=lg, residual=res)
+        for t in range(4):
+            assert np.array_equal(idx[t], TG.G["prefill_t%d_idx" % t])
+            assert cases.rel_l2(out[t] - res[t], TG.G["prefill_t%d_out" % t]) <= TOL_BF16
+    finally:
+        L.free()
+
+
+def test_grouped_graph_replay(torch_dev, ctx, layer):
+    """The batched kernels captured in a graph, replayed with eager work in
+    between: every replay equals the eager result."""
+    torch = torch_dev
+    T = 96
+    lg = torch.from_numpy(S.zipf_logits(65, T)).cuda()
+    x = torch.from_numpy(np.stack([cases.token_x(65, 6, t) for t in range(T)])).cuda()
+    eager = torch.zeros(T, layer.hidden, dtype=torch.float32, device="cuda")
+    ctx.set_mode(2)
+    try:
+        ctx.moe_forward(layer.desc, x, eager, n_tok=T, logits=lg)
+        torch.cuda.synchronize()
+        out = torch.zeros_like(eager)
+        s = torch.cuda.Stream()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(s):
+            ctx.moe_forward(layer.desc, x, out, n_tok=T, logits=lg, stream=s.cuda_stream)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                ctx.moe_forward(layer.desc, x, out, n_tok=T, logits=lg, stream=s.cuda_stream)
+        for _ in range(3):
+            out.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager)
+            ctx.moe_forward(layer.desc, x, eager, n_tok=T, logits=lg)
+            torch.cuda.synchronize()
+    finally:
+        ctx.set_mode(0)
