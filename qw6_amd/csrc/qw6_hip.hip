@@ -1283,7 +1283,7 @@ int ensure_ws(qw6_hip_ctx_t* c, uint32_t hidden, uint32_t inter) {
 int ensure_prefill_ws(qw6_hip_ctx_t* c, uint32_t hidden, uint32_t inter, uint32_t n_experts,
                       uint32_t top_k) {
     (void)top_k;
-    if (c->pre.mid && c->pre_hidden >= hidden && c->pre_inter >= inter &&
+    if (c->pre.ybuf && c->pre_hidden >= hidden && c->pre_inter >= inter &&
         c->pre_experts >= n_experts)
         return 0;
     const uint32_t T = c->max_tokens, K8 = 8;
@@ -1308,8 +1308,18 @@ int ensure_prefill_ws(qw6_hip_ctx_t* c, uint32_t hidden, uint32_t inter, uint32_
     w.logits = (float*)p;
     if (alloc_owned(c, (size_t)T * hidden * 4, &p)) return -1;
     w.xn = (float*)p;
-    if (alloc_owned(c, E * inter * 4, &p)) return -1;
-    w.mid = (float*)p;
+    if (alloc_owned(c, (size_t)T * hidden * 2, &p)) return -1;
+    w.xh = (uint16_t*)p;
+    if (alloc_owned(c, (size_t)T * hidden * 2, &p)) return -1;
+    w.xl = (uint16_t*)p;
+    if (alloc_owned(c, E * inter * 2, &p)) return -1;
+    w.mid_h = (uint16_t*)p;
+    if (alloc_owned(c, E * inter * 2, &p)) return -1;
+    w.mid_l = (uint16_t*)p;
+    if (alloc_owned(c, (size_t)T * (hidden / 32) * 3 * 2, &p)) return -1;
+    w.xs3 = (uint16_t*)p;
+    if (alloc_owned(c, E * (inter / 32) * 3 * 2, &p)) return -1;
+    w.ms3 = (uint16_t*)p;
     if (alloc_owned(c, E * hidden * 4, &p)) return -1;
     w.ybuf = (float*)p;
     c->pre_hidden = hidden;

@@ -46,7 +46,12 @@ struct PrefillWs {
     uint32_t* n_tiles;   // [1]
     float* logits;       // [T][n_experts]
     float* xn;           // [T][hidden] (RMSNorm of the input)
-    float* mid;          // [E][inter]
+    uint16_t* xh;        // [T][hidden] bf16 of the input
+    uint16_t* xl;        // [T][hidden] bf16 of the input's rounding residue
+    uint16_t* mid_h;     // [E][inter] bf16 of silu(gate) * up
+    uint16_t* mid_l;     // [E][inter] bf16 of its rounding residue
+    uint16_t* xs3;       // [T][hidden / 256][3][8] input sums per 32 columns, 3 bf16 parts
+    uint16_t* ms3;       // [E][inter / 256][3][8] the same for mid
     float* ybuf;         // [E][hidden]
 };
 

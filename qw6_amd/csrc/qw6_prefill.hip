@@ -31,6 +31,7 @@
 // Q6_K under qw6's even-scale rule, qw6.c:1567-1570).
 
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
 
 #include "qw6_dev.h"
@@ -48,6 +49,39 @@ constexpr uint32_t kRaw = 128;    // weight rows staged per workgroup and block
 
 __host__ __device__ constexpr uint32_t raw_chunks(int f) {   // 16-B chunks per staged row block
     return (fmt_block_bytes(f) + 14 + 15) / 16;
+}
+
+// ---- bf16 operand preparation -----------------------------------------------------
+
+__device__ __forceinline__ uint32_t bfb(__bf16 b) { return (uint32_t)__builtin_bit_cast(uint16_t, b); }
+
+// Eight floats -> bf16 hi and lo parts (hi = bf16(x), lo = bf16(x - hi)), packed
+// in MFMA operand order; returns sum(hi + lo) in fp32.
+__device__ __forceinline__ float split8(const float (&v)[8], uint4& h, uint4& l) {
+    uint32_t hw[4], lw[4];
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float x0 = v[2 * i], x1 = v[2 * i + 1];
+        const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+        const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
+        sum += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
+        hw[i] = bfb(h0) | (bfb(h1) << 16);
+        lw[i] = bfb(l0) | (bfb(l1) << 16);
+    }
+    h = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    l = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    return sum;
+}
+
+// A sub-block sum as three bf16 parts (hi, mid, lo), exact to fp32 precision.
+__device__ __forceinline__ void split3(float x, uint16_t (&p)[3]) {
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+        const __bf16 b = (__bf16)x;
+        p[i] = __builtin_bit_cast(uint16_t, b);
+        x -= (float)b;
+    }
 }
 
 // ---- routing -----------------------------------------------------------------------
@@ -78,6 +112,27 @@ __global__ __launch_bounds__(64) void k_pre_route(PrefillLayer L, PrefillWs ws,
         const uint32_t e = L.T * L.top_k + t;
         ws.ent_tok[e] = t;
         ws.ent_w[e] = sw;
+    }
+    // the token's bf16 hi / lo operands and its 32-column sums (lanes 4k .. 4k+3
+    // hold one 32-column sub-block, 8 columns each)
+    const float* xr = xin + (size_t)t * L.hidden;
+    for (uint32_t c = lane; c < L.hidden / 8; c += 64) {
+        float v[8];
+        const float4 a = ((const float4*)xr)[2 * c], b = ((const float4*)xr)[2 * c + 1];
+        v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        uint4 h, l;
+        float sum = split8(v, h, l);
+        ((uint4*)(ws.xh + (size_t)t * L.hidden))[c] = h;
+        ((uint4*)(ws.xl + (size_t)t * L.hidden))[c] = l;
+        sum += partner(sum, 1, lane);
+        sum += partner(sum, 2, lane);
+        if ((c & 3u) == 0) {
+            const uint32_t sb = c >> 2;   // sub-block: block sb / 8, slot sb % 8
+            uint16_t p3[3];
+            split3(sum, p3);
+            uint16_t* dst = ws.xs3 + ((size_t)t * (L.hidden / 256) + sb / 8) * 24 + sb % 8;
+            dst[0] = p3[0]; dst[8] = p3[1]; dst[16] = p3[2];
+        }
     }
 }
 
@@ -172,9 +227,10 @@ template <int F>
 __device__ __forceinline__ void decode_btile(const uint32_t* s, uint32_t R, uint32_t q,
                                              BTile& bt) {
     if (F == F_Q4K || F == F_Q5K) {
-        bt.d = h2f(lds16(s, R));
-        bt.dmin = h2f(lds16(s, R + 2));
-        const uint32_t A = lds32(s, R + 4), B = lds32(s, R + 8), C = lds32(s, R + 12);
+        const uint4 hd = *(const uint4*)(s + (R >> 2));
+        bt.d = h2f(hd.x & 0xffffu);
+        bt.dmin = h2f(hd.x >> 16);
+        const uint32_t A = hd.y, B = hd.z, C = hd.w;
         uint32_t sc[8], mn[8];
 #pragma unroll
         for (int j = 0; j < 4; j++) {   // qw6_get_scale_min_k4 (qw6.c:1480-1490)
@@ -185,13 +241,17 @@ __device__ __forceinline__ void decode_btile(const uint32_t* s, uint32_t R, uint
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) bt.dsc[j] = bt.d * (float)sc[j];
+        // Q4_K / Q5_K blocks are 144 / 176 B: 16-byte aligned, plain 8-byte reads
         const uint32_t qo = F == F_Q4K ? 16u : 48u;   // qs offset
         uint32_t h0 = 0, h1 = 0;
-        if (F == F_Q5K) { h0 = lds32(s, R + 16 + 8 * q); h1 = lds32(s, R + 20 + 8 * q); }
+        if (F == F_Q5K) {
+            const uint2 hq = *(const uint2*)(s + ((R + 16 + 8 * q) >> 2));
+            h0 = hq.x; h1 = hq.y;
+        }
 #pragma unroll
         for (int g = 0; g < 4; g++) {
-            const uint32_t w0 = lds32(s, R + qo + 32 * g + 8 * q);
-            const uint32_t w1 = lds32(s, R + qo + 32 * g + 8 * q + 4);
+            const uint2 wq = *(const uint2*)(s + ((R + qo + 32 * g + 8 * q) >> 2));
+            const uint32_t w0 = wq.x, w1 = wq.y;
             uint32_t l0 = w0 & 0x0f0f0f0fu, l1 = w1 & 0x0f0f0f0fu;
             uint32_t u0 = (w0 >> 4) & 0x0f0f0f0fu, u1 = (w1 >> 4) & 0x0f0f0f0fu;
             if (F == F_Q5K) {
@@ -247,11 +307,14 @@ __device__ __forceinline__ void decode_btile(const uint32_t* s, uint32_t R, uint
     }
 }
 
-// Shared memory of k_pre_gemm.
+// Shared memory of k_pre_gemm: the A operands of the tile for one
+// 256-column block, operand-major so both the direct-to-LDS staging (64 lanes
+// write 1 KB contiguously) and the operand reads (lane l reads 16 B at l) are
+// conflict-free; then the raw weight block bytes of the workgroup's rows.
 struct GemmLds {
-    uint4 a[2][8][2][64];        // A operands [row group][sub-block][hi, lo][lane]
-    float sx[kPM][8];            // sum over each sub-block of (hi + lo)
-    uint32_t raw[1];             // kRaw rows x raw_chunks(F) x 16 B, staged block bytes
+    uint4 a[2][2][8][64];        // [hi, lo][row group][sub-block][lane]
+    float part[4][kPM];          // epilogue: per-wave 16-column sums of mid
+    uint32_t raw[1];             // kRaw rows x raw_chunks(F) x 16 B
 };
 
 // MODE 0: gate/up of 64 intermediate rows; MODE 1: down of 128 hidden rows.
@@ -261,8 +324,9 @@ template <int MODE, int F>
 __global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     GemmLds& S = *(GemmLds*)smem;
-    const uint4 tile = ws.tiles[blockIdx.x < *ws.n_tiles ? blockIdx.x : 0];
-    if (blockIdx.x >= *ws.n_tiles) return;
+    const uint32_t ntile = *ws.n_tiles;
+    if (blockIdx.x >= ntile) return;
+    const uint4 tile = ws.tiles[blockIdx.x];
     const uint32_t mid_e = tile.x, ent0 = tile.y, cnt = tile.z;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
     const uint32_t n = lane & 15u, q = lane >> 4;
@@ -271,8 +335,7 @@ __global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws)
     const uint32_t nblk = K / 256;
     constexpr uint32_t NCH = raw_chunks(F);
     constexpr uint32_t bb = fmt_block_bytes(F);
-    const uint32_t rb = (K / 256) * bb;
-    // weight rows of this workgroup: raw row rr -> matrix, row
+    const uint32_t rb = nblk * bb;
     const uint32_t r0 = blockIdx.y * (MODE == 0 ? 64u : 128u);
     const uint8_t* m0;
     const uint8_t* m1 = nullptr;
@@ -289,12 +352,28 @@ __global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws)
         if (MODE == 0) return rr < 64 ? m0 + (size_t)(r0 + rr) * rb : m1 + (size_t)(r0 + rr - 64) * rb;
         return m0 + (size_t)(r0 + rr) * rb;
     };
-    // this lane's two row tiles (raw rows)
     uint32_t rrow[2];
     if (MODE == 0) { rrow[0] = 16 * wave + n; rrow[1] = 64 + 16 * wave + n; }
     else { rrow[0] = 32 * wave + n; rrow[1] = 32 * wave + 16 + n; }
     const uint32_t bias = F == F_Q6K ? 160u : 128u;
     const uint32_t ngrp = (cnt + 15) / 16;   // 16-entry row groups in use
+
+    // activation rows: A staging of wave w covers (hi/lo = w / 2, group w % 2);
+    // lane l stages entry 16 g + l % 16 (clamped into the tile), columns
+    // 8 (l / 16) .. + 8 of each sub-block
+    const uint32_t sg_hl = wave >> 1, sg_g = wave & 1u;
+    const uint32_t sm = min(16 * sg_g + n, cnt - 1);
+    const uint16_t* arow;
+    if (MODE == 0) arow = (sg_hl ? ws.xl : ws.xh) + (size_t)ws.ent_tok[ent0 + sm] * L.hidden;
+    else arow = (sg_hl ? ws.mid_l : ws.mid_h) + (size_t)(ent0 + sm) * L.inter;
+    // sub-block sums: lane (m, q == 0) of group g reads those of entry 16 g + m
+    const uint16_t* srow[2];
+#pragma unroll
+    for (uint32_t g = 0; g < 2; g++) {
+        const uint32_t m = min(16 * g + n, cnt - 1);
+        srow[g] = MODE == 0 ? ws.xs3 + (size_t)ws.ent_tok[ent0 + m] * (L.hidden / 256) * 24
+                            : ws.ms3 + (size_t)(ent0 + m) * (L.inter / 256) * 24;
+    }
 
     f32x4 acc[2][2];
 #pragma unroll
@@ -302,97 +381,45 @@ __global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws)
 #pragma unroll
         for (int r = 0; r < 2; r++) acc[g][r] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // activation rows handled by this thread during staging
-    const uint32_t am = tid >> 3, ac = tid & 7u;
-    const float* arow = nullptr;
-    if (am < cnt) {
-        const uint32_t e = ent0 + am;
-        arow = MODE == 0 ? L.x + (size_t)ws.ent_tok[e] * L.hidden : ws.mid + (size_t)e * L.inter;
-    }
-
     for (uint32_t kb = 0; kb < nblk; kb++) {
-        // stage the raw block bytes of the 128 rows (16-B chunks from the
-        // aligned start of each row block)
+        // raw block bytes of the 128 rows, 16-B chunks from each row block's
+        // aligned start (only chunks that hold bytes of the block)
         for (uint32_t c0 = wave * 64; c0 < kRaw * NCH; c0 += kPWG) {
             const uint32_t c = c0 + lane;
             const uint32_t rr = c / NCH, ch = c % NCH;
             const uint8_t* p = row_ptr(rr) + (size_t)kb * bb;
             const uint32_t off = (uint32_t)((uintptr_t)p & 15u);
-            const uint8_t* pa = p - off + 16 * ch;
-            if (16 * ch < off + bb)   // only chunks holding bytes of this row block
-                __builtin_amdgcn_global_load_lds((glb_void_t*)pa,
+            if (16 * ch < off + bb)
+                __builtin_amdgcn_global_load_lds((glb_void_t*)(p - off + 16 * ch),
                                                  (lds_void_t*)((uint8_t*)S.raw + 16u * c0), 16, 0, 0);
         }
-        // activations: thread (am, ac) converts sub-block ac of entry am
-        if (arow) {
-            const float4* src = (const float4*)(arow + kb * 256 + 32 * ac);
-            float v[32];
+        if (sg_g < ngrp) {
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float4 t4 = src[i];
-                v[4 * i] = t4.x; v[4 * i + 1] = t4.y; v[4 * i + 2] = t4.z; v[4 * i + 3] = t4.w;
-            }
-            float sum = 0.f;
-#pragma unroll
-            for (uint32_t qq = 0; qq < 4; qq++) {
-                uint32_t hw[4], lw[4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float x0 = v[8 * qq + 2 * i], x1 = v[8 * qq + 2 * i + 1];
-                    const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
-                    const float r0f = x0 - (float)h0, r1f = x1 - (float)h1;
-                    const __bf16 l0 = (__bf16)r0f, l1 = (__bf16)r1f;
-                    sum += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
-                    hw[i] = (uint32_t)__builtin_bit_cast(uint16_t, h0) |
-                            ((uint32_t)__builtin_bit_cast(uint16_t, h1) << 16);
-                    lw[i] = (uint32_t)__builtin_bit_cast(uint16_t, l0) |
-                            ((uint32_t)__builtin_bit_cast(uint16_t, l1) << 16);
-                }
-                const uint32_t ln = (am & 15u) + 16u * qq;
-                S.a[am >> 4][ac][0][ln] = u4(hw[0], hw[1], hw[2], hw[3]);
-                S.a[am >> 4][ac][1][ln] = u4(lw[0], lw[1], lw[2], lw[3]);
-            }
-            S.sx[am][ac] = sum;
+            for (uint32_t sb = 0; sb < 8; sb++)
+                __builtin_amdgcn_global_load_lds(
+                    (glb_void_t*)(arow + kb * 256 + 32 * sb + 8 * q),
+                    (lds_void_t*)&S.a[sg_hl][sg_g][sb][0], 16, 0, 0);
         }
+        // sub-block sums of this block (lanes q == 0)
+        uint4 sx3[2][3];
+#pragma unroll
+        for (uint32_t g = 0; g < 2; g++)
+#pragma unroll
+            for (int p3 = 0; p3 < 3; p3++)
+                sx3[g][p3] = (q == 0 && g < ngrp) ? *(const uint4*)(srow[g] + kb * 24 + 8 * p3)
+                                                  : u4(0, 0, 0, 0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        // B operands of this wave's two row tiles
         BTile bt[2];
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             const uint32_t R = rrow[r] * NCH * 16 + ((uintptr_t)(row_ptr(rrow[r]) + (size_t)kb * bb) & 15u);
             decode_btile<F>(S.raw, R, q, bt[r]);
         }
-        // contraction
         for (uint32_t g = 0; g < ngrp; g++) {
-            // A operands of the sub-block sums (k = sub-block, lanes q == 0) in
-            // three bf16 parts: they multiply integer scales whose products
-            // cancel the code bias, so they carry fp32 precision
-            uint4 sx3[3] = {u4(0, 0, 0, 0), u4(0, 0, 0, 0), u4(0, 0, 0, 0)};
-            if (q == 0) {
-                uint32_t w3[3][4];
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    uint32_t h[3][2];
-#pragma unroll
-                    for (int e2 = 0; e2 < 2; e2++) {
-                        float r = S.sx[16 * g + n][2 * i + e2];
-#pragma unroll
-                        for (int p3 = 0; p3 < 3; p3++) {
-                            const __bf16 b = (__bf16)r;
-                            h[p3][e2] = (uint32_t)__builtin_bit_cast(uint16_t, b);
-                            r -= (float)b;
-                        }
-                    }
-#pragma unroll
-                    for (int p3 = 0; p3 < 3; p3++) w3[p3][i] = h[p3][0] | (h[p3][1] << 16);
-                }
-#pragma unroll
-                for (int p3 = 0; p3 < 3; p3++) sx3[p3] = u4(w3[p3][0], w3[p3][1], w3[p3][2], w3[p3][3]);
-            }
 #pragma unroll
             for (int sb = 0; sb < 8; sb++) {
-                const uint4 ah = S.a[g][sb][0][lane], al = S.a[g][sb][1][lane];
+                const uint4 ah = S.a[0][g][sb][lane], al = S.a[1][g][sb][lane];
 #pragma unroll
                 for (int r = 0; r < 2; r++) {
                     f32x4 c = mfma(ah, bt[r].b[sb], f32x4{0.f, 0.f, 0.f, 0.f});
@@ -403,16 +430,16 @@ __global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws)
             }
 #pragma unroll
             for (int r = 0; r < 2; r++) {
-                f32x4 u = mfma(sx3[0], bt[r].bsc, f32x4{0.f, 0.f, 0.f, 0.f});
-                u = mfma(sx3[1], bt[r].bsc, u);
-                u = mfma(sx3[2], bt[r].bsc, u);
+                f32x4 u = mfma(sx3[g][0], bt[r].bsc, f32x4{0.f, 0.f, 0.f, 0.f});
+                u = mfma(sx3[g][1], bt[r].bsc, u);
+                u = mfma(sx3[g][2], bt[r].bsc, u);
                 const float cb = -(float)bias * bt[r].d;
 #pragma unroll
                 for (int j = 0; j < 4; j++) acc[g][r][j] = fmaf(cb, u[j], acc[g][r][j]);
                 if (F != F_Q6K) {
-                    f32x4 v = mfma(sx3[0], bt[r].bmin, f32x4{0.f, 0.f, 0.f, 0.f});
-                    v = mfma(sx3[1], bt[r].bmin, v);
-                    v = mfma(sx3[2], bt[r].bmin, v);
+                    f32x4 v = mfma(sx3[g][0], bt[r].bmin, f32x4{0.f, 0.f, 0.f, 0.f});
+                    v = mfma(sx3[g][1], bt[r].bmin, v);
+                    v = mfma(sx3[g][2], bt[r].bmin, v);
 #pragma unroll
                     for (int j = 0; j < 4; j++) acc[g][r][j] = fmaf(-bt[r].dmin, v[j], acc[g][r][j]);
                 }
@@ -422,18 +449,53 @@ __global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws)
     }
 
     // epilogue: lane holds entries 16 g + 4 q + j of row n of its two tiles
+    if (MODE == 0) {
+        // mid = silu(gate) * up as bf16 hi / lo, plus its 32-column sums: this
+        // wave's 16 columns are half of sub-block (r0 + 16 wave) / 32
+        float part[2][4];
 #pragma unroll
-    for (uint32_t g = 0; g < 2; g++) {
-        if (g >= ngrp) break;
+        for (uint32_t g = 0; g < 2; g++)
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t m = 16 * g + 4 * q + j;
-            if (m >= cnt) continue;
-            const uint32_t e = ent0 + m;
-            if (MODE == 0) {
-                const float gv = acc[g][0][j], uv = acc[g][1][j];
-                ws.mid[(size_t)e * L.inter + r0 + 16 * wave + n] = gv / (1.0f + expf(-gv)) * uv;
-            } else {
+            for (int j = 0; j < 4; j++) {
+                const uint32_t m = 16 * g + 4 * q + j;
+                float hsum = 0.f;
+                if (g < ngrp && m < cnt) {
+                    const float gv = acc[g][0][j], uv = acc[g][1][j];
+                    const float y = gv / (1.0f + expf(-gv)) * uv;
+                    const __bf16 h = (__bf16)y, l = (__bf16)(y - (float)h);
+                    const size_t o = (size_t)(ent0 + m) * L.inter + r0 + 16 * wave + n;
+                    ws.mid_h[o] = __builtin_bit_cast(uint16_t, h);
+                    ws.mid_l[o] = __builtin_bit_cast(uint16_t, l);
+                    hsum = (float)h + (float)l;
+                }
+                part[g][j] = group_sum<16>(hsum);   // over the 16 columns (lanes n)
+            }
+        if (n == 0) {
+#pragma unroll
+            for (uint32_t g = 0; g < 2; g++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) S.part[wave][16 * g + 4 * q + j] = part[g][j];
+        }
+        __syncthreads();
+        if (tid < 2 * kPM) {   // (sub-block half h of the group, entry m)
+            const uint32_t hh = tid / kPM, m = tid % kPM;
+            if (m < cnt) {
+                uint16_t p3[3];
+                split3(S.part[2 * hh][m] + S.part[2 * hh + 1][m], p3);
+                const uint32_t sbg = (r0 + 32 * hh) / 32;   // sub-block index in the row
+                uint16_t* dst = ws.ms3 + ((size_t)(ent0 + m) * (L.inter / 256) + sbg / 8) * 24 + sbg % 8;
+                dst[0] = p3[0]; dst[8] = p3[1]; dst[16] = p3[2];
+            }
+        }
+    } else {
+#pragma unroll
+        for (uint32_t g = 0; g < 2; g++) {
+            if (g >= ngrp) break;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t m = 16 * g + 4 * q + j;
+                if (m >= cnt) continue;
+                const uint32_t e = ent0 + m;
                 const float w = ws.ent_w[e];
                 ws.ybuf[(size_t)e * L.hidden + r0 + 32 * wave + n] = w * acc[g][0][j];
                 ws.ybuf[(size_t)e * L.hidden + r0 + 32 * wave + 16 + n] = w * acc[g][1][j];
@@ -452,14 +514,24 @@ __global__ __launch_bounds__(256) void k_pre_combine(PrefillLayer L, PrefillWs w
     for (uint32_t k = 0; k < 8; k++) pos[k] = k < L.top_k ? ws.ent_pos[(size_t)t * L.top_k + k] : 0u;
     const bool sh = L.sg.p != nullptr;
     const uint32_t se = L.T * L.top_k + t;
-    for (uint32_t i = threadIdx.x; i < L.hidden; i += blockDim.x) {
-        float v = 0.f;
+    const uint32_t n4 = L.hidden / 4;
+    for (uint32_t i = blockIdx.y * 256 + threadIdx.x; i < n4; i += 256 * gridDim.y) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
         for (uint32_t k = 0; k < 8; k++)
-            if (k < L.top_k) v += ws.ybuf[(size_t)pos[k] * L.hidden + i];
-        if (sh) v += ws.ybuf[(size_t)se * L.hidden + i];
-        if (L.residual) v += L.residual[(size_t)t * L.hidden + i];
-        L.out[(size_t)t * L.hidden + i] = v;
+            if (k < L.top_k) {
+                const float4 y = ((const float4*)(ws.ybuf + (size_t)pos[k] * L.hidden))[i];
+                v.x += y.x; v.y += y.y; v.z += y.z; v.w += y.w;
+            }
+        if (sh) {
+            const float4 y = ((const float4*)(ws.ybuf + (size_t)se * L.hidden))[i];
+            v.x += y.x; v.y += y.y; v.z += y.z; v.w += y.w;
+        }
+        if (L.residual) {
+            const float4 r = ((const float4*)(L.residual + (size_t)t * L.hidden))[i];
+            v.x += r.x; v.y += r.y; v.z += r.z; v.w += r.w;
+        }
+        ((float4*)(L.out + (size_t)t * L.hidden))[i] = v;
     }
 }
 
@@ -505,7 +577,7 @@ __global__ __launch_bounds__(64) void k_pre_router(const float* __restrict__ rou
 template <int MODE>
 int launch_gemm(int f, const PrefillLayer& L, const PrefillWs& ws, uint32_t grid_x,
                 uint32_t grid_y, hipStream_t st) {
-    const size_t lds = sizeof(GemmLds) - 4 + (size_t)kRaw * raw_chunks(f) * 16;
+    const size_t lds = offsetof(GemmLds, raw) + (size_t)kRaw * raw_chunks(f) * 16;
     switch (f) {
     case F_Q4K: k_pre_gemm<MODE, F_Q4K><<<dim3(grid_x, grid_y), kPWG, lds, st>>>(L, ws); break;
     case F_Q5K: k_pre_gemm<MODE, F_Q5K><<<dim3(grid_x, grid_y), kPWG, lds, st>>>(L, ws); break;
@@ -552,7 +624,7 @@ int prefill_forward(const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) 
     const uint32_t nt = prefill_tiles_max(L.T, L.top_k, L.n_experts);
     if (launch_gemm<0>(L.fmt_gu, Lx, ws, nt, L.inter / 64, st)) return -1;
     if (launch_gemm<1>(L.fmt_dn, Lx, ws, nt, L.hidden / 128, st)) return -1;
-    k_pre_combine<<<L.T, 256, 0, st>>>(Lx, ws);
+    k_pre_combine<<<dim3(L.T, (L.hidden / 4 + 255) / 256), 256, 0, st>>>(Lx, ws);
     e = hipGetLastError();
     if (e != hipSuccess) return qw6_fail("batched combine launch: %s", hipGetErrorString(e));
     return 0;
