@@ -1,32 +1,51 @@
 #!/usr/bin/env python3
-"""Benchmark of the MI355X MoE FFN decode path (one GPU).
+"""Benchmark of the MI355X routed-expert MoE FFN path (one GPU).
 
-Workload: one MoE FFN decode step, batch 1, hidden 2048, 256 experts top-8,
-expert intermediate 512, Q4_K gate/up + Q6_K down, F32 router [256 x 2048],
-one shared expert of the same shapes; synthetic seeded weights resident in
-HBM. A step is one token through one MoE layer (router GEMV, softmax top-8,
-8 experts + shared expert gate/up/SiLU/down, gate-weighted combine). Steps
-cycle through a pool of independently seeded layer instances (default 16 x
-~526 MB) and inputs, so the 256 MB Infinity Cache cannot serve repeats.
+Headline workload (`value`): one MoE FFN decode step, batch 1, hidden 2048,
+256 experts top-8, expert intermediate 512, Q4_K gate/up + Q6_K down, F32
+router [256 x 2048], one shared expert of the same shapes; synthetic seeded
+weights resident in HBM. A step is one token through one MoE layer (router
+GEMV, softmax top-8, 8 experts + shared expert gate/up/SiLU/down,
+gate-weighted combine). Steps cycle through a pool of independently seeded
+layers (default 16 x ~522 MB) and inputs, so the 256 MB Infinity Cache cannot
+serve repeats. `value` is microseconds per MoE layer of the HIP-graph-replayed
+kernels, inputs already in HBM.
 
-Prints one JSON line. `value` is microseconds per MoE layer (lower is
-better) of the HIP-graph-replayed decode kernels; `hbm_GBps` is the step's
-algorithmic bytes over that time. `roofline` is for the dominant kernel
-(gate/up/SiLU over the 8 selected experts), timed with HIP events on the
-launch stream. `cpu_baseline` times qw6's own CPU path (compiled from the
-reference when available, else the repository's bit-identical C restatement)
-on a bounded sample of the same workload on this host.
+`roofline` is for the dominant kernel (gate/up/SiLU over the 8 selected
+experts + shared): algorithmic bytes per launch over its average duration,
+measured with dispatch-timestamped HIP events on the launch stream.
+`traffic` is the HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE
+counter runs, scaled by what the counters read for a copy kernel of known
+size (read from the committed summary; null when absent).
+
+`cpu_baseline` times qw6's own CPU path (compiled from the reference where
+available, else the repository's bit-identical C restatement) on a bounded
+sample of the same workload on this host, single thread as qw6 runs it.
+
+`secondary` (with --workload all, the default) adds:
+  iq2m_decode   the same layer with IQ2_XXS gate/up and IQ3_S / IQ2_S down;
+  stack         40 such layers, h <- h + MoE_l(RMSNorm(h, w_l)), 128 single-
+                token steps: tokens/s and aggregate GB/s;
+  prefill_T512  512 tokens with Zipf(1.1)-skewed router logits through the
+                grouped bf16-MFMA kernels, Q4_K / Q6_K experts: us/layer,
+                TFLOP/s, MFMA fraction, HBM GB/s;
+  mtp_T2        two tokens (MTP draft verification) with the router GEMV.
 """
 from __future__ import annotations
 
 import argparse
+import csv
+import glob
 import json
 import os
 import sys
 import time
 
+HERE = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 HIDDEN, INTER, N_EXPERTS, TOP_K = 2048, 512, 256, 8
+TRAFFIC_FILE = os.path.join(HERE, "profiles", "moe_gate_up_q4k_decode_traffic.json")
 
 
 def parse():
@@ -35,9 +54,19 @@ def parse():
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--pool", type=int, default=16)
-    ap.add_argument("--mix", default="q4k", choices=["q4k", "iq2m"])
+    ap.add_argument("--workload", default="all",
+                    choices=["all", "q4k", "iq2m", "stack", "prefill"])
+    ap.add_argument("--stack-steps", type=int, default=128)
+    ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="eager launches only (for counter collection)")
+    ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
+                    help="first run a device copy of MIB MiB 4 times (counter calibration)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="turn two rocprofv3 --pmc csv outputs into the traffic summary")
+    ap.add_argument("--command", default="", help="command line recorded in the summary")
     return ap.parse_args()
 
 
@@ -45,10 +74,113 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+# ---- counter summaries -----------------------------------------------------------
+
+def _pmc_rows(d):
+    files = glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit("no counter_collection.csv under %s" % d)
+    rows = []
+    for f in files:
+        with open(f) as fh:
+            rows.extend(csv.DictReader(fh))
+    return rows
+
+
+def _per_kernel(rows, counter):
+    """Mean counter value per dispatch of each kernel name (KiB for *_SIZE)."""
+    acc = {}
+    for r in rows:
+        if r.get("Counter_Name") != counter:
+            continue
+        name = r["Kernel_Name"]
+        disp = r.get("Dispatch_Id") or r.get("Correlation_Id")
+        acc.setdefault(name, {}).setdefault(disp, 0.0)
+        acc[name][disp] += float(r["Counter_Value"])
+    return {k: (sum(v.values()) / len(v), len(v)) for k, v in acc.items()}
+
+
+def summarize_pmc(fetch_dir, write_dir, calib_mib, command):
+    f = _per_kernel(_pmc_rows(fetch_dir), "FETCH_SIZE")
+    w = _per_kernel(_pmc_rows(write_dir), "WRITE_SIZE")
+    nbytes = calib_mib * 1024 * 1024
+
+    def pick(d, key):
+        ks = [k for k in d if key in k]
+        if not ks:
+            raise SystemExit("kernel %s not in counters: %s" % (key, list(d)))
+        return max(ks, key=lambda k: d[k][1])
+
+    ck_f = pick(f, "elementwise")
+    ck_w = pick(w, "elementwise")
+    fac_f = nbytes / (f[ck_f][0] * 1024.0)
+    fac_w = nbytes / (w[ck_w][0] * 1024.0)
+    gu_f = pick(f, "k_moe_gate_up")
+    gu_w = pick(w, "k_moe_gate_up")
+    fetch = f[gu_f][0] * 1024.0 * fac_f
+    write = w[gu_w][0] * 1024.0 * fac_w
+    out = {
+        "kernel": "k_moe_gate_up",
+        "workload": "decode layer, batch 1, Q4_K gate/up + Q6_K down (pool of 16 layers)",
+        "fetch_bytes_per_launch": round(fetch),
+        "write_bytes_per_launch": round(write),
+        "traffic_bytes_per_launch": round(fetch + write),
+        "dispatches": [f[gu_f][1], w[gu_w][1]],
+        "copy_kernel": {"bytes": nbytes, "fetch_KiB": f[ck_f][0], "write_KiB": w[ck_w][0],
+                        "fetch_factor": fac_f, "write_factor": fac_w},
+        "other_kernels_KiB": {k: [round(f[k][0], 1), round(w.get(k, (0.0, 0))[0], 1)]
+                              for k in f if k not in (gu_f, ck_f)},
+        "command": command,
+    }
+    print(json.dumps(out, indent=1))
+
+
+# ---- shared helpers ---------------------------------------------------------------
+
+def algorithmic_bytes(pool, sel, hidden=HIDDEN, inter=INTER):
+    """Mean bytes per decode layer step split into router / gate_up / down from
+    the experts each step actually selected (sel[j] for pool layer j)."""
+    import numpy as np
+    from qw6_amd import synth as S
+    L0 = pool[0]
+    sh_gu = sum(S.row_bytes(m[1], m[3]) * m[2] for m in L0.shared[:2])
+    sh_dn = S.row_bytes(L0.shared[2][1], L0.shared[2][3]) * L0.shared[2][2]
+    r_b = N_EXPERTS * hidden * 4 + hidden * 4 + N_EXPERTS * 4
+    gu, dn = [], []
+    for j, L in enumerate(pool):
+        gub = sum(2 * S.row_bytes(L.quants[int(e)][0], hidden) * inter for e in sel[j])
+        dnb = sum(S.row_bytes(L.quants[int(e)][2], inter) * hidden for e in sel[j])
+        gu.append(gub + sh_gu + hidden * 4 + N_EXPERTS * 4 + (TOP_K + 1) * inter * 4)
+        dn.append(dnb + sh_dn + (TOP_K + 1) * inter * 4 + hidden * 4)
+    gu_b, d_b = float(np.mean(gu)), float(np.mean(dn))
+    step_b = r_b + gu_b + d_b - N_EXPERTS * 4 - (TOP_K + 1) * inter * 4
+    return r_b, gu_b, d_b, step_b
+
+
+def graph_time(torch, fn, reps):
+    """Seconds per replay of fn() captured as one HIP graph."""
+    g = torch.cuda.CUDAGraph()
+    s2 = torch.cuda.Stream()
+    with torch.cuda.stream(s2):
+        fn(s2.cuda_stream)                       # warm (first-use allocations)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s2):
+            fn(s2.cuda_stream)
+    torch.cuda.synchronize()
+    for _ in range(2):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / reps, g
+
+
 def cpu_baseline(L, xs_host, budget_s):
     """qw6's CPU path on a bounded sample: tokens through pool layer 0."""
     import numpy as np
-    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    sys.path.insert(0, HERE)
     import oracle as O
     kind = "reference" if O.ref() is not None else "port"
     router = L.router_host()
@@ -76,11 +208,194 @@ def cpu_baseline(L, xs_host, budget_s):
                       "selected experts copied to host; single thread as qw6" % len(times)}
 
 
+# ---- workloads --------------------------------------------------------------------
+
+def bench_decode(torch, Q, S, ctx, pool, X, out, idx, args, profile=True):
+    P = len(pool)
+
+    def step(k, sp):
+        j = k % P
+        ctx.moe_forward(pool[j].desc, X[j], out[j], n_tok=1, idx=idx[j], stream=sp)
+
+    sp = torch.cuda.current_stream().cuda_stream
+    for k in range(args.warmup):
+        step(k, sp)
+    torch.cuda.synchronize()
+    r_b, gu_b, d_b, step_b = algorithmic_bytes(pool, idx.cpu().numpy())
+
+    K = args.steps
+    t0 = time.perf_counter()
+    for k in range(K):
+        step(k, sp)
+    torch.cuda.synchronize()
+    eager_us = 1e6 * (time.perf_counter() - t0) / K
+    if args.no_graph:
+        us_layer, steps = eager_us, K
+    else:
+        reps = max(1, K // P)
+        sec, _ = graph_time(torch, lambda s: [step(j, s) for j in range(P)], reps)
+        us_layer, steps = 1e6 * sec / P, reps * P
+    res = {"us_per_layer": round(us_layer, 3), "eager_us_per_layer": round(eager_us, 3),
+           "steps": steps, "bytes_per_step": int(step_b),
+           "hbm_GBps": round(step_b / us_layer / 1e3, 1),
+           "hbm_frac": round(step_b / us_layer / 1e3 / HBM_PEAK_GBPS, 4)}
+    if profile:
+        # per-kernel durations from each kernel's own dispatch timestamps (HIP
+        # events recorded by hipExtLaunchKernel on the launch stream)
+        nprof = min(K, 256)
+        ctx.profile(nprof)
+        for k in range(nprof):
+            step(k, sp)
+        ms, calls = ctx.profile_read()
+        ctx.profile(0)
+        kus = [1e3 * m / calls for m in ms]
+        res["kernels"] = {
+            "k_moe_router": {"us": round(kus[0], 3), "bytes": int(r_b),
+                             "GBps": round(r_b / kus[0] / 1e3, 1)},
+            "k_moe_gate_up": {"us": round(kus[1], 3), "bytes": int(gu_b),
+                              "GBps": round(gu_b / kus[1] / 1e3, 1)},
+            "k_moe_down": {"us": round(kus[2], 3), "bytes": int(d_b),
+                           "GBps": round(d_b / kus[2] / 1e3, 1)},
+        }
+        res["profiled_calls"] = calls
+    return res
+
+
+def bench_stack(torch, Q, S, ctx, args):
+    """40 IQ2_M-mix layers, h <- h + MoE_l(RMSNorm(h, w_l)), single-token steps."""
+    from qw6_amd.workload import SynthLayer
+    NL, NS = 40, args.stack_steps
+    log("stack: building %d layers" % NL)
+    layers = [SynthLayer(ctx, 3000 + l, l, "iq2m") for l in range(NL)]
+    nw = torch.empty(NL, HIDDEN, dtype=torch.float32, device="cuda")
+    descs = []
+    for l, L in enumerate(layers):
+        Q.synth_normal(nw[l], HIDDEN, 0.1, 3000, S.stream_id(l, S.K_NORM), mean=1.0)
+        d = Q.MoeLayer.from_buffer_copy(L.desc)
+        d.norm_w, d.norm_eps = nw[l].data_ptr(), 1e-6
+        descs.append(d)
+    X = torch.empty(NS, HIDDEN, dtype=torch.float32, device="cuda")
+    for s in range(NS):
+        Q.synth_normal(X[s], HIDDEN, 1.0, 3001, S.stream_id(s, S.K_X))
+    h = torch.empty(1, HIDDEN, dtype=torch.float32, device="cuda")
+    idx = torch.zeros(NL, TOP_K, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+
+    def one_step(sp):
+        for l in range(NL):
+            ctx.moe_forward(descs[l], h, h, n_tok=1, residual=h, idx=idx[l], stream=sp)
+
+    # the step is captured once; each token's input is copied in before its replay
+    _, g = graph_time(torch, one_step, 1)
+    for s in range(4):
+        h.copy_(X[s])
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(NS):
+        h.copy_(X[s])
+        g.replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    r_b, gu_b, d_b, step_b = algorithmic_bytes(layers, idx.cpu().numpy())
+    tok_bytes = step_b * NL
+    res = {"layers": NL, "steps": NS, "tokens_per_s": round(NS / wall, 1),
+           "us_per_token": round(1e6 * wall / NS, 2),
+           "us_per_layer": round(1e6 * wall / NS / NL, 3),
+           "bytes_per_token": int(tok_bytes),
+           "hbm_GBps": round(tok_bytes * NS / wall / 1e9, 1),
+           "resident_GB": round(sum(sum(p.numel() for p in L.packs) for L in layers) / 1e9, 2),
+           "workload": "40 layers IQ2_XXS gate/up + IQ3_S/IQ2_S down, F32 router, shared "
+                       "expert, RMSNorm (eps 1e-6) fused before each layer, residual in "
+                       "place; 128 single-token steps with fresh inputs"}
+    for L in layers:
+        L.free()
+    return res
+
+
+def bench_prefill(torch, Q, S, ctx, pool, args):
+    """T tokens with Zipf-skewed logits through the grouped MFMA kernels, plus the
+    T=2 MTP case through the per-token kernels with the router GEMV."""
+    import numpy as np
+    T = args.prefill_tokens
+    P = min(2, len(pool))
+    lg_h = [S.zipf_logits(4000 + j, T) for j in range(P)]
+    lg = [torch.from_numpy(a).cuda() for a in lg_h]
+    X = torch.empty(P, T, HIDDEN, dtype=torch.float32, device="cuda")
+    for j in range(P):
+        Q.synth_normal(X[j], T * HIDDEN, 1.0, 4001, S.stream_id(j, S.K_X))
+    out = torch.empty(P, T, HIDDEN, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ctx.set_mode(2)
+    try:
+        def fwd(sp):
+            for j in range(P):
+                ctx.moe_forward(pool[j].desc, X[j], out[j], n_tok=T, logits=lg[j], stream=sp)
+        fwd(torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        reps = 10
+        sec, _ = graph_time(torch, fwd, reps)
+    finally:
+        ctx.set_mode(0)
+    us = 1e6 * sec / P
+    flops, byts = [], []
+    L0 = pool[0]
+    for j in range(P):
+        top = np.argsort(-lg_h[j], axis=1, kind="stable")[:, :TOP_K]
+        used = np.unique(top)
+        n_ent = T * TOP_K + T
+        flops.append(2.0 * n_ent * 3 * HIDDEN * INTER)
+        byts.append(sum(pool[j].expert_bytes(int(e)) for e in used) + L0.shared_bytes()
+                    + 2 * T * HIDDEN * 4 + T * N_EXPERTS * 4)
+    fl, by = float(np.mean(flops)), float(np.mean(byts))
+    tf = fl / (us * 1e-6) / 1e12
+    ai = fl / by
+    roof = min(MFMA_BF16_PEAK_TFLOPS, ai * HBM_PEAK_GBPS / 1e3)
+    res = {"tokens": T, "us_per_layer": round(us, 2), "TFLOPs": round(tf, 2),
+           "mfma_frac": round(tf / MFMA_BF16_PEAK_TFLOPS, 4),
+           "roofline_TFLOPs": round(roof, 1), "roofline_frac": round(tf / roof, 4),
+           "flops": int(fl), "bytes": int(by), "hbm_GBps": round(by / us / 1e3, 1),
+           "tokens_per_s": round(T / (us * 1e-6), 1),
+           "workload": "T=%d, hidden 2048, 256 experts top-8 + shared, Q4_K gate/up, Q6_K "
+                       "down; router logits given, Zipf(1.1)-skewed (Gumbel-top-k)" % T}
+
+    # T = 2 (MTP draft verification): router GEMV + per-token kernels
+    X2 = torch.empty(len(pool), 2, HIDDEN, dtype=torch.float32, device="cuda")
+    for j in range(len(pool)):
+        Q.synth_normal(X2[j], 2 * HIDDEN, 1.0, 4002, S.stream_id(j, S.K_X))
+    o2 = torch.empty_like(X2)
+    i2 = torch.zeros(len(pool), 2, TOP_K, dtype=torch.int32, device="cuda")
+
+    def fwd2(sp):
+        for j in range(len(pool)):
+            ctx.moe_forward(pool[j].desc, X2[j], o2[j], n_tok=2, idx=i2[j], stream=sp)
+    sec2, _ = graph_time(torch, fwd2, max(1, args.steps // len(pool)))
+    us2 = 1e6 * sec2 / len(pool)
+    sel = i2.cpu().numpy()
+    b2 = []
+    for j, L in enumerate(pool):
+        used = np.unique(sel[j])
+        b2.append(sum(L.expert_bytes(int(e)) for e in used) + L.shared_bytes()
+                  + N_EXPERTS * HIDDEN * 4 + 4 * HIDDEN * 4)
+    b2m = float(np.mean(b2))
+    res_t2 = {"tokens": 2, "us_per_layer": round(us2, 3), "bytes": int(b2m),
+              "hbm_GBps": round(b2m / us2 / 1e3, 1),
+              "distinct_experts_mean": round(float(np.mean([len(np.unique(s)) for s in sel])), 2),
+              "workload": "T=2 through the per-token fp32 kernels with the router GEMV, "
+                          "Q4_K/Q6_K layer pool"}
+    return res, res_t2
+
+
 def main():
     args = parse()
+    if args.summarize_pmc:
+        summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.calib_copy or 512,
+                      args.command)
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU only: the MoE FFN path is benchmarked on a single "
-              "MI355X (multi-GPU sharding is described in DESIGN.md, not run).", file=sys.stderr)
+              "MI355X; --gpus %d is not run (sharding is a design note, not a benchmark)."
+              % args.gpus, file=sys.stderr)
         sys.exit(2)
     import numpy as np
     import torch
@@ -89,109 +404,89 @@ def main():
     from qw6_amd.workload import SynthLayer
 
     torch.cuda.set_device(0)
-    ctx = Q.Context(0, max_tokens=4)
+    if args.calib_copy:
+        n = args.calib_copy * 1024 * 1024 // 4
+        a = torch.ones(n, dtype=torch.float32, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(4):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+    want_prefill = args.workload in ("all", "prefill")
+    ctx = Q.Context(0, max_tokens=args.prefill_tokens if want_prefill else 4)
     P = args.pool
-    log("building %d synthetic layers (%s)" % (P, args.mix))
-    pool = [SynthLayer(ctx, 1000 + i, i, args.mix) for i in range(P)]
-    X = torch.empty(P, HIDDEN, dtype=torch.float32, device="cuda")
-    for i in range(P):
-        Q.synth_normal(X[i], HIDDEN, 1.0, 77, S.stream_id(i, S.K_X))
-    out = torch.empty(P, HIDDEN, dtype=torch.float32, device="cuda")
-    idx = torch.zeros(P, TOP_K, dtype=torch.int32, device="cuda")
-    torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    sp = stream.cuda_stream
-
-    def step(k):
-        j = k % P
-        ctx.moe_forward(pool[j].desc, X[j], out[j], n_tok=1, idx=idx[j], stream=sp)
-
-    for k in range(args.warmup):
-        step(k)
-    torch.cuda.synchronize()
-
-    # algorithmic bytes per step and per kernel: the router, the 8 selected
-    # experts' gate/up/down, the shared expert, activations in and out
-    sel = idx.cpu().numpy()
-    L0 = pool[0]
-    sh_gu = sum(S.row_bytes(m[1], m[3]) * m[2] for m in L0.shared[:2])
-    sh_dn = S.row_bytes(L0.shared[2][1], L0.shared[2][3]) * L0.shared[2][2]
-    r_b = N_EXPERTS * HIDDEN * 4 + HIDDEN * 4 + N_EXPERTS * 4
-    gu_bytes, dn_bytes = [], []
-    for j in range(P):
-        L = pool[j]
-        gub = sum(2 * S.row_bytes(L.quants[int(e)][0], HIDDEN) * INTER for e in sel[j])
-        dnb = sum(S.row_bytes(L.quants[int(e)][2], INTER) * HIDDEN for e in sel[j])
-        gu_bytes.append(gub + sh_gu + HIDDEN * 4 + N_EXPERTS * 4 + (TOP_K + 1) * INTER * 4)
-        dn_bytes.append(dnb + sh_dn + (TOP_K + 1) * INTER * 4 + HIDDEN * 4)
-    gu_b, d_b = float(np.mean(gu_bytes)), float(np.mean(dn_bytes))
-    bytes_per_step = r_b + gu_b + d_b - N_EXPERTS * 4 - (TOP_K + 1) * INTER * 4
-
-    K = args.steps
-    # eager timing
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(K):
-        step(k)
-    torch.cuda.synchronize()
-    eager_s = time.perf_counter() - t0
-
-    # HIP graph over one pass of the pool, replayed
-    g = torch.cuda.CUDAGraph()
-    s2 = torch.cuda.Stream()
-    with torch.cuda.stream(s2):
-        with torch.cuda.graph(g, stream=s2):
-            for j in range(P):
-                ctx.moe_forward(pool[j].desc, X[j], out[j], n_tok=1, idx=idx[j],
-                                stream=s2.cuda_stream)
-    torch.cuda.synchronize()
-    reps = max(1, K // P)
-    for _ in range(2):
-        g.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(reps):
-        g.replay()
-    torch.cuda.synchronize()
-    graph_s = time.perf_counter() - t0
-    steps_graph = reps * P
-    us_layer = 1e6 * graph_s / steps_graph
-    eager_us = 1e6 * eager_s / K
-
-    # per-kernel durations: each kernel's own dispatch timestamps (HIP events
-    # recorded by hipExtLaunchKernel on the launch stream)
-    nprof = min(K, 256)
-    ctx.profile(nprof)
-    for k in range(nprof):
-        step(k)
-    ms, calls = ctx.profile_read()
-    ctx.profile(0)
-    kus = [1e3 * m / calls for m in ms]
-    achieved = gu_b / (kus[1] * 1e-6) / 1e9
-    kernels = {
-        "moe_router": {"us": round(kus[0], 2), "bytes": int(r_b),
-                       "GBps": round(r_b / kus[0] / 1e3, 1)},
-        "moe_gate_up": {"us": round(kus[1], 2), "bytes": int(gu_b),
-                        "GBps": round(achieved, 1)},
-        "moe_down": {"us": round(kus[2], 2), "bytes": int(d_b),
-                     "GBps": round(d_b / kus[2] / 1e3, 1)},
-    }
-    log("graph %.2f us/layer, eager %.2f us/layer, kernels %s" % (us_layer, eager_us, kernels))
+    mix = "iq2m" if args.workload == "iq2m" else "q4k"
+    secondary = {}
+    res_main = None
+    pool = []
+    if args.workload in ("all", "q4k", "iq2m", "prefill"):
+        log("building %d synthetic layers (%s)" % (P, mix))
+        pool = [SynthLayer(ctx, 1000 + i, i, mix) for i in range(P)]
+        X = torch.empty(P, HIDDEN, dtype=torch.float32, device="cuda")
+        for i in range(P):
+            Q.synth_normal(X[i], HIDDEN, 1.0, 77, S.stream_id(i, S.K_X))
+        out = torch.empty(P, HIDDEN, dtype=torch.float32, device="cuda")
+        idx = torch.zeros(P, TOP_K, dtype=torch.int32, device="cuda")
+        torch.cuda.synchronize()
+        if args.workload != "prefill":
+            res_main = bench_decode(torch, Q, S, ctx, pool, X, out, idx, args)
+            log("decode %s: %s" % (mix, json.dumps(res_main)))
+    if want_prefill:
+        pf, t2 = bench_prefill(torch, Q, S, ctx, pool, args)
+        secondary["prefill_T%d" % args.prefill_tokens] = pf
+        secondary["mtp_T2"] = t2
+        log("prefill: %s" % json.dumps(pf))
+        log("T=2: %s" % json.dumps(t2))
 
     cpu = None
-    if not args.no_cpu:
-        xs_host = X.cpu().numpy()
-        cpu = cpu_baseline(pool[0], xs_host, args.cpu_seconds)
+    if res_main is not None and not args.no_cpu:
+        cpu = cpu_baseline(pool[0], X.cpu().numpy(), args.cpu_seconds)
+    for L in pool:
+        L.free()
+    pool = []
 
-    hbm = bytes_per_step / (us_layer * 1e-6) / 1e9
+    if args.workload == "all":
+        log("building %d synthetic layers (iq2m)" % P)
+        pool2 = [SynthLayer(ctx, 2000 + i, i, "iq2m") for i in range(P)]
+        X2 = torch.empty(P, HIDDEN, dtype=torch.float32, device="cuda")
+        for i in range(P):
+            Q.synth_normal(X2[i], HIDDEN, 1.0, 78, S.stream_id(i, S.K_X))
+        o2 = torch.empty_like(X2)
+        i2 = torch.zeros(P, TOP_K, dtype=torch.int32, device="cuda")
+        r2 = bench_decode(torch, Q, S, ctx, pool2, X2, o2, i2, args)
+        r2["workload"] = ("decode layer, batch 1, IQ2_XXS gate/up, IQ3_S (even experts) / "
+                          "IQ2_S (odd) down, F32 router, shared expert (Q4_K/Q6_K)")
+        secondary["iq2m_decode"] = r2
+        log("decode iq2m: %s" % json.dumps(r2))
+        for L in pool2:
+            L.free()
+    if args.workload in ("all", "stack"):
+        st = bench_stack(torch, Q, S, ctx, args)
+        secondary["stack"] = st
+        log("stack: %s" % json.dumps(st))
+
+    if res_main is None:
+        print(json.dumps({"secondary": secondary}), flush=True)
+        ctx.close()
+        return
+
+    gk = res_main["kernels"]["k_moe_gate_up"]
+    achieved = gk["GBps"]
+    traffic = None
+    traffic_src = None
+    if mix == "q4k" and os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as fh:
+            tj = json.load(fh)
+        traffic = tj.get("traffic_bytes_per_launch")
+        traffic_src = os.path.relpath(TRAFFIC_FILE, HERE)
     res = {
         "metric": "decode MoE-FFN us/layer + HBM GB/s vs 8 TB/s peak; T=512 prefill TFLOP/s",
-        "value": round(us_layer, 3),
+        "value": res_main["us_per_layer"],
         "unit": "us/layer",
         "n_gpus": 1,
-        "steps": steps_graph,
+        "steps": res_main["steps"],
         "warmup": args.warmup,
-        "ms_per_step": round(us_layer / 1e3, 6),
+        "ms_per_step": round(res_main["us_per_layer"] / 1e3, 6),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -199,22 +494,23 @@ def main():
         "data": "synthetic (seeded GGUF blocks generated on device)",
         "config": {"workload": "MoE FFN decode layer, batch 1: hidden 2048, 256 experts "
                                "top-8, inter 512, %s, F32 router, shared expert"
-                               % ("Q4_K gate/up + Q6_K down" if args.mix == "q4k"
+                               % ("Q4_K gate/up + Q6_K down" if mix == "q4k"
                                   else "IQ2_XXS gate/up + IQ3_S/IQ2_S down"),
                    "tokens_per_step": 1, "layer_pool": P},
-        "hbm_GBps": round(hbm, 1),
-        "hbm_frac": round(hbm / HBM_PEAK_GBPS, 4),
-        "bytes_per_step": int(bytes_per_step),
-        "eager_us_per_layer": round(eager_us, 3),
-        "kernels": kernels,
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+        "hbm_GBps": res_main["hbm_GBps"],
+        "hbm_frac": res_main["hbm_frac"],
+        "bytes_per_step": res_main["bytes_per_step"],
+        "eager_us_per_layer": res_main["eager_us_per_layer"],
+        "kernels": res_main["kernels"],
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "kernel": "moe_gate_up"},
+                     "traffic": traffic, "kernel": "k_moe_gate_up",
+                     "algorithmic_bytes": gk["bytes"], "avg_us": gk["us"],
+                     "traffic_source": traffic_src},
         "cpu_baseline": cpu,
+        "secondary": secondary,
     }
     print(json.dumps(res), flush=True)
-    for L in pool:
-        L.free()
     ctx.close()
 
 

@@ -588,6 +588,8 @@ __device__ __forceinline__ void route_keys(const float* __restrict__ logits, uin
 // heads (each lane's keys sorted, stable); the lowest lane whose head equals
 // the maximum holds the lowest index with that logit and pops its head.
 // Writes the (key, index) of rank r to scr[32 + r] for r < top_k.
+constexpr uint32_t kRouteScr = 128;   // routing scratch per wave (uint2)
+
 __device__ __forceinline__ void route_rounds(uint32_t (&k)[4], uint32_t top_k, uint2* scr) {
     const uint32_t lane = threadIdx.x & 63u;
     uint32_t id[4] = {0, 1, 2, 3};
@@ -611,20 +613,22 @@ __device__ __forceinline__ void route_rounds(uint32_t (&k)[4], uint32_t top_k, u
     }
 }
 
-// One wave routes one token. Fast path: T = the minimum over 8 groups of 8
-// lanes of each group's largest key is at most the 8th-largest key (8
-// distinct keys are >= T), so the top_k <= 8 winners are among the keys >= T
-// -- about 20 of 256 for router logits. Those candidates are compacted into
-// LDS and each is ranked against all of them at once with one 64-bit compare
-// of (key, ~index) per pair; more than 32 candidates take route_rounds.
-// scr: 40 uint2 of LDS private to the wave. Lanes j < top_k leave the j-th
-// selected expert and its gate weight in out_e[j] / out_w[j] (any memory).
-__device__ __forceinline__ void wave_route(const float* __restrict__ logits, uint32_t n,
-                                           uint32_t top_k, uint2* scr, uint32_t* out_e,
-                                           float* out_w) {
+// One wave routes one token (scr: kRouteScr uint2 of LDS private to the
+// wave). Fast path: T = the minimum over 8 groups of 8 lanes of each group's
+// largest key is at most the 8th-largest key (8 distinct keys are >= T), so
+// the top_k <= 8 winners are among the keys >= T -- about 20 of 256 for
+// router logits. Those candidates are compacted into LDS and each is ranked
+// against all of them at once with one 64-bit compare of (key, ~index) per
+// pair; more than 32 candidates take route_rounds.
+//
+// route_rank ranks the top_k <= 8 keys. Fast path (returns true): lanes l and l + 32 both
+// hold candidate l (l < ncand) as me = (~index, key) and, in rank, how many
+// candidates order above it, each lane comparing against 16 of the 32 slots.
+// Slow path (more than 32 candidates, returns false): scr[32 + r] holds the
+// (~index, key) of rank r for r < top_k after a wave barrier.
+__device__ __forceinline__ bool route_rank(uint32_t (&k)[4], uint32_t top_k, uint2* scr,
+                                           uint2& me2, uint32_t& rank, uint32_t& ncand) {
     const uint32_t lane = threadIdx.x & 63u;
-    uint32_t k[4];
-    route_keys(logits, n, k);
     uint32_t g = max(max(k[0], k[1]), max(k[2], k[3]));
 #pragma unroll
     for (int i = 0; i < 3; i++) {   // group maxima over lanes 8q .. 8q+7
@@ -638,7 +642,8 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ logits, uin
     }
     const uint32_t t = (uint32_t)__builtin_amdgcn_readfirstlane((int)g);
     bool c[4];
-    uint32_t ncand = 0, pos = 0;
+    uint32_t pos = 0;
+    ncand = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         c[i] = k[i] >= t && k[i] != 0u;
@@ -646,28 +651,49 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ logits, uin
         ncand += __popcll(b);
         pos += __builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
     }
-    if (ncand <= 32) {
-        // candidates of lower lanes first, then this lane's in index order
-#pragma unroll
-        for (int i = 0; i < 4; i++)
-            if (c[i]) scr[pos++] = make_uint2(~(4 * lane + (uint32_t)i), k[i]);
-        __builtin_amdgcn_wave_barrier();
-        if (lane < ncand) {
-            const uint2 me2 = scr[lane];
-            const uint64_t me = ((uint64_t)me2.y << 32) | me2.x;
-            uint32_t rank = 0;
-#pragma unroll
-            for (uint32_t m = 0; m < 32; m++) {
-                const uint2 o2 = scr[m];
-                const uint64_t o = ((uint64_t)o2.y << 32) | o2.x;
-                rank += (m < ncand && o > me) ? 1u : 0u;
-            }
-            if (rank < top_k) scr[32 + rank] = me2;
-        }
-    } else {
+    if (ncand > 32) {
         route_rounds(k, top_k, scr);
+        __builtin_amdgcn_wave_barrier();
+        return false;
+    }
+    // candidates of lower lanes first, then this lane's in index order, into
+    // slots [0, ncand); the other slots below 64 hold (0, 0), below every
+    // candidate. Branch-free: a non-candidate writes its own discard slot
+    // 64 + lane (the wave's LDS writes land in program order).
+    scr[lane] = make_uint2(0u, 0u);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        scr[c[i] ? pos : 64u + lane] = make_uint2(~(4 * lane + (uint32_t)i), k[i]);
+        pos += c[i] ? 1u : 0u;
     }
     __builtin_amdgcn_wave_barrier();
+    const uint32_t h = lane >> 5, l = lane & 31u;
+    me2 = scr[l];
+    const uint64_t me = ((uint64_t)me2.y << 32) | me2.x;
+    uint32_t r = 0;
+#pragma unroll
+    for (uint32_t m = 0; m < 16; m++) {
+        const uint2 o2 = scr[16 * h + m];
+        const uint64_t o = ((uint64_t)o2.y << 32) | o2.x;
+        r += o > me ? 1u : 0u;
+    }
+    rank = r + __float_as_uint(partner(__uint_as_float(r), 32, lane));
+    return true;
+}
+
+// wave_route_keys: lanes j < top_k leave the j-th selected expert and its gate
+// weight in out_e[j] / out_w[j] (any memory). It takes the keys already loaded
+// by route_keys, so a caller can issue that load before its other memory
+// traffic.
+__device__ __forceinline__ void wave_route_keys(uint32_t (&k)[4], uint32_t top_k, uint2* scr,
+                                                uint32_t* out_e, float* out_w) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint2 me2;
+    uint32_t rank, ncand;
+    if (route_rank(k, top_k, scr, me2, rank, ncand)) {
+        if (lane < ncand && rank < top_k) scr[32 + rank] = me2;
+        __builtin_amdgcn_wave_barrier();
+    }
     uint32_t e = 0;
     float v = -INFINITY;
     if (lane < top_k) {
@@ -685,6 +711,35 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ logits, uin
         out_e[lane] = e;
         out_w[lane] = ex / sum;
     }
+}
+
+// The expert of rank u < top_k alone (same selection as wave_route_keys, no
+// gate weights), uniform across the wave.
+__device__ __forceinline__ uint32_t wave_route_select(uint32_t (&k)[4], uint32_t top_k,
+                                                      uint32_t u, uint2* scr) {
+    const uint32_t lane = threadIdx.x & 63u;
+    uint2 me2 = make_uint2(0u, 0u);
+    uint32_t rank = 0xffffffffu, ncand = 0;
+    uint32_t ix, key;
+    if (route_rank(k, top_k, scr, me2, rank, ncand)) {
+        const uint64_t b = __ballot(lane < ncand && rank == u);
+        const int w = b ? __ffsll((unsigned long long)b) - 1 : 0;
+        ix = (uint32_t)__builtin_amdgcn_readlane((int)me2.x, w);
+        key = (uint32_t)__builtin_amdgcn_readlane((int)me2.y, w);
+    } else {
+        const uint2 me = scr[32 + u];
+        ix = (uint32_t)__builtin_amdgcn_readfirstlane((int)me.x);
+        key = (uint32_t)__builtin_amdgcn_readfirstlane((int)me.y);
+    }
+    return key > kKeyNegInf ? ~ix : 0u;   // only -inf left: qw6 picks index 0
+}
+
+__device__ __forceinline__ void wave_route(const float* __restrict__ logits, uint32_t n,
+                                           uint32_t top_k, uint2* scr, uint32_t* out_e,
+                                           float* out_w) {
+    uint32_t k[4];
+    route_keys(logits, n, k);
+    wave_route_keys(k, top_k, scr, out_e, out_w);
 }
 
 // ---- synthetic data hash (twin of qw6_amd/synth.py) ------------------------------

@@ -143,12 +143,17 @@ __device__ __forceinline__ void stage_wait() {
     __syncthreads();
 }
 
-// Lattice tables needed by `mask` into LDS (IqTables layout at tab).
-__device__ __forceinline__ void stage_tables(uint8_t* tab, uint32_t mask) {
+// Lattice tables needed by `mask` into LDS (IqTables layout at tab), by the
+// waves [w0, 4) of a 4-wave block (all waves of any block when w0 == 0).
+__device__ __forceinline__ void stage_tables_from(uint8_t* tab, uint32_t mask, uint32_t w0) {
     const uint8_t* g = (const uint8_t*)&g_tabs;
-    if (mask & 1u) stage(tab + kTabOffIq2xxs, g + kTabOffIq2xxs, 256 * 8);
-    if (mask & 2u) stage(tab + kTabOffIq2s, g + kTabOffIq2s, 1024 * 8);
-    if (mask & 4u) stage(tab + kTabOffIq3s, g + kTabOffIq3s, 512 * 4);
+    const uint32_t nw = w0 ? 4u - w0 : 0xffffu;
+    if (mask & 1u) stage(tab + kTabOffIq2xxs, g + kTabOffIq2xxs, 256 * 8, w0, nw);
+    if (mask & 2u) stage(tab + kTabOffIq2s, g + kTabOffIq2s, 1024 * 8, w0, nw);
+    if (mask & 4u) stage(tab + kTabOffIq3s, g + kTabOffIq3s, 512 * 4, w0, nw);
+}
+__device__ __forceinline__ void stage_tables(uint8_t* tab, uint32_t mask) {
+    stage_tables_from(tab, mask, 0);
 }
 
 __host__ __device__ inline uint32_t tab_bytes(uint32_t mask) {
@@ -292,7 +297,7 @@ __global__ __launch_bounds__(64) void k_matvec_f32(const float* __restrict__ w,
 
 __global__ __launch_bounds__(64) void k_route(const float* __restrict__ logits, uint32_t n,
                                               uint32_t top_k, uint32_t* idx, float* w) {
-    __shared__ uint2 scr[40];
+    __shared__ uint2 scr[kRouteScr];
     const uint32_t t = blockIdx.x;
     wave_route(logits + (size_t)t * n, n, top_k, scr, idx + t * top_k, w + t * top_k);
 }
@@ -401,14 +406,16 @@ __device__ __forceinline__ void wait_vm(uint32_t n) {
 // distinct selected experts are numbered in first-use order ("slots").
 // Leaves s_slot_e[u] (expert of slot u), s_wt[u][t] (gate weight of slot u
 // for token t, 0 if unused), s_idx / s_w (per-token selection) and *s_n.
+// keys: token `wave`'s logit keys, loaded by route_keys in waves < T.
 template <int T>
-__device__ __forceinline__ void route_prologue(const MoeArgs& a, uint32_t* s_idx, float* s_w,
+__device__ __forceinline__ void route_prologue(const MoeArgs& a, uint32_t (&keys)[4],
+                                               uint32_t* s_idx, float* s_w,
                                                uint32_t* s_slot_e, float* s_wt, uint32_t* s_n) {
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    __shared__ uint2 s_rt[4][40];
+    __shared__ uint2 s_rt[4][kRouteScr];
     if (T == 1) {   // one token: the slots are the selection itself
         if (wave == 0) {
-            wave_route(a.route_logits, a.n_experts, a.top_k, s_rt[0], s_idx, s_w);
+            wave_route_keys(keys, a.top_k, s_rt[0], s_idx, s_w);
             __builtin_amdgcn_wave_barrier();
             if (lane < a.top_k) {
                 s_slot_e[lane] = s_idx[lane];
@@ -422,8 +429,7 @@ __device__ __forceinline__ void route_prologue(const MoeArgs& a, uint32_t* s_idx
         return;
     }
     if (wave < (uint32_t)T)
-        wave_route(a.route_logits + (size_t)wave * a.n_experts, a.n_experts, a.top_k, s_rt[wave],
-                   s_idx + wave * a.top_k, s_w + wave * a.top_k);
+        wave_route_keys(keys, a.top_k, s_rt[wave], s_idx + wave * a.top_k, s_w + wave * a.top_k);
     __syncthreads();
     if (wave == 0) {
         const uint32_t ne = T * a.top_k;
@@ -590,19 +596,31 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
     const uint32_t toff = tab_bytes(a.tmask_gu);
     uint8_t* wslots = smem + toff + wave * 2 * kStepsGu * kSlotBytes;
     const uint32_t slot_off = toff + wave * 2 * kStepsGu * kSlotBytes;
-    stage_tables(smem, a.tmask_gu);
     const bool shared_wg = blockIdx.x < a.n_sh_wg;
-    // Activations first when their unit layout is known before the routing
-    // (one gate/up format): their loads then overlap the logits round trip.
-    const bool early = FG >= 0 || shared_wg || a.pk[0].regular;
+    // Waves t < T of a routed block route token t. Their logits load is the
+    // block's first memory operation (loads complete in issue order, so
+    // nothing queued ahead of it delays the routing); the other waves stage
+    // the lattice tables and load their activations meanwhile.
+    const bool rwave = !shared_wg && wave < (uint32_t)T;
+    uint32_t keys[4];
+    if (rwave) route_keys(a.route_logits + (size_t)wave * a.n_experts, a.n_experts, keys);
+    TRACE_MARK_IF(rwave, 2, 4);
+    // (with T = 4 every wave routes, and the routing waves stage the tables too)
+    const uint32_t tw0 = shared_wg || T >= 4 ? 0u : (uint32_t)T;
+    stage_tables_from(smem, a.tmask_gu, tw0);
+    // Activations before the routing when their unit layout is known then (one
+    // gate/up format): their loads overlap the logits round trip.
+    const bool early = !rwave && (FG >= 0 || shared_wg || a.pk[0].regular);
     const int fx = FG >= 0 ? FG : shared_wg ? a.sg.fmt : a.pk[0].fmt;
     float xr[T][32], sx[T][4];
     if (early) load_x_all<T, FG>(fx, a.xin, a.hidden, a.hidden, xr, sx);
-    if (a.tmask_gu) {   // the lattice tables are in LDS before any wave reads them
+    if (a.tmask_gu && (!rwave || tw0 == 0)) {   // this wave's table loads have landed
         if (early) wait_vm(8u * T);
         else wait_vm(0);
-        __syncthreads();
     }
+    // the lattice tables are in LDS before any wave reads them: the barrier
+    // below, or the one that ends route_prologue
+    if (a.tmask_gu && shared_wg) __syncthreads();
     MatD G, Up;
     uint32_t row0;
     float* midp;
@@ -611,8 +629,27 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
         Up = a.su;
         row0 = (blockIdx.x * 4 + wave) * kStepsGu * rps;
         midp = a.mid + (size_t)a.max_u * T * a.inter;
+    } else if (T == 1 && blockIdx.x != a.n_sh_wg) {
+        // one token, not the publishing block: only the expert of this block's
+        // rank is needed (no gate weights, no slot table)
+        __shared__ uint2 s_rt1[kRouteScr];
+        __shared__ uint32_t s_e1;
+        const uint32_t b = blockIdx.x - a.n_sh_wg;
+        const uint32_t u = b / ntile, tile = b % ntile;
+        if (wave == 0) {
+            const uint32_t e = wave_route_select(keys, a.top_k, u, s_rt1);
+            if ((threadIdx.x & 63u) == 0) s_e1 = e;
+        }
+        __syncthreads();
+        TRACE_MARK(2, 0);
+        const uint32_t e = s_e1;
+        G = expert_mat(a, e, 0);
+        Up = expert_mat(a, e, 1);
+        row0 = (tile * 4 + wave) * kStepsGu * rps;
+        midp = a.mid + (size_t)u * T * a.inter;
+        if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr, sx);
     } else {
-        route_prologue<T>(a, s_idx, s_w, s_slot_e, s_wt, &s_n);   // ends with a barrier
+        route_prologue<T>(a, keys, s_idx, s_w, s_slot_e, s_wt, &s_n);   // ends with a barrier
         TRACE_MARK(2, 0);
         const uint32_t b = blockIdx.x - a.n_sh_wg;
         const uint32_t u = b / ntile, tile = b % ntile;
@@ -676,9 +713,25 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
     const uint32_t slot_off = toff + wave * S * kSlotBytes;
     const uint32_t unit = lane & (U - 1), blk = unit >> 3, q = lane / U;
     const int j = (int)(unit & 7);
-    const uint32_t nslot = a.slots->n;   // one scalar load, shared by every wave
+    // The slot table is read in one round trip: the count, this wave's first
+    // slot (speculatively: entries past the count are null) and the gate
+    // weights are independent loads. The combine's residual and shared weight
+    // are fetched now too, not after the products.
+    const uint32_t nslot = a.slots->n;
+    const uint32_t u0 = wave - has_sh;
+    const bool first_sh = has_sh && wave == 0;
+    const uint32_t u0c = first_sh ? 0u : min(u0, kMaxSlots - 1);
+    const uint8_t* p0 = a.slots->p[u0c];
+    const int f0 = a.slots->fmt[u0c];
+    const uint32_t rb0 = a.slots->rb[u0c];
     if (threadIdx.x < kMaxSlots * kMaxTok)
         s_wt[threadIdx.x] = a.slots->wt[threadIdx.x / kMaxTok][threadIdx.x % kMaxTok];
+    float resid = 0.f, shw = 1.0f;
+    if (threadIdx.x < R * T) {
+        const uint32_t rl = threadIdx.x / T, t = threadIdx.x % T;
+        if (a.residual) resid = a.residual[(size_t)t * a.hidden + r0 + rl];
+        if (has_sh && a.shared_router) shw = a.sw[t];
+    }
     const uint32_t ntot = nslot + has_sh;
     if (a.tmask_dn) {   // the lattice tables are in LDS before any wave reads them
         wave_wait();
@@ -691,8 +744,10 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
         float xr[T][32], sx[T][4];
         // activations (independent of the slot table) before the weights
         if (FD >= 0) load_x_all<T, FD>(FD, xm, a.inter, a.inter, xr, sx);
-        const MatD D = sh ? a.sd : MatD{a.slots->p[u], a.slots->fmt[u], a.hidden, a.inter,
-                                        a.slots->rb[u]};
+        const MatD D = sh ? a.sd
+                          : m == wave ? MatD{p0, f0, a.hidden, a.inter, rb0}
+                                      : MatD{a.slots->p[u], a.slots->fmt[u], a.hidden, a.inter,
+                                             a.slots->rb[u]};
         const int f = FD >= 0 ? FD : D.fmt;
         if (FD < 0) load_x_all<T, FD>(f, xm, a.inter, a.inter, xr, sx);
 #pragma unroll
@@ -724,13 +779,14 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
     }
     TRACE_MARK(3, 2);
     __syncthreads();
-    for (uint32_t i = threadIdx.x; i < R * T; i += blockDim.x) {
-        const uint32_t rl = i / T, t = i % T;
+    static_assert(R * T <= 64, "one combine output per thread of the smallest block");
+    if (threadIdx.x < R * T) {
+        const uint32_t rl = threadIdx.x / T, t = threadIdx.x % T;
         float v = 0.f;
         for (uint32_t u = 0; u < nslot; u++)
             v = fmaf(s_wt[u * kMaxTok + t], ybuf[((u + has_sh) * R + rl) * T + t], v);
-        if (has_sh) v = fmaf(a.shared_router ? a.sw[t] : 1.0f, ybuf[rl * T + t], v);
-        if (a.residual) v += a.residual[(size_t)t * a.hidden + r0 + rl];
+        if (has_sh) v = fmaf(shw, ybuf[rl * T + t], v);
+        if (a.residual) v += resid;
         a.out[(size_t)t * a.hidden + r0 + rl] = v;
     }
 }

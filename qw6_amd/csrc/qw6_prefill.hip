@@ -90,7 +90,7 @@ __device__ __forceinline__ void split3(float x, uint16_t (&p)[3]) {
 __global__ __launch_bounds__(64) void k_pre_route(PrefillLayer L, PrefillWs ws,
                                                   const float* __restrict__ xin,
                                                   const float* __restrict__ logits) {
-    __shared__ uint2 scr[40];
+    __shared__ uint2 scr[kRouteScr];
     const uint32_t t = blockIdx.x, lane = threadIdx.x;
     wave_route(logits + (size_t)t * L.n_experts, L.n_experts, L.top_k, scr,
                ws.pidx + (size_t)t * L.top_k, ws.pw + (size_t)t * L.top_k);

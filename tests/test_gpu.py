@@ -340,3 +340,23 @@ def test_given_logits_on_a_layer_with_router(torch_dev, ctx, layers):
             (oo, oi, _), _ = oracle_for(L, xs[t], logits=lg[t])
             assert np.array_equal(idx[t], oi)
             assert cases.rel_l2(out[t], oo) <= TOL
+
+
+def test_in_place_residual_update(torch_dev, ctx, layers):
+    """hidden <- hidden + MoE(rmsnorm(hidden)) with x, residual and out the same
+    buffer (qw6.c:2475-2484 updates the hidden state in place) equals the call
+    with separate buffers, for T = 1 and 3."""
+    torch = torch_dev
+    L = layers[("q4k", 11)]
+    nw = torch.from_numpy(cases.norm_w(11, 0)).cuda()
+    layer = Q.MoeLayer.from_buffer_copy(L.desc)
+    layer.norm_w, layer.norm_eps = nw.data_ptr(), 1e-6
+    for T in (1, 3):
+        xs = np.stack([cases.token_x(91, 3, t) for t in range(T)])
+        h = torch.from_numpy(xs).cuda()
+        ref = torch.empty_like(h)
+        ctx.moe_forward(layer, h, ref, n_tok=T, residual=h)
+        torch.cuda.synchronize()
+        ctx.moe_forward(layer, h, h, n_tok=T, residual=h)
+        torch.cuda.synchronize()
+        assert torch.equal(h, ref)

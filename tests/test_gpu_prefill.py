@@ -207,3 +207,24 @@ def test_grouped_graph_replay(torch_dev, ctx, layer):
             torch.cuda.synchronize()
     finally:
         ctx.set_mode(0)
+
+
+def test_grouped_in_place_residual_update(torch_dev, ctx, layer):
+    """x, residual and out the same buffer on the grouped path (router and
+    RMSNorm on the device) equals the call with separate buffers."""
+    torch = torch_dev
+    T = 80
+    nw = torch.from_numpy(cases.norm_w(61, 0)).cuda()
+    desc = Q.MoeLayer.from_buffer_copy(layer.desc)
+    desc.norm_w, desc.norm_eps = nw.data_ptr(), 1e-6
+    h = torch.from_numpy(np.stack([cases.token_x(66, 2, t) for t in range(T)])).cuda()
+    ref = torch.empty_like(h)
+    ctx.set_mode(2)
+    try:
+        ctx.moe_forward(desc, h, ref, n_tok=T, residual=h)
+        torch.cuda.synchronize()
+        ctx.moe_forward(desc, h, h, n_tok=T, residual=h)
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_mode(0)
+    assert torch.equal(h, ref)
