@@ -15,8 +15,9 @@ kernels, inputs already in HBM.
 experts + shared): algorithmic bytes per launch over its average duration,
 measured with dispatch-timestamped HIP events on the launch stream.
 `traffic` is the HBM bytes per launch from rocprofv3 FETCH_SIZE + WRITE_SIZE
-counter runs, scaled by what the counters read for a copy kernel of known
-size (read from the committed summary; null when absent).
+counter runs, each scaled by what the same counter reads for an elementwise
+y = 2x kernel over 512 MiB (read from the committed summary; null when
+absent).
 
 `cpu_baseline` times qw6's own CPU path (compiled from the reference where
 available, else the repository's bit-identical C restatement) on a bounded
@@ -63,9 +64,10 @@ def parse():
     ap.add_argument("--no-graph", action="store_true",
                     help="eager launches only (for counter collection)")
     ap.add_argument("--calib-copy", type=int, default=0, metavar="MIB",
-                    help="first run a device copy of MIB MiB 4 times (counter calibration)")
+                    help="first run y = 2x over MIB MiB 4 times (counter calibration: "
+                         "MIB MiB read and written per launch)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
-                    help="turn two rocprofv3 --pmc csv outputs into the traffic summary")
+                    help="turn two rocprofv3 --pmc csv outputs (FETCH_SIZE, WRITE_SIZE) into the traffic summary")
     ap.add_argument("--command", default="", help="command line recorded in the summary")
     return ap.parse_args()
 
@@ -111,8 +113,8 @@ def summarize_pmc(fetch_dir, write_dir, calib_mib, command):
             raise SystemExit("kernel %s not in counters: %s" % (key, list(d)))
         return max(ks, key=lambda k: d[k][1])
 
-    ck_f = pick(f, "elementwise")
-    ck_w = pick(w, "elementwise")
+    ck_f = pick(f, "MulFunctor")
+    ck_w = pick(w, "MulFunctor")
     fac_f = nbytes / (f[ck_f][0] * 1024.0)
     fac_w = nbytes / (w[ck_w][0] * 1024.0)
     gu_f = pick(f, "k_moe_gate_up")
@@ -121,7 +123,7 @@ def summarize_pmc(fetch_dir, write_dir, calib_mib, command):
     write = w[gu_w][0] * 1024.0 * fac_w
     out = {
         "kernel": "k_moe_gate_up",
-        "workload": "decode layer, batch 1, Q4_K gate/up + Q6_K down (pool of 16 layers)",
+        "workload": "decode layer, batch 1, Q4_K gate/up + Q6_K down, F32 router, shared expert",
         "fetch_bytes_per_launch": round(fetch),
         "write_bytes_per_launch": round(write),
         "traffic_bytes_per_launch": round(fetch + write),
@@ -408,8 +410,8 @@ def main():
         n = args.calib_copy * 1024 * 1024 // 4
         a = torch.ones(n, dtype=torch.float32, device="cuda")
         b = torch.empty_like(a)
-        for _ in range(4):
-            b.copy_(a)
+        for _ in range(4):   # reads MIB MiB, writes MIB MiB per launch
+            torch.mul(a, 2.0, out=b)
         torch.cuda.synchronize()
         del a, b
     want_prefill = args.workload in ("all", "prefill")
