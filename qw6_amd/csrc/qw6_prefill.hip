@@ -10,10 +10,10 @@
 //   k_pre_sort    one workgroup: counting sort of the (token, k) pairs by
 //                 expert into "entries", and a tile list of <= 32 entries of
 //                 one expert (the shared expert last, with every token).
-//   k_pre_gemm<0> gate and up for 64 intermediate rows of one tile:
-//                 mid[entry] = silu(x.gate) * (x.up).
-//   k_pre_gemm<1> down for 128 hidden rows of one tile, times the entry's
-//                 gate weight -> ybuf[entry].
+//   k_pre_gemm<0> gate and up for 128 intermediate rows of one tile (64
+//                 for Q6_K): mid[entry] = silu(x.gate) * (x.up).
+//   k_pre_gemm<1> down for 256 hidden rows of one tile (128 for Q6_K), times
+//                 the entry's gate weight -> ybuf[entry].
 //   k_pre_combine out[t] = sum_k ybuf[entry(t, k)] + ybuf[shared entry(t)]
 //                 (+ residual), a fixed order: deterministic, no atomics.
 //
@@ -25,8 +25,11 @@
 //    MFMAs per 32-column sub-block;
 //  - the fp32 sub-block scale d*sc multiplies each sub-block's 16x16 MFMA
 //    result; the code bias (128 or 160) and the K-quant minimum dmin*m, both
-//    of the form (per-row integer) x (per-token sub-block sum of x), are two
-//    more small MFMAs per 256-column block with the sub-block sums as A.
+//    of the form (per-row integer) x (per-token sub-block sum of x), take one
+//    more MFMA each per 256-column block: A holds the three bf16 parts of the
+//    eight sub-block sums in k-slots 0-7, 8-15, 16-23, B the integers.
+// Weight codes are decoded from the raw block bytes in LDS just before their
+// MFMAs, two sub-blocks at a time, so a wave keeps 4 row tiles in flight.
 // Sub-blocks are 32 columns in every format handled here (Q4_K, Q5_K, and
 // Q6_K under qw6's even-scale rule, qw6.c:1567-1570).
 
@@ -45,10 +48,12 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr uint32_t kPM = 32;      // entries per tile (2 MFMA row groups of 16)
 constexpr uint32_t kPWG = 256;    // threads per workgroup (4 waves)
-constexpr uint32_t kRaw = 128;    // weight rows staged per workgroup and block
 
-__host__ __device__ constexpr uint32_t raw_chunks(int f) {   // 16-B chunks per staged row block
-    return (fmt_block_bytes(f) + 14 + 15) / 16;
+// 16-B chunks per staged row block: Q4_K / Q5_K blocks (144 / 176 B) of
+// 16-byte aligned rows are 16-byte aligned; a Q6_K block (210 B) may start at
+// any even offset within its first chunk.
+__host__ __device__ constexpr uint32_t raw_chunks(int f) {
+    return f == F_Q6K ? (fmt_block_bytes(f) + 14 + 15) / 16 : fmt_block_bytes(f) / 16;
 }
 
 // ---- bf16 operand preparation -----------------------------------------------------
@@ -210,118 +215,166 @@ __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, const f32x
                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
 }
 
-// The B operands of one 16-row tile for one 256-column block, decoded from
-// the raw block bytes in LDS (s = LDS words, R = byte offset of this lane's
-// row block). Lane (n = l % 16, q = l / 16) holds codes of row n, columns
-// 32 s + 8 q .. + 8 for the eight sub-blocks s, the fp32 sub-block scales of
-// row n, and, in lanes q == 0, the per-sub-block integer factors of the
-// bias / minimum terms as B operands over k = sub-block.
-struct BTile {
-    uint4 b[8];       // codes per sub-block
-    float dsc[8];     // d * sc per sub-block
-    uint4 bsc, bmin;  // B operands: sub-block scales, sub-block minimums (q == 0 lanes)
+// ---- B-tile decoding ----------------------------------------------------------------
+// A wave works on RT tiles of 16 weight rows. For one 256-column block, lane
+// (n = l % 16, q = l / 16) of tile r reads row n's raw block bytes from LDS
+// (s = LDS words, R = byte offset of the row's block) and produces, per
+// sub-block s, the B operand: codes 128 + q (bf16) of columns 32 s + 8 q .. + 8.
+
+// Per-tile scale state of one block: d * sc per sub-block, and d, dmin.
+struct TileScales {
+    float dsc[8];
     float d, dmin;
 };
 
+// The sub-block scales (and minimums) of row n as B operands over k =
+// 8 q' + j (j = sub-block), replicated in lanes q' = 0, 1, 2 (one per bf16
+// part of the activation sums) and zero in q' = 3.
 template <int F>
-__device__ __forceinline__ void decode_btile(const uint32_t* s, uint32_t R, uint32_t q,
-                                             BTile& bt) {
+__device__ __forceinline__ void tile_scales(const uint32_t* s, uint32_t R, uint32_t q,
+                                            TileScales& ts, uint4& bsc, uint4& bmin) {
+    float sc[8], mn[8];
     if (F == F_Q4K || F == F_Q5K) {
-        const uint4 hd = *(const uint4*)(s + (R >> 2));
-        bt.d = h2f(hd.x & 0xffffu);
-        bt.dmin = h2f(hd.x >> 16);
+        const uint4 hd = *(const uint4*)(s + (R >> 2));   // 16-byte aligned block
+        ts.d = h2f(hd.x & 0xffffu);
+        ts.dmin = h2f(hd.x >> 16);
         const uint32_t A = hd.y, B = hd.z, C = hd.w;
-        uint32_t sc[8], mn[8];
 #pragma unroll
         for (int j = 0; j < 4; j++) {   // qw6_get_scale_min_k4 (qw6.c:1480-1490)
-            sc[j] = (A >> (8 * j)) & 63u;
-            mn[j] = (B >> (8 * j)) & 63u;
-            sc[j + 4] = ((C >> (8 * j)) & 15u) | (((A >> (8 * j + 6)) & 3u) << 4);
-            mn[j + 4] = ((C >> (8 * j + 4)) & 15u) | (((B >> (8 * j + 6)) & 3u) << 4);
+            sc[j] = (float)((A >> (8 * j)) & 63u);
+            mn[j] = (float)((B >> (8 * j)) & 63u);
+            sc[j + 4] = (float)(((C >> (8 * j)) & 15u) | (((A >> (8 * j + 6)) & 3u) << 4));
+            mn[j + 4] = (float)(((C >> (8 * j + 4)) & 15u) | (((B >> (8 * j + 6)) & 3u) << 4));
         }
-#pragma unroll
-        for (int j = 0; j < 8; j++) bt.dsc[j] = bt.d * (float)sc[j];
-        // Q4_K / Q5_K blocks are 144 / 176 B: 16-byte aligned, plain 8-byte reads
-        const uint32_t qo = F == F_Q4K ? 16u : 48u;   // qs offset
-        uint32_t h0 = 0, h1 = 0;
-        if (F == F_Q5K) {
-            const uint2 hq = *(const uint2*)(s + ((R + 16 + 8 * q) >> 2));
-            h0 = hq.x; h1 = hq.y;
-        }
-#pragma unroll
-        for (int g = 0; g < 4; g++) {
-            const uint2 wq = *(const uint2*)(s + ((R + qo + 32 * g + 8 * q) >> 2));
-            const uint32_t w0 = wq.x, w1 = wq.y;
-            uint32_t l0 = w0 & 0x0f0f0f0fu, l1 = w1 & 0x0f0f0f0fu;
-            uint32_t u0 = (w0 >> 4) & 0x0f0f0f0fu, u1 = (w1 >> 4) & 0x0f0f0f0fu;
-            if (F == F_Q5K) {
-                l0 |= ((h0 >> (2 * g)) & 0x01010101u) << 4;
-                l1 |= ((h1 >> (2 * g)) & 0x01010101u) << 4;
-                u0 |= ((h0 >> (2 * g + 1)) & 0x01010101u) << 4;
-                u1 |= ((h1 >> (2 * g + 1)) & 0x01010101u) << 4;
-            }
-            bt.b[2 * g] = codes8(l0, l1);
-            bt.b[2 * g + 1] = codes8(u0, u1);
-        }
-        bt.bsc = q == 0 ? u4(bf16_bits((float)sc[0]) | (bf16_bits((float)sc[1]) << 16),
-                             bf16_bits((float)sc[2]) | (bf16_bits((float)sc[3]) << 16),
-                             bf16_bits((float)sc[4]) | (bf16_bits((float)sc[5]) << 16),
-                             bf16_bits((float)sc[6]) | (bf16_bits((float)sc[7]) << 16))
-                        : u4(0, 0, 0, 0);
-        bt.bmin = q == 0 ? u4(bf16_bits((float)mn[0]) | (bf16_bits((float)mn[1]) << 16),
-                              bf16_bits((float)mn[2]) | (bf16_bits((float)mn[3]) << 16),
-                              bf16_bits((float)mn[4]) | (bf16_bits((float)mn[5]) << 16),
-                              bf16_bits((float)mn[6]) | (bf16_bits((float)mn[7]) << 16))
-                         : u4(0, 0, 0, 0);
-    } else {   // Q6_K: sub-block s = 4h + k, scale sc[8h + 2k] (qw6.c:1550-1578)
-        bt.d = h2f(lds16(s, R + 208));
-        bt.dmin = 0.f;
-        float scf[8];
+    } else {   // Q6_K: sub-block 4h + k uses scale 8h + 2k (qw6.c:1550-1578)
+        ts.d = h2f(lds16(s, R + 208));
+        ts.dmin = 0.f;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const uint32_t sw0 = lds32(s, R + 192 + 8 * h), sw1 = lds32(s, R + 196 + 8 * h);
-            scf[4 * h + 0] = (float)(int8_t)(sw0 & 0xffu);
-            scf[4 * h + 1] = (float)(int8_t)((sw0 >> 16) & 0xffu);
-            scf[4 * h + 2] = (float)(int8_t)(sw1 & 0xffu);
-            scf[4 * h + 3] = (float)(int8_t)((sw1 >> 16) & 0xffu);
-            const uint32_t a0 = lds32(s, R + 64 * h + 8 * q), a1 = lds32(s, R + 64 * h + 8 * q + 4);
-            const uint32_t b0 = lds32(s, R + 64 * h + 32 + 8 * q), b1 = lds32(s, R + 64 * h + 36 + 8 * q);
-            const uint32_t x0 = lds32(s, R + 128 + 32 * h + 8 * q), x1 = lds32(s, R + 132 + 32 * h + 8 * q);
-            bt.b[4 * h + 0] = codes8((a0 & 0x0f0f0f0fu) | ((x0 & 0x03030303u) << 4),
-                                     (a1 & 0x0f0f0f0fu) | ((x1 & 0x03030303u) << 4));
-            bt.b[4 * h + 1] = codes8((b0 & 0x0f0f0f0fu) | (((x0 >> 2) & 0x03030303u) << 4),
-                                     (b1 & 0x0f0f0f0fu) | (((x1 >> 2) & 0x03030303u) << 4));
-            bt.b[4 * h + 2] = codes8(((a0 >> 4) & 0x0f0f0f0fu) | (((x0 >> 4) & 0x03030303u) << 4),
-                                     ((a1 >> 4) & 0x0f0f0f0fu) | (((x1 >> 4) & 0x03030303u) << 4));
-            bt.b[4 * h + 3] = codes8(((b0 >> 4) & 0x0f0f0f0fu) | (((x0 >> 6) & 0x03030303u) << 4),
-                                     ((b1 >> 4) & 0x0f0f0f0fu) | (((x1 >> 6) & 0x03030303u) << 4));
+            const uint32_t w0 = lds32(s, R + 192 + 8 * h), w1 = lds32(s, R + 196 + 8 * h);
+            sc[4 * h + 0] = (float)(int8_t)(w0 & 0xffu);
+            sc[4 * h + 1] = (float)(int8_t)((w0 >> 16) & 0xffu);
+            sc[4 * h + 2] = (float)(int8_t)(w1 & 0xffu);
+            sc[4 * h + 3] = (float)(int8_t)((w1 >> 16) & 0xffu);
         }
 #pragma unroll
-        for (int j = 0; j < 8; j++) bt.dsc[j] = bt.d * scf[j];
-        bt.bsc = q == 0 ? u4(bf16_bits(scf[0]) | (bf16_bits(scf[1]) << 16),
-                             bf16_bits(scf[2]) | (bf16_bits(scf[3]) << 16),
-                             bf16_bits(scf[4]) | (bf16_bits(scf[5]) << 16),
-                             bf16_bits(scf[6]) | (bf16_bits(scf[7]) << 16))
-                        : u4(0, 0, 0, 0);
-        bt.bmin = u4(0, 0, 0, 0);
+        for (int j = 0; j < 8; j++) mn[j] = 0.f;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) ts.dsc[j] = ts.d * sc[j];
+    auto pk = [](float a, float b) { return bf16_bits(a) | (bf16_bits(b) << 16); };
+    const bool on = q < 3;
+    bsc = on ? u4(pk(sc[0], sc[1]), pk(sc[2], sc[3]), pk(sc[4], sc[5]), pk(sc[6], sc[7]))
+             : u4(0, 0, 0, 0);
+    bmin = (on && F != F_Q6K) ? u4(pk(mn[0], mn[1]), pk(mn[2], mn[3]), pk(mn[4], mn[5]), pk(mn[6], mn[7]))
+                              : u4(0, 0, 0, 0);
+}
+
+// Codes of sub-blocks 2p and 2p + 1 of row n (this lane's 8 columns of each).
+template <int F>
+__device__ __forceinline__ void tile_codes(const uint32_t* s, uint32_t R, uint32_t q, int p,
+                                           uint4& b0, uint4& b1) {
+    if (F == F_Q4K || F == F_Q5K) {
+        // qs byte 32 p + l: low nibble column 64 p + l, high nibble 64 p + 32 + l
+        const uint32_t qo = F == F_Q4K ? 16u : 48u;
+        const uint2 wq = *(const uint2*)(s + ((R + qo + 32 * p + 8 * q) >> 2));
+        uint32_t l0 = wq.x & 0x0f0f0f0fu, l1 = wq.y & 0x0f0f0f0fu;
+        uint32_t h0 = (wq.x >> 4) & 0x0f0f0f0fu, h1 = (wq.y >> 4) & 0x0f0f0f0fu;
+        if (F == F_Q5K) {   // qh byte l: bit 2p -> column 64 p + l, bit 2p + 1 -> + 32
+            const uint2 hq = *(const uint2*)(s + ((R + 16 + 8 * q) >> 2));
+            l0 |= ((hq.x >> (2 * p)) & 0x01010101u) << 4;
+            l1 |= ((hq.y >> (2 * p)) & 0x01010101u) << 4;
+            h0 |= ((hq.x >> (2 * p + 1)) & 0x01010101u) << 4;
+            h1 |= ((hq.y >> (2 * p + 1)) & 0x01010101u) << 4;
+        }
+        b0 = codes8(l0, l1);
+        b1 = codes8(h0, h1);
+    } else {
+        // half h = p / 2; sub-blocks 4h + 2i, 4h + 2i + 1 (i = p % 2): ql bytes
+        // 64 h + l (a) and 64 h + 32 + l (b), low nibbles for i = 0, high for
+        // i = 1; 2-bit fields 2k of qh byte 128 + 32 h + l (k = 2i, 2i + 1)
+        const uint32_t h = (uint32_t)p >> 1, i = (uint32_t)p & 1u;
+        const uint32_t a0 = lds32(s, R + 64 * h + 8 * q), a1 = lds32(s, R + 64 * h + 8 * q + 4);
+        const uint32_t c0 = lds32(s, R + 64 * h + 32 + 8 * q), c1 = lds32(s, R + 64 * h + 36 + 8 * q);
+        const uint32_t x0 = lds32(s, R + 128 + 32 * h + 8 * q), x1 = lds32(s, R + 132 + 32 * h + 8 * q);
+        const uint32_t sh = 4 * i;   // nibble shift; also the qh shift 2k of k = 2i
+        b0 = codes8(((a0 >> sh) & 0x0f0f0f0fu) | (((x0 >> sh) & 0x03030303u) << 4),
+                    ((a1 >> sh) & 0x0f0f0f0fu) | (((x1 >> sh) & 0x03030303u) << 4));
+        b1 = codes8(((c0 >> sh) & 0x0f0f0f0fu) | (((x0 >> (sh + 2)) & 0x03030303u) << 4),
+                    ((c1 >> sh) & 0x0f0f0f0fu) | (((x1 >> (sh + 2)) & 0x03030303u) << 4));
     }
 }
 
-// Shared memory of k_pre_gemm: the A operands of the tile for one
-// 256-column block, operand-major so both the direct-to-LDS staging (64 lanes
-// write 1 KB contiguously) and the operand reads (lane l reads 16 B at l) are
+// Shared memory of k_pre_gemm: the A operands of the tile for one 256-column
+// block, operand-major so both the direct-to-LDS staging (64 lanes write 1 KB
+// contiguously) and the operand reads (lane l reads 16 B at l) are
 // conflict-free; then the raw weight block bytes of the workgroup's rows.
 struct GemmLds {
     uint4 a[2][2][8][64];        // [hi, lo][row group][sub-block][lane]
-    float part[4][kPM];          // epilogue: per-wave 16-column sums of mid
-    uint32_t raw[1];             // kRaw rows x raw_chunks(F) x 16 B
+    float part[4][kPM];          // epilogue: per-wave 16-row sums of mid
+    uint32_t raw[1];             // rows x raw_chunks(F) x 16 B
 };
 
-// MODE 0: gate/up of 64 intermediate rows; MODE 1: down of 128 hidden rows.
-// Block (tile, row group). Wave w: row tiles {2w, 2w+1} of 16 rows (MODE 0:
-// gate and up rows 16w .. 16w+15 of the group; MODE 1: rows 32w .. 32w+31).
 template <int MODE, int F>
-__global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
+__host__ __device__ constexpr int gemm_rt() {   // row tiles per wave
+    return (F == F_Q6K) ? 2 : 4;                  // Q6_K blocks need more LDS
+}
+
+// The products of one block for NG row groups of entries (g < NG) and RT row
+// tiles: acc[g][r] += sum over sub-blocks of d*sc * (codes . x), plus the
+// bias / minimum corrections from one MFMA each against the 3-part sums.
+template <int F, int RT, int NG>
+__device__ __forceinline__ void gemm_block(const GemmLds& S, const uint32_t* raw,
+                                           const uint32_t (&R)[RT], uint32_t q, uint32_t lane,
+                                           const uint4 (&sxa)[2], f32x4 (&acc)[2][RT]) {
+    constexpr float bias = F == F_Q6K ? 160.f : 128.f;
+    TileScales ts[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        uint4 bsc, bmin;
+        tile_scales<F>(raw, R[r], q, ts[r], bsc, bmin);
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+            const f32x4 u = mfma(sxa[g], bsc, f32x4{0.f, 0.f, 0.f, 0.f});
+            const float cb = -bias * ts[r].d;
+#pragma unroll
+            for (int j = 0; j < 4; j++) acc[g][r][j] = fmaf(cb, u[j], acc[g][r][j]);
+            if (F != F_Q6K) {
+                const f32x4 v = mfma(sxa[g], bmin, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[g][r][j] = fmaf(-ts[r].dmin, v[j], acc[g][r][j]);
+            }
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 4; p++) {
+        uint4 b[RT][2];
+#pragma unroll
+        for (int r = 0; r < RT; r++) tile_codes<F>(raw, R[r], q, p, b[r][0], b[r][1]);
+#pragma unroll
+        for (int g = 0; g < NG; g++) {
+#pragma unroll
+            for (int t = 0; t < 2; t++) {
+                const int sb = 2 * p + t;
+                const uint4 ah = S.a[0][g][sb][lane], al = S.a[1][g][sb][lane];
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+                    f32x4 c = mfma(ah, b[r][t], f32x4{0.f, 0.f, 0.f, 0.f});
+                    c = mfma(al, b[r][t], c);
+#pragma unroll
+                    for (int j = 0; j < 4; j++) acc[g][r][j] = fmaf(ts[r].dsc[sb], c[j], acc[g][r][j]);
+                }
+            }
+        }
+    }
+}
+
+// MODE 0: gate/up; wave w holds RT/2 gate tiles and the RT/2 up tiles of the
+// same 8 RT intermediate rows (block rows: 32 RT). MODE 1: down; wave w holds
+// RT tiles of 16 hidden rows (block rows: 64 RT). Block (tile, row group).
+template <int MODE, int F>
+__global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
+    constexpr int RT = gemm_rt<MODE, F>();
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     GemmLds& S = *(GemmLds*)smem;
     const uint32_t ntile = *ws.n_tiles;
@@ -335,8 +388,9 @@ __global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws)
     const uint32_t nblk = K / 256;
     constexpr uint32_t NCH = raw_chunks(F);
     constexpr uint32_t bb = fmt_block_bytes(F);
+    constexpr uint32_t ROWS = 64 * RT;   // weight rows staged per block
     const uint32_t rb = nblk * bb;
-    const uint32_t r0 = blockIdx.y * (MODE == 0 ? 64u : 128u);
+    const uint32_t r0 = blockIdx.y * (MODE == 0 ? 32u * RT : 64u * RT);
     const uint8_t* m0;
     const uint8_t* m1 = nullptr;
     if (MODE == 0) {
@@ -348,25 +402,32 @@ __global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws)
         m0 = shared ? L.sd.p : L.pk[2].regular ? L.pk[2].base + L.pk[2].stride * mid_e
                                                : L.experts[mid_e].p[2];
     }
+    // staged row rr of the block: MODE 0 gate rows [0, ROWS/2), up rows after
     auto row_ptr = [&](uint32_t rr) -> const uint8_t* {
-        if (MODE == 0) return rr < 64 ? m0 + (size_t)(r0 + rr) * rb : m1 + (size_t)(r0 + rr - 64) * rb;
+        if (MODE == 0)
+            return rr < ROWS / 2 ? m0 + (size_t)(r0 + rr) * rb : m1 + (size_t)(r0 + rr - ROWS / 2) * rb;
         return m0 + (size_t)(r0 + rr) * rb;
     };
-    uint32_t rrow[2];
-    if (MODE == 0) { rrow[0] = 16 * wave + n; rrow[1] = 64 + 16 * wave + n; }
-    else { rrow[0] = 32 * wave + n; rrow[1] = 32 * wave + 16 + n; }
-    const uint32_t bias = F == F_Q6K ? 160u : 128u;
+    uint32_t rrow[RT];
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        if (MODE == 0)
+            rrow[r] = (r < RT / 2 ? 0u : ROWS / 2) + 8 * RT * wave + 16 * (r % (RT / 2)) + n;
+        else
+            rrow[r] = 16 * RT * wave + 16 * r + n;
+    }
     const uint32_t ngrp = (cnt + 15) / 16;   // 16-entry row groups in use
 
-    // activation rows: A staging of wave w covers (hi/lo = w / 2, group w % 2);
-    // lane l stages entry 16 g + l % 16 (clamped into the tile), columns
-    // 8 (l / 16) .. + 8 of each sub-block
+    // A staging: wave w covers (hi/lo = w / 2, group w % 2); lane l stages
+    // entry 16 g + l % 16 (clamped into the tile), columns 8 (l / 16) .. + 8 of
+    // each sub-block
     const uint32_t sg_hl = wave >> 1, sg_g = wave & 1u;
     const uint32_t sm = min(16 * sg_g + n, cnt - 1);
     const uint16_t* arow;
     if (MODE == 0) arow = (sg_hl ? ws.xl : ws.xh) + (size_t)ws.ent_tok[ent0 + sm] * L.hidden;
     else arow = (sg_hl ? ws.mid_l : ws.mid_h) + (size_t)(ent0 + sm) * L.inter;
-    // sub-block sums: lane (m, q == 0) of group g reads those of entry 16 g + m
+    // 3-part sub-block sums as MFMA A operands: lane (m, q < 3) of group g
+    // holds part q of entry 16 g + m's eight sums of the block
     const uint16_t* srow[2];
 #pragma unroll
     for (uint32_t g = 0; g < 2; g++) {
@@ -375,16 +436,16 @@ __global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws)
                             : ws.ms3 + (size_t)(ent0 + m) * (L.inter / 256) * 24;
     }
 
-    f32x4 acc[2][2];
+    f32x4 acc[2][RT];
 #pragma unroll
     for (int g = 0; g < 2; g++)
 #pragma unroll
-        for (int r = 0; r < 2; r++) acc[g][r] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < RT; r++) acc[g][r] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     for (uint32_t kb = 0; kb < nblk; kb++) {
-        // raw block bytes of the 128 rows, 16-B chunks from each row block's
+        // raw block bytes of the ROWS rows, 16-B chunks from each row block's
         // aligned start (only chunks that hold bytes of the block)
-        for (uint32_t c0 = wave * 64; c0 < kRaw * NCH; c0 += kPWG) {
+        for (uint32_t c0 = wave * 64; c0 < ROWS * NCH; c0 += kPWG) {
             const uint32_t c = c0 + lane;
             const uint32_t rr = c / NCH, ch = c % NCH;
             const uint8_t* p = row_ptr(rr) + (size_t)kb * bb;
@@ -400,58 +461,25 @@ __global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws)
                     (glb_void_t*)(arow + kb * 256 + 32 * sb + 8 * q),
                     (lds_void_t*)&S.a[sg_hl][sg_g][sb][0], 16, 0, 0);
         }
-        // sub-block sums of this block (lanes q == 0)
-        uint4 sx3[2][3];
+        uint4 sxa[2];
 #pragma unroll
         for (uint32_t g = 0; g < 2; g++)
-#pragma unroll
-            for (int p3 = 0; p3 < 3; p3++)
-                sx3[g][p3] = (q == 0 && g < ngrp) ? *(const uint4*)(srow[g] + kb * 24 + 8 * p3)
-                                                  : u4(0, 0, 0, 0);
+            sxa[g] = (q < 3 && g < ngrp) ? *(const uint4*)(srow[g] + kb * 24 + 8 * q) : u4(0, 0, 0, 0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        BTile bt[2];
+        uint32_t R[RT];
 #pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const uint32_t R = rrow[r] * NCH * 16 + ((uintptr_t)(row_ptr(rrow[r]) + (size_t)kb * bb) & 15u);
-            decode_btile<F>(S.raw, R, q, bt[r]);
-        }
-        for (uint32_t g = 0; g < ngrp; g++) {
-#pragma unroll
-            for (int sb = 0; sb < 8; sb++) {
-                const uint4 ah = S.a[0][g][sb][lane], al = S.a[1][g][sb][lane];
-#pragma unroll
-                for (int r = 0; r < 2; r++) {
-                    f32x4 c = mfma(ah, bt[r].b[sb], f32x4{0.f, 0.f, 0.f, 0.f});
-                    c = mfma(al, bt[r].b[sb], c);
-#pragma unroll
-                    for (int j = 0; j < 4; j++) acc[g][r][j] = fmaf(bt[r].dsc[sb], c[j], acc[g][r][j]);
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 2; r++) {
-                f32x4 u = mfma(sx3[g][0], bt[r].bsc, f32x4{0.f, 0.f, 0.f, 0.f});
-                u = mfma(sx3[g][1], bt[r].bsc, u);
-                u = mfma(sx3[g][2], bt[r].bsc, u);
-                const float cb = -(float)bias * bt[r].d;
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[g][r][j] = fmaf(cb, u[j], acc[g][r][j]);
-                if (F != F_Q6K) {
-                    f32x4 v = mfma(sx3[g][0], bt[r].bmin, f32x4{0.f, 0.f, 0.f, 0.f});
-                    v = mfma(sx3[g][1], bt[r].bmin, v);
-                    v = mfma(sx3[g][2], bt[r].bmin, v);
-#pragma unroll
-                    for (int j = 0; j < 4; j++) acc[g][r][j] = fmaf(-bt[r].dmin, v[j], acc[g][r][j]);
-                }
-            }
-        }
+        for (int r = 0; r < RT; r++)
+            R[r] = rrow[r] * NCH * 16 + (uint32_t)((uintptr_t)(row_ptr(rrow[r]) + (size_t)kb * bb) & 15u);
+        if (ngrp > 1) gemm_block<F, RT, 2>(S, S.raw, R, q, lane, sxa, acc);
+        else gemm_block<F, RT, 1>(S, S.raw, R, q, lane, sxa, acc);
         __syncthreads();   // LDS is restaged for the next block
     }
 
-    // epilogue: lane holds entries 16 g + 4 q + j of row n of its two tiles
+    // epilogue: lane holds entries 16 g + 4 q + j of row n of its tiles
     if (MODE == 0) {
-        // mid = silu(gate) * up as bf16 hi / lo, plus its 32-column sums: this
-        // wave's 16 columns are half of sub-block (r0 + 16 wave) / 32
+        // mid = silu(gate) * up as bf16 hi / lo, plus the 32-row sums of mid:
+        // wave w's 8 RT rows are part of sub-block (r0 + 8 RT w) / 32
         float part[2][4];
 #pragma unroll
         for (uint32_t g = 0; g < 2; g++)
@@ -459,16 +487,19 @@ __global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws)
             for (int j = 0; j < 4; j++) {
                 const uint32_t m = 16 * g + 4 * q + j;
                 float hsum = 0.f;
-                if (g < ngrp && m < cnt) {
-                    const float gv = acc[g][0][j], uv = acc[g][1][j];
-                    const float y = gv / (1.0f + expf(-gv)) * uv;
-                    const __bf16 h = (__bf16)y, l = (__bf16)(y - (float)h);
-                    const size_t o = (size_t)(ent0 + m) * L.inter + r0 + 16 * wave + n;
-                    ws.mid_h[o] = __builtin_bit_cast(uint16_t, h);
-                    ws.mid_l[o] = __builtin_bit_cast(uint16_t, l);
-                    hsum = (float)h + (float)l;
+#pragma unroll
+                for (int r = 0; r < RT / 2; r++) {
+                    if (g < ngrp && m < cnt) {
+                        const float gv = acc[g][r][j], uv = acc[g][r + RT / 2][j];
+                        const float y = gv / (1.0f + expf(-gv)) * uv;
+                        const __bf16 h = (__bf16)y, l = (__bf16)(y - (float)h);
+                        const size_t o = (size_t)(ent0 + m) * L.inter + r0 + 8 * RT * wave + 16 * r + n;
+                        ws.mid_h[o] = __builtin_bit_cast(uint16_t, h);
+                        ws.mid_l[o] = __builtin_bit_cast(uint16_t, l);
+                        hsum += (float)h + (float)l;
+                    }
                 }
-                part[g][j] = group_sum<16>(hsum);   // over the 16 columns (lanes n)
+                part[g][j] = group_sum<16>(hsum);   // over the 16 rows n
             }
         if (n == 0) {
 #pragma unroll
@@ -477,11 +508,17 @@ __global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws)
                 for (int j = 0; j < 4; j++) S.part[wave][16 * g + 4 * q + j] = part[g][j];
         }
         __syncthreads();
-        if (tid < 2 * kPM) {   // (sub-block half h of the group, entry m)
+        // sub-block sums: the 32 rows of a sub-block are 32 / (8 RT) waves' rows
+        constexpr uint32_t WPS = 4 / RT;                  // waves per sub-block
+        constexpr uint32_t NSB = 4 / WPS;                 // sub-blocks per block
+        if (tid < NSB * kPM) {
             const uint32_t hh = tid / kPM, m = tid % kPM;
             if (m < cnt) {
+                float v = 0.f;
+#pragma unroll
+                for (uint32_t w = 0; w < WPS; w++) v += S.part[WPS * hh + w][m];
                 uint16_t p3[3];
-                split3(S.part[2 * hh][m] + S.part[2 * hh + 1][m], p3);
+                split3(v, p3);
                 const uint32_t sbg = (r0 + 32 * hh) / 32;   // sub-block index in the row
                 uint16_t* dst = ws.ms3 + ((size_t)(ent0 + m) * (L.inter / 256) + sbg / 8) * 24 + sbg % 8;
                 dst[0] = p3[0]; dst[8] = p3[1]; dst[16] = p3[2];
@@ -497,8 +534,9 @@ __global__ __launch_bounds__(kPWG) void k_pre_gemm(PrefillLayer L, PrefillWs ws)
                 if (m >= cnt) continue;
                 const uint32_t e = ent0 + m;
                 const float w = ws.ent_w[e];
-                ws.ybuf[(size_t)e * L.hidden + r0 + 32 * wave + n] = w * acc[g][0][j];
-                ws.ybuf[(size_t)e * L.hidden + r0 + 32 * wave + 16 + n] = w * acc[g][1][j];
+#pragma unroll
+                for (int r = 0; r < RT; r++)
+                    ws.ybuf[(size_t)e * L.hidden + r0 + 16 * RT * wave + 16 * r + n] = w * acc[g][r][j];
             }
         }
     }
@@ -574,14 +612,21 @@ __global__ __launch_bounds__(64) void k_pre_router(const float* __restrict__ rou
     }
 }
 
+template <int MODE, int F>
+void launch_gemm_f(const PrefillLayer& L, const PrefillWs& ws, uint32_t grid_x, hipStream_t st) {
+    constexpr int RT = gemm_rt<MODE, F>();
+    const size_t lds = offsetof(GemmLds, raw) + (size_t)64 * RT * raw_chunks(F) * 16;
+    const uint32_t grid_y = MODE == 0 ? L.inter / (32 * RT) : L.hidden / (64 * RT);
+    k_pre_gemm<MODE, F><<<dim3(grid_x, grid_y), kPWG, lds, st>>>(L, ws);
+}
+
 template <int MODE>
 int launch_gemm(int f, const PrefillLayer& L, const PrefillWs& ws, uint32_t grid_x,
-                uint32_t grid_y, hipStream_t st) {
-    const size_t lds = offsetof(GemmLds, raw) + (size_t)kRaw * raw_chunks(f) * 16;
+                hipStream_t st) {
     switch (f) {
-    case F_Q4K: k_pre_gemm<MODE, F_Q4K><<<dim3(grid_x, grid_y), kPWG, lds, st>>>(L, ws); break;
-    case F_Q5K: k_pre_gemm<MODE, F_Q5K><<<dim3(grid_x, grid_y), kPWG, lds, st>>>(L, ws); break;
-    case F_Q6K: k_pre_gemm<MODE, F_Q6K><<<dim3(grid_x, grid_y), kPWG, lds, st>>>(L, ws); break;
+    case F_Q4K: launch_gemm_f<MODE, F_Q4K>(L, ws, grid_x, st); break;
+    case F_Q5K: launch_gemm_f<MODE, F_Q5K>(L, ws, grid_x, st); break;
+    case F_Q6K: launch_gemm_f<MODE, F_Q6K>(L, ws, grid_x, st); break;
     default: return qw6_fail("batched path: unsupported weight format %d", f);
     }
     const hipError_t e = hipGetLastError();
@@ -598,7 +643,7 @@ uint32_t prefill_tiles_max(uint32_t T, uint32_t top_k, uint32_t n_experts) {
 bool prefill_supports(int f) { return f == F_Q4K || f == F_Q5K || f == F_Q6K; }
 
 int prefill_forward(const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) {
-    if (L.hidden % 256 || L.inter % 256 || L.inter % 64 || L.hidden % 128)
+    if (L.hidden % 256 || L.inter % 256)
         return qw6_fail("batched path needs hidden, inter multiples of 256");
     if (!prefill_supports(L.fmt_gu) || !prefill_supports(L.fmt_dn))
         return qw6_fail("batched path: unsupported expert format");
@@ -622,8 +667,8 @@ int prefill_forward(const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return qw6_fail("batched routing launch: %s", hipGetErrorString(e));
     const uint32_t nt = prefill_tiles_max(L.T, L.top_k, L.n_experts);
-    if (launch_gemm<0>(L.fmt_gu, Lx, ws, nt, L.inter / 64, st)) return -1;
-    if (launch_gemm<1>(L.fmt_dn, Lx, ws, nt, L.hidden / 128, st)) return -1;
+    if (launch_gemm<0>(L.fmt_gu, Lx, ws, nt, st)) return -1;
+    if (launch_gemm<1>(L.fmt_dn, Lx, ws, nt, st)) return -1;
     k_pre_combine<<<dim3(L.T, (L.hidden / 4 + 255) / 256), 256, 0, st>>>(Lx, ws);
     e = hipGetLastError();
     if (e != hipSuccess) return qw6_fail("batched combine launch: %s", hipGetErrorString(e));

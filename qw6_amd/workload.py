@@ -17,8 +17,14 @@ from . import synth_blocks, synth_normal
 MIXES = {
     "q4k": (S.Q_Q4_K_M, lambda e: S.Q_Q6_K),
     "iq2m": (S.Q_IQ2_XXS, lambda e: S.Q_IQ3_S if e % 2 == 0 else S.Q_IQ2_S),
+    # further K-quant combinations (format coverage of the batched path)
+    "q5k": (S.Q_Q5_K, lambda e: S.Q_Q5_K),
+    "q6q4": (S.Q_Q6_K, lambda e: S.Q_Q4_K_M),
 }
 SHARED_Q = (S.Q_Q4_K_M, S.Q_Q4_K_M, S.Q_Q6_K)
+# shared expert formats where they differ from SHARED_Q: the same formats as
+# the routed experts
+SHARED_Q_MIX = {"q5k": (S.Q_Q5_K, S.Q_Q5_K, S.Q_Q5_K), "q6q4": (S.Q_Q6_K, S.Q_Q6_K, S.Q_Q4_K_M)}
 
 
 def _align(n: int, a: int = 256) -> int:
@@ -63,7 +69,8 @@ class SynthLayer:
         self.shared_bufs = []
         if shared:
             sh = []
-            for k, q, kind in zip(range(3), SHARED_Q, (S.K_SGATE, S.K_SUP, S.K_SDOWN)):
+            for k, q, kind in zip(range(3), SHARED_Q_MIX.get(mix, SHARED_Q),
+                                  (S.K_SGATE, S.K_SUP, S.K_SDOWN)):
                 r, c = shapes[k]
                 buf = torch.empty(S.row_bytes(q, c) * r, dtype=torch.uint8, device=dev)
                 synth_blocks(buf, q, r * c // 256, seed, S.stream_id(layer, kind))

@@ -99,6 +99,32 @@ def test_grouped_given_logits_vs_oracle(torch_dev, ctx, layer):
     assert np.mean(rels) <= TOL_MEAN
 
 
+@pytest.mark.parametrize("mix", ["q5k", "q6q4"])
+def test_grouped_other_formats_vs_oracle(torch_dev, ctx, mix):
+    """Q5_K gate/up/down, and Q6_K gate/up with Q4_K down, through the grouped
+    kernels (T = 48, given logits, shared expert of the same formats)."""
+    from qw6_amd.workload import SynthLayer
+    L = SynthLayer(ctx, 71, 0, mix)
+    try:
+        T = 48
+        lg = S.zipf_logits(72, T)
+        xs = np.stack([cases.token_x(71, 5, t) for t in range(T)])
+        say("grouped %s T=%d" % (mix, T))
+        out, idx, _ = run(torch_dev, ctx, L, xs, logits=lg)
+        toks = list(range(0, T, 3))
+        want = oracle_tokens(L, xs, lg, toks)
+        rels = []
+        for t in toks:
+            oo, oi, _ = want[t]
+            assert np.array_equal(idx[t], oi), t
+            rels.append(cases.rel_l2(out[t], oo))
+        say("rel-L2 max %.2e mean %.2e" % (max(rels), np.mean(rels)))
+        assert max(rels) <= TOL_BF16
+        assert np.mean(rels) <= TOL_MEAN
+    finally:
+        L.free()
+
+
 def test_grouped_router_and_norm_vs_oracle(torch_dev, ctx):
     """Router GEMV and the fused RMSNorm on the batched path (T = 40)."""
     torch = torch_dev
