@@ -45,8 +45,9 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // register-resident 16 B
 
-constexpr uint32_t kPM = 32;      // entries per tile (2 MFMA row groups of 16)
+constexpr uint32_t kPM = 16;      // entries per tile (one MFMA row group)
 constexpr uint32_t kPWG = 256;    // threads per workgroup (4 waves)
 
 // 16-B chunks per staged row block: Q4_K / Q5_K blocks (144 / 176 B) of
@@ -228,23 +229,35 @@ struct TileScales {
 };
 
 // The sub-block scales (and minimums) of row n as B operands over k =
-// 8 q' + j (j = sub-block), replicated in lanes q' = 0, 1, 2 (one per bf16
-// part of the activation sums) and zero in q' = 3.
+// 8 q' + j (j = sub-block): lanes q' = 0, 1, 2 pair them with the three bf16
+// parts of the activation sums; lanes q' = 3 meet a zero A operand.
+// bf16 pair of two small integral floats (their low 16 bits are zero).
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
+}
+
 template <int F>
-__device__ __forceinline__ void tile_scales(const uint32_t* s, uint32_t R, uint32_t q,
-                                            TileScales& ts, uint4& bsc, uint4& bmin) {
+__device__ __forceinline__ void tile_scales(const uint32_t* s, uint32_t R, TileScales& ts,
+                                            uint4& bsc, uint4& bmin) {
     float sc[8], mn[8];
     if (F == F_Q4K || F == F_Q5K) {
         const uint4 hd = *(const uint4*)(s + (R >> 2));   // 16-byte aligned block
         ts.d = h2f(hd.x & 0xffffu);
         ts.dmin = h2f(hd.x >> 16);
+        // qw6_get_scale_min_k4 (qw6.c:1480-1490) for all eight sub-blocks at
+        // once, four 6-bit values per word: j < 4 from the low 6 bits of bytes
+        // 0-3 (scales) and 4-7 (minimums); j >= 4 from the nibbles of bytes
+        // 8-11 with the top two bits of bytes j - 4 and j
         const uint32_t A = hd.y, B = hd.z, C = hd.w;
+        const uint32_t sc_lo = A & 0x3f3f3f3fu, mn_lo = B & 0x3f3f3f3fu;
+        const uint32_t sc_hi = (C & 0x0f0f0f0fu) | ((A >> 2) & 0x30303030u);
+        const uint32_t mn_hi = ((C >> 4) & 0x0f0f0f0fu) | ((B >> 2) & 0x30303030u);
 #pragma unroll
-        for (int j = 0; j < 4; j++) {   // qw6_get_scale_min_k4 (qw6.c:1480-1490)
-            sc[j] = (float)((A >> (8 * j)) & 63u);
-            mn[j] = (float)((B >> (8 * j)) & 63u);
-            sc[j + 4] = (float)(((C >> (8 * j)) & 15u) | (((A >> (8 * j + 6)) & 3u) << 4));
-            mn[j + 4] = (float)(((C >> (8 * j + 4)) & 15u) | (((B >> (8 * j + 6)) & 3u) << 4));
+        for (int j = 0; j < 4; j++) {
+            sc[j] = ub(sc_lo, j);
+            sc[j + 4] = ub(sc_hi, j);
+            mn[j] = ub(mn_lo, j);
+            mn[j + 4] = ub(mn_hi, j);
         }
     } else {   // Q6_K: sub-block 4h + k uses scale 8h + 2k (qw6.c:1550-1578)
         ts.d = h2f(lds16(s, R + 208));
@@ -262,12 +275,10 @@ __device__ __forceinline__ void tile_scales(const uint32_t* s, uint32_t R, uint3
     }
 #pragma unroll
     for (int j = 0; j < 8; j++) ts.dsc[j] = ts.d * sc[j];
-    auto pk = [](float a, float b) { return bf16_bits(a) | (bf16_bits(b) << 16); };
-    const bool on = q < 3;
-    bsc = on ? u4(pk(sc[0], sc[1]), pk(sc[2], sc[3]), pk(sc[4], sc[5]), pk(sc[6], sc[7]))
-             : u4(0, 0, 0, 0);
-    bmin = (on && F != F_Q6K) ? u4(pk(mn[0], mn[1]), pk(mn[2], mn[3]), pk(mn[4], mn[5]), pk(mn[6], mn[7]))
-                              : u4(0, 0, 0, 0);
+    bsc = u4(pk_bf16(sc[0], sc[1]), pk_bf16(sc[2], sc[3]), pk_bf16(sc[4], sc[5]), pk_bf16(sc[6], sc[7]));
+    bmin = F != F_Q6K ? u4(pk_bf16(mn[0], mn[1]), pk_bf16(mn[2], mn[3]), pk_bf16(mn[4], mn[5]),
+                           pk_bf16(mn[6], mn[7]))
+                      : u4(0, 0, 0, 0);
 }
 
 // Codes of sub-blocks 2p and 2p + 1 of row n (this lane's 8 columns of each).
@@ -306,12 +317,11 @@ __device__ __forceinline__ void tile_codes(const uint32_t* s, uint32_t R, uint32
 }
 
 // Shared memory of k_pre_gemm: the A operands of the tile for one 256-column
-// block, operand-major so both the direct-to-LDS staging (64 lanes write 1 KB
-// contiguously) and the operand reads (lane l reads 16 B at l) are
+// block, operand-major so the operand reads (lane l reads 16 B at l) are
 // conflict-free; then the raw weight block bytes of the workgroup's rows.
 struct GemmLds {
-    uint4 a[2][2][8][64];        // [hi, lo][row group][sub-block][lane]
-    float part[4][kPM];          // epilogue: per-wave 16-row sums of mid
+    uint4 a[2][8][64];           // [hi, lo][sub-block][lane]
+    float part[4][kPM];          // epilogue: per-wave sums of mid
     uint32_t raw[1];             // rows x raw_chunks(F) x 16 B
 };
 
@@ -320,66 +330,97 @@ __host__ __device__ constexpr int gemm_rt() {   // row tiles per wave
     return (F == F_Q6K) ? 2 : 4;                  // Q6_K blocks need more LDS
 }
 
-// The products of one block for NG row groups of entries (g < NG) and RT row
-// tiles: acc[g][r] += sum over sub-blocks of d*sc * (codes . x), plus the
-// bias / minimum corrections from one MFMA each against the 3-part sums.
-template <int F, int RT, int NG>
-__device__ __forceinline__ void gemm_block(const GemmLds& S, const uint32_t* raw,
-                                           const uint32_t (&R)[RT], uint32_t q, uint32_t lane,
-                                           const uint4 (&sxa)[2], f32x4 (&acc)[2][RT]) {
+// The products of one block for RT row tiles: acc[r] += sum over sub-blocks
+// of d*sc * (codes . x), plus the bias / minimum corrections from one MFMA
+// each against the 3-part sums (sxa: A operand, zero in lanes q = 3).
+template <int F, int RT>
+__device__ __forceinline__ void gemm_block(const GemmLds& S, const uint32_t (&R)[RT], uint32_t lane,
+                                           const uint4& sxa, f32x4 (&acc)[RT]) {
     constexpr float bias = F == F_Q6K ? 160.f : 128.f;
+    const uint32_t q = lane >> 4;
     TileScales ts[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) {
         uint4 bsc, bmin;
-        tile_scales<F>(raw, R[r], q, ts[r], bsc, bmin);
+        tile_scales<F>(S.raw, R[r], ts[r], bsc, bmin);
+        const f32x4 u = mfma(sxa, bsc, f32x4{0.f, 0.f, 0.f, 0.f});
+        const float cb = -bias * ts[r].d;
 #pragma unroll
-        for (int g = 0; g < NG; g++) {
-            const f32x4 u = mfma(sxa[g], bsc, f32x4{0.f, 0.f, 0.f, 0.f});
-            const float cb = -bias * ts[r].d;
+        for (int j = 0; j < 4; j++) acc[r][j] = fmaf(cb, u[j], acc[r][j]);
+        if (F != F_Q6K) {
+            const f32x4 v = mfma(sxa, bmin, f32x4{0.f, 0.f, 0.f, 0.f});
 #pragma unroll
-            for (int j = 0; j < 4; j++) acc[g][r][j] = fmaf(cb, u[j], acc[g][r][j]);
-            if (F != F_Q6K) {
-                const f32x4 v = mfma(sxa[g], bmin, f32x4{0.f, 0.f, 0.f, 0.f});
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[g][r][j] = fmaf(-ts[r].dmin, v[j], acc[g][r][j]);
-            }
+            for (int j = 0; j < 4; j++) acc[r][j] = fmaf(-ts[r].dmin, v[j], acc[r][j]);
         }
     }
 #pragma unroll
     for (int p = 0; p < 4; p++) {
         uint4 b[RT][2];
 #pragma unroll
-        for (int r = 0; r < RT; r++) tile_codes<F>(raw, R[r], q, p, b[r][0], b[r][1]);
+        for (int r = 0; r < RT; r++) tile_codes<F>(S.raw, R[r], q, p, b[r][0], b[r][1]);
 #pragma unroll
-        for (int g = 0; g < NG; g++) {
+        for (int t = 0; t < 2; t++) {
+            const int sb = 2 * p + t;
+            const uint4 ah = S.a[0][sb][lane], al = S.a[1][sb][lane];
 #pragma unroll
-            for (int t = 0; t < 2; t++) {
-                const int sb = 2 * p + t;
-                const uint4 ah = S.a[0][g][sb][lane], al = S.a[1][g][sb][lane];
+            for (int r = 0; r < RT; r++) {
+                f32x4 c = mfma(ah, b[r][t], f32x4{0.f, 0.f, 0.f, 0.f});
+                c = mfma(al, b[r][t], c);
 #pragma unroll
-                for (int r = 0; r < RT; r++) {
-                    f32x4 c = mfma(ah, b[r][t], f32x4{0.f, 0.f, 0.f, 0.f});
-                    c = mfma(al, b[r][t], c);
-#pragma unroll
-                    for (int j = 0; j < 4; j++) acc[g][r][j] = fmaf(ts[r].dsc[sb], c[j], acc[g][r][j]);
-                }
+                for (int j = 0; j < 4; j++) acc[r][j] = fmaf(ts[r].dsc[sb], c[j], acc[r][j]);
             }
         }
     }
 }
 
+// Registers of one 256-column block kb for k_pre_gemm's pipeline: this
+// thread's NR raw 16-B pieces (pieces past a Q6_K block's end reload its first
+// piece; the last piece of a block ends at most 15 bytes past it, inside the
+// matrix, whose size -- a multiple of 256 rows of 16-byte-aligned blocks or of
+// 420-byte Q6_K rows -- is a multiple of 16), its four A operand pieces and
+// its part of the 3-part sums.
+template <int F, uint32_t NR>
+__device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NR],
+                                           const uint32_t (&piece)[NR], const uint16_t* arow,
+                                           const uint16_t* srow, uint32_t sb0, uint32_t q,
+                                           uint32_t kb, u32x4 (&rawv)[NR], u32x4 (&av)[4],
+                                           u32x4& sxv) {
+    constexpr uint32_t bb = fmt_block_bytes(F);
+#pragma unroll
+    for (uint32_t i = 0; i < NR; i++) {
+        const uint8_t* p = rowp[i] + (size_t)kb * bb;
+        const uint32_t off = (uint32_t)((uintptr_t)p & 15u);
+        const uint32_t ch = 16 * piece[i] < off + bb ? piece[i] : 0u;
+        rawv[i] = *(const u32x4*)(p - off + 16 * ch);
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < 4; i++) av[i] = *(const u32x4*)(arow + kb * 256 + 32 * (sb0 + i) + 8 * q);
+    sxv = *(const u32x4*)(srow + kb * 24 + 8 * min(q, 2u));
+}
+
 // MODE 0: gate/up; wave w holds RT/2 gate tiles and the RT/2 up tiles of the
 // same 8 RT intermediate rows (block rows: 32 RT). MODE 1: down; wave w holds
 // RT tiles of 16 hidden rows (block rows: 64 RT). Block (tile, row group).
+// Software pipeline over the 256-column blocks: the raw weight bytes and the
+// A operands of block kb + 1 are loaded into registers while block kb is
+// multiplied, then written to LDS between two barriers.
 template <int MODE, int F>
 __global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
     constexpr int RT = gemm_rt<MODE, F>();
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     GemmLds& S = *(GemmLds*)smem;
-    const uint32_t ntile = *ws.n_tiles;
-    if (blockIdx.x >= ntile) return;
-    const uint4 tile = ws.tiles[blockIdx.x];
+    // XCD-aware work order: workgroup p runs on XCD p % 8 (round-robin
+    // dispatch), so XCD x takes the x-th contiguous range of the (tile, row
+    // block) items -- the row blocks of one tile (same A rows) and the tiles of
+    // one expert (same weights) then share that XCD's L2.
+    const uint32_t ny = MODE == 0 ? L.inter / (32 * RT) : L.hidden / (64 * RT);
+    const uint32_t total = *ws.n_tiles * ny;
+    const uint32_t per_xcd = (total + 7) / 8;
+    const uint32_t slot = blockIdx.x / 8;
+    const uint32_t item = (blockIdx.x % 8) * per_xcd + slot;
+    if (slot >= per_xcd || item >= total) return;
+    const uint32_t ti = item / ny, yb = item % ny;
+    const uint4 tile = ws.tiles[ti];
     const uint32_t mid_e = tile.x, ent0 = tile.y, cnt = tile.z;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
     const uint32_t n = lane & 15u, q = lane >> 4;
@@ -388,9 +429,11 @@ __global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs 
     const uint32_t nblk = K / 256;
     constexpr uint32_t NCH = raw_chunks(F);
     constexpr uint32_t bb = fmt_block_bytes(F);
-    constexpr uint32_t ROWS = 64 * RT;   // weight rows staged per block
+    constexpr uint32_t ROWS = 64 * RT;            // weight rows staged per block
+    constexpr uint32_t NR = ROWS * NCH / kPWG;    // raw chunks per thread
+    static_assert(ROWS * NCH % kPWG == 0, "raw chunks split evenly over the threads");
     const uint32_t rb = nblk * bb;
-    const uint32_t r0 = blockIdx.y * (MODE == 0 ? 32u * RT : 64u * RT);
+    const uint32_t r0 = yb * (MODE == 0 ? 32u * RT : 64u * RT);
     const uint8_t* m0;
     const uint8_t* m1 = nullptr;
     if (MODE == 0) {
@@ -416,96 +459,77 @@ __global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs 
         else
             rrow[r] = 16 * RT * wave + 16 * r + n;
     }
-    const uint32_t ngrp = (cnt + 15) / 16;   // 16-entry row groups in use
 
-    // A staging: wave w covers (hi/lo = w / 2, group w % 2); lane l stages
-    // entry 16 g + l % 16 (clamped into the tile), columns 8 (l / 16) .. + 8 of
-    // each sub-block
-    const uint32_t sg_hl = wave >> 1, sg_g = wave & 1u;
-    const uint32_t sm = min(16 * sg_g + n, cnt - 1);
+    // A operands: thread (wave w, lane l) loads half hl = w / 2 of entry
+    // l % 16 (clamped into the tile), columns 8 (l / 16) .. + 8 of sub-blocks
+    // 4 (w % 2) .. + 4; the 3-part sub-block sums of entry l % 16 (part l / 16)
+    const uint32_t sm = min(n, cnt - 1);
+    const uint32_t hl = wave >> 1, sb0 = 4 * (wave & 1u);
     const uint16_t* arow;
-    if (MODE == 0) arow = (sg_hl ? ws.xl : ws.xh) + (size_t)ws.ent_tok[ent0 + sm] * L.hidden;
-    else arow = (sg_hl ? ws.mid_l : ws.mid_h) + (size_t)(ent0 + sm) * L.inter;
-    // 3-part sub-block sums as MFMA A operands: lane (m, q < 3) of group g
-    // holds part q of entry 16 g + m's eight sums of the block
-    const uint16_t* srow[2];
-#pragma unroll
-    for (uint32_t g = 0; g < 2; g++) {
-        const uint32_t m = min(16 * g + n, cnt - 1);
-        srow[g] = MODE == 0 ? ws.xs3 + (size_t)ws.ent_tok[ent0 + m] * (L.hidden / 256) * 24
-                            : ws.ms3 + (size_t)(ent0 + m) * (L.inter / 256) * 24;
+    const uint16_t* srow;
+    if (MODE == 0) {
+        const uint32_t tok = ws.ent_tok[ent0 + sm];
+        arow = (hl ? ws.xl : ws.xh) + (size_t)tok * L.hidden;
+        srow = ws.xs3 + (size_t)tok * (L.hidden / 256) * 24;
+    } else {
+        arow = (hl ? ws.mid_l : ws.mid_h) + (size_t)(ent0 + sm) * L.inter;
+        srow = ws.ms3 + (size_t)(ent0 + sm) * (L.inter / 256) * 24;
     }
-
-    f32x4 acc[2][RT];
+    const uint8_t* rowp[NR];   // this thread's raw pieces: row block start, piece
+    uint32_t piece[NR];
 #pragma unroll
-    for (int g = 0; g < 2; g++)
+    for (uint32_t i = 0; i < NR; i++) {
+        const uint32_t c = i * kPWG + tid;    // chunk: row c / NCH, 16-B piece c % NCH
+        rowp[i] = row_ptr(c / NCH);
+        piece[i] = c % NCH;
+    }
+    u32x4 rawv[NR], av[4], sxv;
+    f32x4 acc[RT];
 #pragma unroll
-        for (int r = 0; r < RT; r++) acc[g][r] = f32x4{0.f, 0.f, 0.f, 0.f};
-
+    for (int r = 0; r < RT; r++) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    load_block<F, NR>(rowp, piece, arow, srow, sb0, q, 0, rawv, av, sxv);
     for (uint32_t kb = 0; kb < nblk; kb++) {
-        // raw block bytes of the ROWS rows, 16-B chunks from each row block's
-        // aligned start (only chunks that hold bytes of the block)
-        for (uint32_t c0 = wave * 64; c0 < ROWS * NCH; c0 += kPWG) {
-            const uint32_t c = c0 + lane;
-            const uint32_t rr = c / NCH, ch = c % NCH;
-            const uint8_t* p = row_ptr(rr) + (size_t)kb * bb;
-            const uint32_t off = (uint32_t)((uintptr_t)p & 15u);
-            if (16 * ch < off + bb)
-                __builtin_amdgcn_global_load_lds((glb_void_t*)(p - off + 16 * ch),
-                                                 (lds_void_t*)((uint8_t*)S.raw + 16u * c0), 16, 0, 0);
-        }
-        if (sg_g < ngrp) {
+        __syncthreads();   // every wave is done with block kb - 1's LDS data
 #pragma unroll
-            for (uint32_t sb = 0; sb < 8; sb++)
-                __builtin_amdgcn_global_load_lds(
-                    (glb_void_t*)(arow + kb * 256 + 32 * sb + 8 * q),
-                    (lds_void_t*)&S.a[sg_hl][sg_g][sb][0], 16, 0, 0);
-        }
-        uint4 sxa[2];
+        for (uint32_t i = 0; i < NR; i++) *(u32x4*)((uint8_t*)S.raw + 16u * (i * kPWG + tid)) = rawv[i];
 #pragma unroll
-        for (uint32_t g = 0; g < 2; g++)
-            sxa[g] = (q < 3 && g < ngrp) ? *(const uint4*)(srow[g] + kb * 24 + 8 * q) : u4(0, 0, 0, 0);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __syncthreads();
+        for (uint32_t i = 0; i < 4; i++) *(u32x4*)&S.a[hl][sb0 + i][lane] = av[i];
+        const uint4 sxa = q < 3 ? u4(sxv.x, sxv.y, sxv.z, sxv.w) : u4(0, 0, 0, 0);
+        if (kb + 1 < nblk) load_block<F, NR>(rowp, piece, arow, srow, sb0, q, kb + 1, rawv, av, sxv);
+        __syncthreads();   // block kb's bytes are in LDS
         uint32_t R[RT];
 #pragma unroll
         for (int r = 0; r < RT; r++)
             R[r] = rrow[r] * NCH * 16 + (uint32_t)((uintptr_t)(row_ptr(rrow[r]) + (size_t)kb * bb) & 15u);
-        if (ngrp > 1) gemm_block<F, RT, 2>(S, S.raw, R, q, lane, sxa, acc);
-        else gemm_block<F, RT, 1>(S, S.raw, R, q, lane, sxa, acc);
-        __syncthreads();   // LDS is restaged for the next block
+        gemm_block<F, RT>(S, R, lane, sxa, acc);
     }
 
-    // epilogue: lane holds entries 16 g + 4 q + j of row n of its tiles
+    // epilogue: lane holds entries 4 q + j of row n of its tiles
     if (MODE == 0) {
         // mid = silu(gate) * up as bf16 hi / lo, plus the 32-row sums of mid:
         // wave w's 8 RT rows are part of sub-block (r0 + 8 RT w) / 32
-        float part[2][4];
+        float part[4];
 #pragma unroll
-        for (uint32_t g = 0; g < 2; g++)
+        for (int j = 0; j < 4; j++) {
+            const uint32_t m = 4 * q + j;
+            float hsum = 0.f;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t m = 16 * g + 4 * q + j;
-                float hsum = 0.f;
-#pragma unroll
-                for (int r = 0; r < RT / 2; r++) {
-                    if (g < ngrp && m < cnt) {
-                        const float gv = acc[g][r][j], uv = acc[g][r + RT / 2][j];
-                        const float y = gv / (1.0f + expf(-gv)) * uv;
-                        const __bf16 h = (__bf16)y, l = (__bf16)(y - (float)h);
-                        const size_t o = (size_t)(ent0 + m) * L.inter + r0 + 8 * RT * wave + 16 * r + n;
-                        ws.mid_h[o] = __builtin_bit_cast(uint16_t, h);
-                        ws.mid_l[o] = __builtin_bit_cast(uint16_t, l);
-                        hsum += (float)h + (float)l;
-                    }
+            for (int r = 0; r < RT / 2; r++) {
+                if (m < cnt) {
+                    const float gv = acc[r][j], uv = acc[r + RT / 2][j];
+                    const float y = gv / (1.0f + expf(-gv)) * uv;
+                    const __bf16 h = (__bf16)y, l = (__bf16)(y - (float)h);
+                    const size_t o = (size_t)(ent0 + m) * L.inter + r0 + 8 * RT * wave + 16 * r + n;
+                    ws.mid_h[o] = __builtin_bit_cast(uint16_t, h);
+                    ws.mid_l[o] = __builtin_bit_cast(uint16_t, l);
+                    hsum += (float)h + (float)l;
                 }
-                part[g][j] = group_sum<16>(hsum);   // over the 16 rows n
             }
+            part[j] = group_sum<16>(hsum);   // over the 16 rows n
+        }
         if (n == 0) {
 #pragma unroll
-            for (uint32_t g = 0; g < 2; g++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) S.part[wave][16 * g + 4 * q + j] = part[g][j];
+            for (int j = 0; j < 4; j++) S.part[wave][4 * q + j] = part[j];
         }
         __syncthreads();
         // sub-block sums: the 32 rows of a sub-block are 32 / (8 RT) waves' rows
@@ -526,18 +550,14 @@ __global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs 
         }
     } else {
 #pragma unroll
-        for (uint32_t g = 0; g < 2; g++) {
-            if (g >= ngrp) break;
+        for (int j = 0; j < 4; j++) {
+            const uint32_t m = 4 * q + j;
+            if (m >= cnt) continue;
+            const uint32_t e = ent0 + m;
+            const float w = ws.ent_w[e];
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const uint32_t m = 16 * g + 4 * q + j;
-                if (m >= cnt) continue;
-                const uint32_t e = ent0 + m;
-                const float w = ws.ent_w[e];
-#pragma unroll
-                for (int r = 0; r < RT; r++)
-                    ws.ybuf[(size_t)e * L.hidden + r0 + 16 * RT * wave + 16 * r + n] = w * acc[g][r][j];
-            }
+            for (int r = 0; r < RT; r++)
+                ws.ybuf[(size_t)e * L.hidden + r0 + 16 * RT * wave + 16 * r + n] = w * acc[r][j];
         }
     }
 }
@@ -616,8 +636,10 @@ template <int MODE, int F>
 void launch_gemm_f(const PrefillLayer& L, const PrefillWs& ws, uint32_t grid_x, hipStream_t st) {
     constexpr int RT = gemm_rt<MODE, F>();
     const size_t lds = offsetof(GemmLds, raw) + (size_t)64 * RT * raw_chunks(F) * 16;
-    const uint32_t grid_y = MODE == 0 ? L.inter / (32 * RT) : L.hidden / (64 * RT);
-    k_pre_gemm<MODE, F><<<dim3(grid_x, grid_y), kPWG, lds, st>>>(L, ws);
+    const uint32_t ny = MODE == 0 ? L.inter / (32 * RT) : L.hidden / (64 * RT);
+    // grid_x tiles at most; the kernel maps workgroups to the actual items
+    const uint32_t nwg = (grid_x * ny + 7) / 8 * 8;
+    k_pre_gemm<MODE, F><<<nwg, kPWG, lds, st>>>(L, ws);
 }
 
 template <int MODE>
