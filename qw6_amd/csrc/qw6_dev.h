@@ -153,6 +153,12 @@ __device__ __forceinline__ float sgn(float v, uint32_t signs, int n) {
 
 // ---- activations for a unit ------------------------------------------------------
 
+// Activation layout class of a format's units (load_unit_x): Q4_K and Q5_K
+// share one, Q6_K has its own, the IQ formats read 32 contiguous values.
+__host__ __device__ inline int x_layout(int f) {
+    return (f == F_Q4K || f == F_Q5K) ? 0 : f == F_Q6K ? 1 : 2;
+}
+
 // Load the 32 activations of unit j of block blk for format f from x (one
 // token, contiguous), and the partial sums the decoders use.
 __device__ __forceinline__ void load_unit_x(int f, const float* __restrict__ x, uint32_t blk,

@@ -357,6 +357,8 @@ struct MoeArgs {
     uint32_t* idx_out;
     float* w_out;
     uint32_t tmask_gu, tmask_dn;
+    int xl_dn;                    // a format with every routed down matrix's
+                                  // activation layout, or -1 (x_layout)
 };
 
 __device__ __forceinline__ MatD expert_mat(const MoeArgs& a, uint32_t e, int k) {
@@ -396,8 +398,11 @@ __device__ __forceinline__ void wait_vm(uint32_t n) {
     case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
     case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
     case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
+    case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
     case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
+    case 28: asm volatile("s_waitcnt vmcnt(28)" ::: "memory"); break;
     case 32: asm volatile("s_waitcnt vmcnt(32)" ::: "memory"); break;
+    case 36: asm volatile("s_waitcnt vmcnt(36)" ::: "memory"); break;
     default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
     }
 }
@@ -733,26 +738,30 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
         if (has_sh && a.shared_router) shw = a.sw[t];
     }
     const uint32_t ntot = nslot + has_sh;
-    if (a.tmask_dn) {   // the lattice tables are in LDS before any wave reads them
-        wave_wait();
-        __syncthreads();
-    }
+    // every wave has at least one matrix (nw <= ntot): each issues its first
+    // matrix's loads before the barrier that makes the lattice tables visible
     for (uint32_t m = wave; m < ntot; m += nw) {
         const bool sh = has_sh && m == 0;
         const uint32_t u = m - has_sh;
         const float* xm = a.mid + (size_t)(sh ? a.max_u : u) * T * a.inter;
         float xr[T][32], sx[T][4];
-        // activations (independent of the slot table) before the weights
-        if (FD >= 0) load_x_all<T, FD>(FD, xm, a.inter, a.inter, xr, sx);
+        // activations before the slot table's answer when their layout is
+        // known already (one format, the shared expert, or one layout class)
+        const int fx = FD >= 0 ? FD : sh ? a.sd.fmt : a.xl_dn;
+        if (fx >= 0) load_x_all<T, FD>(fx, xm, a.inter, a.inter, xr, sx);
         const MatD D = sh ? a.sd
                           : m == wave ? MatD{p0, f0, a.hidden, a.inter, rb0}
                                       : MatD{a.slots->p[u], a.slots->fmt[u], a.hidden, a.inter,
                                              a.slots->rb[u]};
         const int f = FD >= 0 ? FD : D.fmt;
-        if (FD < 0) load_x_all<T, FD>(f, xm, a.inter, a.inter, xr, sx);
+        if (fx < 0) load_x_all<T, FD>(f, xm, a.inter, a.inter, xr, sx);
 #pragma unroll
         for (int s = 0; s < S; s++)
             stage_group(slots + s * kSlotBytes, D.p + (size_t)(r0 + s * rps) * D.rb, rps * D.rb);
+        if (a.tmask_dn && m == wave) {
+            wait_vm(8u * T + 2u * S);   // this wave's table loads (its oldest) have landed
+            __syncthreads();            // and every other wave's: the tables are complete
+        }
         const uint32_t bb = fmt_block_bytes(f);
         const uint32_t boff = slot_off + q * D.rb + blk * bb;
         float acc[T][S];
@@ -902,6 +911,8 @@ struct qw6_hip_experts_s {
     uint32_t rb_gu_max;   // widest gate/up row in bytes
     uint32_t rb_dn_max;   // widest down row in bytes
     int fmt_gu, fmt_dn;   // the single gate/up (down) format, -1 if mixed
+    int xl_dn;            // a down format whose activation layout every expert's
+                          // down format shares (the IQ formats share one), or -1
     int gu_same;          // every expert's gate and up share a format
     PackRef pk[3];        // regular-pack addressing per matrix kind
 };
@@ -1281,10 +1292,12 @@ int qw6_hip_experts_create(qw6_hip_ctx_t* c, const qw6_hip_matrix_t* gate,
     }
     E->fmt_gu = tab[0].fmt[0];
     E->fmt_dn = tab[0].fmt[2];
+    E->xl_dn = tab[0].fmt[2];
     E->gu_same = 1;
     for (uint32_t e = 0; e < n_experts; e++) {
         if (tab[e].fmt[0] != E->fmt_gu || tab[e].fmt[1] != E->fmt_gu) E->fmt_gu = -1;
         if (tab[e].fmt[2] != E->fmt_dn) E->fmt_dn = -1;
+        if (E->xl_dn >= 0 && x_layout(tab[e].fmt[2]) != x_layout(E->xl_dn)) E->xl_dn = -1;
         if (tab[e].fmt[0] != tab[e].fmt[1]) E->gu_same = 0;
     }
     E->rb_dn_max = rb_dn;
@@ -1547,6 +1560,7 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
     a.logits = c->logits; a.sw = c->sw; a.xn = c->xn; a.mid = c->mid; a.slots = c->slots;
     a.tmask_gu = mgu;
     a.tmask_dn = mdn;
+    a.xl_dn = E->xl_dn;
 
     MoeLaunch m;
     m.fg = (has_sh && sg.fmt != E->fmt_gu) ? -1 : E->fmt_gu;
