@@ -507,14 +507,17 @@ __global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs 
     // epilogue: lane holds entries 4 q + j of row n of its tiles
     if (MODE == 0) {
         // mid = silu(gate) * up as bf16 hi / lo, plus the 32-row sums of mid:
-        // wave w's 8 RT rows are part of sub-block (r0 + 8 RT w) / 32
+        // wave w's 8 RT rows are part of sub-block (r0 + 8 RT w) / 32. Each
+        // 16-row tile is summed over its lanes first and the tiles are added in
+        // row order, so a sub-block's sum rounds the same for every tile shape.
         float part[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint32_t m = 4 * q + j;
-            float hsum = 0.f;
+            float psum = 0.f;
 #pragma unroll
             for (int r = 0; r < RT / 2; r++) {
+                float hs = 0.f;
                 if (m < cnt) {
                     const float gv = acc[r][j], uv = acc[r + RT / 2][j];
                     const float y = gv / (1.0f + expf(-gv)) * uv;
@@ -522,10 +525,11 @@ __global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs 
                     const size_t o = (size_t)(ent0 + m) * L.inter + r0 + 8 * RT * wave + 16 * r + n;
                     ws.mid_h[o] = __builtin_bit_cast(uint16_t, h);
                     ws.mid_l[o] = __builtin_bit_cast(uint16_t, l);
-                    hsum += (float)h + (float)l;
+                    hs = (float)h + (float)l;
                 }
+                psum += group_sum<16>(hs);   // over the 16 rows n of tile r
             }
-            part[j] = group_sum<16>(hsum);   // over the 16 rows n
+            part[j] = psum;
         }
         if (n == 0) {
 #pragma unroll
