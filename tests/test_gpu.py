@@ -360,3 +360,38 @@ def test_in_place_residual_update(torch_dev, ctx, layers):
         ctx.moe_forward(layer, h, h, n_tok=T, residual=h)
         torch.cuda.synchronize()
         assert torch.equal(h, ref)
+
+
+@pytest.mark.parametrize("mix", ["q4k", "iq2m"])
+def test_layer_other_shape_vs_oracle(torch_dev, ctx, mix):
+    """hidden 1024, inter 256, 64 experts, top-4 (the unit-count-generic
+    kernels, fewer experts, top_k < 8): T = 1 and 3 with the router GEMV on the
+    device, against the oracle."""
+    from qw6_amd.workload import SynthLayer
+    L = SynthLayer(ctx, 31, 0, mix, hidden=1024, inter=256, n_experts=64, top_k=4)
+    try:
+        router = L.router_host()
+        checked = 0
+        for T in (1, 3):
+            xs = np.stack([cases.token_x(31, 2, t, hidden=1024) for t in range(T)])
+            out, idx, _ = run_layer(torch_dev, ctx, L, xs)
+            for t in range(T):
+                (oo, oi, _), gap = oracle_for(L, xs[t], router=router)
+                if gap < TIE:
+                    continue
+                assert np.array_equal(idx[t], oi)
+                assert cases.rel_l2(out[t], oo) <= TOL
+                checked += 1
+        assert checked >= 3
+    finally:
+        L.free()
+
+
+def test_zero_tokens_is_a_no_op(torch_dev, ctx, layers):
+    torch = torch_dev
+    L = layers[("q4k", 11)]
+    x = torch.zeros(1, 2048, dtype=torch.float32, device="cuda")
+    out = torch.full((1, 2048), 7.0, dtype=torch.float32, device="cuda")
+    ctx.moe_forward(L.desc, x, out, n_tok=0)
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())

@@ -125,6 +125,31 @@ def test_grouped_other_formats_vs_oracle(torch_dev, ctx, mix):
         L.free()
 
 
+def test_grouped_other_shape_vs_oracle(torch_dev, ctx):
+    """hidden 1024, inter 256, 64 experts, top-4 through the grouped kernels
+    (T = 40, given logits, shared expert), against the oracle."""
+    from qw6_amd.workload import SynthLayer
+    L = SynthLayer(ctx, 33, 0, "q4k", hidden=1024, inter=256, n_experts=64, top_k=4)
+    try:
+        T = 40
+        lg = S.zipf_logits(34, T, n_experts=64)
+        xs = np.stack([cases.token_x(33, 4, t, hidden=1024) for t in range(T)])
+        say("grouped 1024x256 E64 k4 T=%d" % T)
+        out, idx, _ = run(torch_dev, ctx, L, xs, logits=lg)
+        toks = list(range(0, T, 4))
+        want = oracle_tokens(L, xs, lg, toks)
+        rels = []
+        for t in toks:
+            oo, oi, _ = want[t]
+            assert np.array_equal(idx[t], oi), t
+            rels.append(cases.rel_l2(out[t], oo))
+        say("rel-L2 max %.2e mean %.2e" % (max(rels), np.mean(rels)))
+        assert max(rels) <= TOL_BF16
+        assert np.mean(rels) <= TOL_MEAN
+    finally:
+        L.free()
+
+
 def test_grouped_router_and_norm_vs_oracle(torch_dev, ctx):
     """Router GEMV and the fused RMSNorm on the batched path (T = 40)."""
     torch = torch_dev
