@@ -1522,12 +1522,13 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
     hipStream_t st = (hipStream_t)stream;
     // batched tokens: grouped MFMA contraction when every matrix kind has one
     // supported format (qw6_hip_set_mode: 0 automatic, 1 per-token, 2 grouped)
-    const int fgu = (has_sh && sg.fmt != E->fmt_gu) ? -1 : E->fmt_gu;
-    const int fdn = (has_sh && sd.fmt != E->fmt_dn) ? -1 : E->fmt_dn;
+    // (the shared expert's formats may differ from the routed experts')
+    const int fgu = E->fmt_gu, fdn = E->fmt_dn;
     const bool grouped_ok = prefill_supports(fgu) && prefill_supports(fdn) &&
+                            (!has_sh || (prefill_supports(sg.fmt) && prefill_supports(sd.fmt))) &&
                             L->hidden % 256 == 0 && L->inter % 256 == 0;
     if (c->mode == 2 && !grouped_ok)
-        return fail("grouped MFMA path needs one Q4_K / Q5_K / Q6_K format per matrix kind");
+        return fail("grouped MFMA path needs one format per matrix kind across the routed experts");
     if (grouped_ok && (c->mode == 2 || (c->mode == 0 && n_tok >= kGroupedMinTokens))) {
         if (ensure_prefill_ws(c, L->hidden, L->inter, E->n, L->top_k)) return -1;
         PrefillLayer P;

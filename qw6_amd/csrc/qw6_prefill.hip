@@ -43,6 +43,8 @@
 namespace qw6 {
 namespace {
 
+__device__ const IqTables g_tabs_pre = make_tables();
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // register-resident 16 B
@@ -51,10 +53,23 @@ constexpr uint32_t kPM = 16;      // entries per tile (one MFMA row group)
 constexpr uint32_t kPWG = 256;    // threads per workgroup (4 waves)
 
 // 16-B chunks per staged row block: Q4_K / Q5_K blocks (144 / 176 B) of
-// 16-byte aligned rows are 16-byte aligned; a Q6_K block (210 B) may start at
-// any even offset within its first chunk.
+// 16-byte aligned rows are 16-byte aligned; Q6_K (210 B) and IQ blocks (66,
+// 82, 110 B) may start at any even offset within their first chunk.
 __host__ __device__ constexpr uint32_t raw_chunks(int f) {
-    return f == F_Q6K ? (fmt_block_bytes(f) + 14 + 15) / 16 : fmt_block_bytes(f) / 16;
+    return (f == F_Q4K || f == F_Q5K) ? fmt_block_bytes(f) / 16
+                                      : (fmt_block_bytes(f) + 14 + 15) / 16;
+}
+__host__ __device__ constexpr bool is_iq(int f) {
+    return f == F_IQ2XXS || f == F_IQ2S || f == F_IQ3S;
+}
+// LDS of the bf16 lattice tables of an IQ format: the grid (8 or 4 values
+// per entry, 16 or 8 B) then 256 sign masks (16 B: bit j of the sign byte ->
+// the sign bit of bf16 value j).
+__host__ __device__ constexpr uint32_t iq_grid_bytes(int f) {
+    return f == F_IQ2XXS ? 256 * 16 : f == F_IQ2S ? 1024 * 16 : f == F_IQ3S ? 512 * 8 : 0;
+}
+__host__ __device__ constexpr uint32_t iq_tab_bytes(int f) {
+    return is_iq(f) ? iq_grid_bytes(f) + 256 * 16 : 0;
 }
 
 // ---- bf16 operand preparation -----------------------------------------------------
@@ -191,7 +206,10 @@ __global__ __launch_bounds__(1024) void k_pre_sort(PrefillLayer L, PrefillWs ws)
     const uint32_t nsh = L.sg.p ? (L.T + kPM - 1) / kPM : 0u;
     for (uint32_t j = tid; j < nsh; j += blockDim.x)
         ws.tiles[nrt + j] = make_uint4(E, ne + j * kPM, min(kPM, L.T - j * kPM), 0u);
-    if (tid == 0) *ws.n_tiles = nrt + nsh;
+    if (tid == 0) {
+        ws.n_tiles[0] = nrt;
+        ws.n_tiles[1] = nsh;
+    }
 }
 
 // ---- the grouped contraction --------------------------------------------------------
@@ -316,6 +334,89 @@ __device__ __forceinline__ void tile_codes(const uint32_t* s, uint32_t R, uint32
     }
 }
 
+// ---- IQ formats -------------------------------------------------------------------
+// The lattice values are small integers (IQ2: 8, 25, 43; IQ3: odd 1 .. 15),
+// exact in bf16, and every weight is db * (+-value): the B operand is the
+// bf16 grid entry with the sign bits flipped, with no bias or minimum term.
+
+// Expand the lattice tables of format F into LDS as bf16 (all threads).
+template <int F>
+__device__ __forceinline__ void stage_iq_tables(uint8_t* tab) {
+    const uint32_t tid = threadIdx.x;
+    auto bf = [](uint32_t v) { return bf16_bits((float)v); };
+    if (F == F_IQ2XXS || F == F_IQ2S) {
+        const uint32_t n = F == F_IQ2XXS ? 256u : 1024u;
+        const uint64_t* g = F == F_IQ2XXS ? g_tabs_pre.iq2xxs : g_tabs_pre.iq2s;
+        for (uint32_t i = tid; i < n; i += kPWG) {
+            const uint64_t v = g[i];
+            uint32_t w[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                w[k] = bf((uint32_t)(v >> (16 * k)) & 255u) | (bf((uint32_t)(v >> (16 * k + 8)) & 255u) << 16);
+            ((uint4*)tab)[i] = u4(w[0], w[1], w[2], w[3]);
+        }
+    } else {
+        for (uint32_t i = tid; i < 512; i += kPWG) {
+            const uint32_t v = g_tabs_pre.iq3s[i];
+            ((uint2*)tab)[i] = make_uint2(bf(v & 255u) | (bf((v >> 8) & 255u) << 16),
+                                          bf((v >> 16) & 255u) | (bf(v >> 24) << 16));
+        }
+    }
+    uint4* sg = (uint4*)(tab + iq_grid_bytes(F));
+    for (uint32_t s8 = tid; s8 < 256; s8 += kPWG) {
+        uint32_t w[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++)
+            w[k] = (((s8 >> (2 * k)) & 1u) << 15) | (((s8 >> (2 * k + 1)) & 1u) << 31);
+        sg[s8] = u4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+__device__ __forceinline__ uint4 xor4(const uint4& a, const uint4& b) {
+    return u4(a.x ^ b.x, a.y ^ b.y, a.z ^ b.z, a.w ^ b.w);
+}
+
+// B operand of sub-block sb of row n (this lane's 8 weights, group q of the
+// sub-block) and its scale(s): db for all 32 weights, or (IQ2_S) db for
+// groups 0-1 and db2 for groups 2-3 (qw6.c:1580-1672).
+template <int F>
+__device__ __forceinline__ void tile_iq(const uint32_t* s, const uint8_t* tab, uint32_t R,
+                                        uint32_t q, int sb, float d, uint4& b, float& db,
+                                        float& db2) {
+    const uint4* sgn = (const uint4*)(tab + iq_grid_bytes(F));
+    if (F == F_IQ2XXS) {   // 8 B per 32 weights: 4 grid indices, 4 x 7 sign bits + scale
+        const uint32_t aux0 = lds32(s, R + 2 + 8 * sb), aux1 = lds32(s, R + 6 + 8 * sb);
+        const uint32_t idx = (aux0 >> (8 * q)) & 255u;
+        const uint32_t s7 = (aux1 >> (7 * q)) & 127u;
+        const uint32_t sg = s7 | ((__builtin_popcount(s7) & 1u) << 7);   // ksigns_iq2xs
+        b = xor4(((const uint4*)tab)[idx], sgn[sg]);
+        db = d * (0.5f + (float)(aux1 >> 28)) * 0.25f;
+        db2 = db;
+    } else if (F == F_IQ2S) {   // grid index: qs byte + 2 bits of qh; own sign byte
+        const uint32_t qsb = lds8(s, R + 2 + 4 * sb + q);
+        const uint32_t qh = lds8(s, R + 66 + sb);
+        const uint32_t sg = lds8(s, R + 34 + 4 * sb + q);
+        const uint32_t sc = lds8(s, R + 74 + sb);
+        const uint32_t gi = qsb | ((qh << (8 - 2 * q)) & 0x300u);
+        b = xor4(((const uint4*)tab)[gi], sgn[sg]);
+        db = d * (0.5f + (float)(sc & 15u)) * 0.25f;
+        db2 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
+    } else {   // IQ3_S: two 4-value grid entries per 8 weights, 9-bit indices
+        const uint32_t qw = lds32(s, R + 2 + 8 * sb + 4 * (q >> 1));
+        const uint32_t qh = lds8(s, R + 66 + sb);
+        const uint32_t sg = lds8(s, R + 74 + 4 * sb + q);
+        const uint32_t scb = lds8(s, R + 106 + (sb >> 1));
+        const uint32_t nib = (sb & 1) ? (scb >> 4) : (scb & 15u);
+        const uint32_t sh = 16 * (q & 1u);
+        const uint32_t i1 = ((qw >> sh) & 255u) | ((qh << (8 - 2 * q)) & 256u);
+        const uint32_t i2 = ((qw >> (sh + 8)) & 255u) | ((qh << (7 - 2 * q)) & 256u);
+        const uint2 g1 = ((const uint2*)tab)[i1], g2 = ((const uint2*)tab)[i2];
+        b = xor4(u4(g1.x, g1.y, g2.x, g2.y), sgn[sg]);
+        db = d * (float)(1 + 2 * (int)nib);
+        db2 = db;
+    }
+}
+
 // Shared memory of k_pre_gemm: the A operands of the tile for one 256-column
 // block, operand-major so the operand reads (lane l reads 16 B at l) are
 // conflict-free; then the raw weight block bytes of the workgroup's rows.
@@ -327,17 +428,51 @@ struct GemmLds {
 
 template <int MODE, int F>
 __host__ __device__ constexpr int gemm_rt() {   // row tiles per wave
-    return (F == F_Q6K) ? 2 : 4;                  // Q6_K blocks need more LDS
+    return (F == F_Q6K || F == F_IQ3S) ? 2 : 4;   // larger raw blocks: fewer rows
 }
 
 // The products of one block for RT row tiles: acc[r] += sum over sub-blocks
 // of d*sc * (codes . x), plus the bias / minimum corrections from one MFMA
 // each against the 3-part sums (sxa: A operand, zero in lanes q = 3).
 template <int F, int RT>
-__device__ __forceinline__ void gemm_block(const GemmLds& S, const uint32_t (&R)[RT], uint32_t lane,
+__device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
+                                           const uint32_t (&R)[RT], uint32_t lane,
                                            const uint4& sxa, f32x4 (&acc)[RT]) {
     constexpr float bias = F == F_Q6K ? 160.f : 128.f;
     const uint32_t q = lane >> 4;
+    if constexpr (is_iq(F)) {
+        float d[RT];
+#pragma unroll
+        for (int r = 0; r < RT; r++) d[r] = h2f(lds16(S.raw, R[r]));
+#pragma unroll 2
+        for (int sb = 0; sb < 8; sb++) {
+            uint4 b[RT];
+            float db[RT], db2[RT];
+#pragma unroll
+            for (int r = 0; r < RT; r++) tile_iq<F>(S.raw, tab, R[r], q, sb, d[r], b[r], db[r], db2[r]);
+            const uint4 ah = S.a[0][sb][lane], al = S.a[1][sb][lane];
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                if (F == F_IQ2S) {   // scales per 16 weights: groups 0-1, then 2-3
+                    const uint4 z = u4(0, 0, 0, 0);
+                    const uint4 b0 = q < 2 ? b[r] : z, b1 = q < 2 ? z : b[r];
+                    f32x4 c = mfma(ah, b0, f32x4{0.f, 0.f, 0.f, 0.f});
+                    c = mfma(al, b0, c);
+                    f32x4 c1 = mfma(ah, b1, f32x4{0.f, 0.f, 0.f, 0.f});
+                    c1 = mfma(al, b1, c1);
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        acc[r][j] = fmaf(db2[r], c1[j], fmaf(db[r], c[j], acc[r][j]));
+                } else {
+                    f32x4 c = mfma(ah, b[r], f32x4{0.f, 0.f, 0.f, 0.f});
+                    c = mfma(al, b[r], c);
+#pragma unroll
+                    for (int j = 0; j < 4; j++) acc[r][j] = fmaf(db[r], c[j], acc[r][j]);
+                }
+            }
+        }
+        return;
+    }
     TileScales ts[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) {
@@ -404,8 +539,10 @@ __device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NR],
 // Software pipeline over the 256-column blocks: the raw weight bytes and the
 // A operands of block kb + 1 are loaded into registers while block kb is
 // multiplied, then written to LDS between two barriers.
+// sel: the tiles of the routed experts (0), of the shared expert (1), or both
+// (2); the shared expert's tiles follow the routed ones in the tile list.
 template <int MODE, int F>
-__global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
+__global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs ws, uint32_t sel) {
     constexpr int RT = gemm_rt<MODE, F>();
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     GemmLds& S = *(GemmLds*)smem;
@@ -414,13 +551,15 @@ __global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs 
     // block) items -- the row blocks of one tile (same A rows) and the tiles of
     // one expert (same weights) then share that XCD's L2.
     const uint32_t ny = MODE == 0 ? L.inter / (32 * RT) : L.hidden / (64 * RT);
-    const uint32_t total = *ws.n_tiles * ny;
+    const uint32_t t_first = sel == 1 ? ws.n_tiles[0] : 0u;
+    const uint32_t n_t = sel == 0 ? ws.n_tiles[0] : sel == 1 ? ws.n_tiles[1] : ws.n_tiles[0] + ws.n_tiles[1];
+    const uint32_t total = n_t * ny;
     const uint32_t per_xcd = (total + 7) / 8;
     const uint32_t slot = blockIdx.x / 8;
     const uint32_t item = (blockIdx.x % 8) * per_xcd + slot;
     if (slot >= per_xcd || item >= total) return;
     const uint32_t ti = item / ny, yb = item % ny;
-    const uint4 tile = ws.tiles[ti];
+    const uint4 tile = ws.tiles[t_first + ti];
     const uint32_t mid_e = tile.x, ent0 = tile.y, cnt = tile.z;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
     const uint32_t n = lane & 15u, q = lane >> 4;
@@ -484,6 +623,8 @@ __global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs 
         piece[i] = c % NCH;
     }
     u32x4 rawv[NR], av[4], sxv;
+    uint8_t* tab = (uint8_t*)S.raw + (size_t)NR * kPWG * 16;   // IQ lattice tables
+    if constexpr (is_iq(F)) stage_iq_tables<F>(tab);   // visible after the loop's first barrier
     f32x4 acc[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -501,7 +642,7 @@ __global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs 
 #pragma unroll
         for (int r = 0; r < RT; r++)
             R[r] = rrow[r] * NCH * 16 + (uint32_t)((uintptr_t)(row_ptr(rrow[r]) + (size_t)kb * bb) & 15u);
-        gemm_block<F, RT>(S, R, lane, sxa, acc);
+        gemm_block<F, RT>(S, tab, R, lane, sxa, acc);
     }
 
     // epilogue: lane holds entries 4 q + j of row n of its tiles
@@ -637,27 +778,42 @@ __global__ __launch_bounds__(64) void k_pre_router(const float* __restrict__ rou
 }
 
 template <int MODE, int F>
-void launch_gemm_f(const PrefillLayer& L, const PrefillWs& ws, uint32_t grid_x, hipStream_t st) {
+void launch_gemm_f(const PrefillLayer& L, const PrefillWs& ws, uint32_t cap, uint32_t sel,
+                   hipStream_t st) {
     constexpr int RT = gemm_rt<MODE, F>();
-    const size_t lds = offsetof(GemmLds, raw) + (size_t)64 * RT * raw_chunks(F) * 16;
+    const size_t lds = offsetof(GemmLds, raw) + (size_t)64 * RT * raw_chunks(F) * 16 + iq_tab_bytes(F);
     const uint32_t ny = MODE == 0 ? L.inter / (32 * RT) : L.hidden / (64 * RT);
-    // grid_x tiles at most; the kernel maps workgroups to the actual items
-    const uint32_t nwg = (grid_x * ny + 7) / 8 * 8;
-    k_pre_gemm<MODE, F><<<nwg, kPWG, lds, st>>>(L, ws);
+    // cap tiles at most; the kernel maps workgroups to the actual items
+    const uint32_t nwg = (cap * ny + 7) / 8 * 8;
+    k_pre_gemm<MODE, F><<<nwg, kPWG, lds, st>>>(L, ws, sel);
 }
 
 template <int MODE>
-int launch_gemm(int f, const PrefillLayer& L, const PrefillWs& ws, uint32_t grid_x,
-                hipStream_t st) {
+int launch_gemm_sel(int f, const PrefillLayer& L, const PrefillWs& ws, uint32_t cap, uint32_t sel,
+                    hipStream_t st) {
     switch (f) {
-    case F_Q4K: launch_gemm_f<MODE, F_Q4K>(L, ws, grid_x, st); break;
-    case F_Q5K: launch_gemm_f<MODE, F_Q5K>(L, ws, grid_x, st); break;
-    case F_Q6K: launch_gemm_f<MODE, F_Q6K>(L, ws, grid_x, st); break;
+    case F_Q4K: launch_gemm_f<MODE, F_Q4K>(L, ws, cap, sel, st); break;
+    case F_Q5K: launch_gemm_f<MODE, F_Q5K>(L, ws, cap, sel, st); break;
+    case F_Q6K: launch_gemm_f<MODE, F_Q6K>(L, ws, cap, sel, st); break;
+    case F_IQ2XXS: launch_gemm_f<MODE, F_IQ2XXS>(L, ws, cap, sel, st); break;
+    case F_IQ2S: launch_gemm_f<MODE, F_IQ2S>(L, ws, cap, sel, st); break;
+    case F_IQ3S: launch_gemm_f<MODE, F_IQ3S>(L, ws, cap, sel, st); break;
     default: return qw6_fail("batched path: unsupported weight format %d", f);
     }
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return qw6_fail("batched kernel launch: %s", hipGetErrorString(e));
     return 0;
+}
+
+// The routed experts' tiles with their format f; the shared expert's with
+// its own format fs (one launch when the formats agree).
+template <int MODE>
+int launch_gemm(int f, int fs, const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) {
+    const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
+    const uint32_t cap_sh = (L.T + kPM - 1) / kPM;
+    if (!L.sg.p || fs == f) return launch_gemm_sel<MODE>(f, L, ws, cap, 2, st);
+    if (launch_gemm_sel<MODE>(f, L, ws, cap, 0, st)) return -1;
+    return launch_gemm_sel<MODE>(fs, L, ws, cap_sh, 1, st);
 }
 
 }  // namespace
@@ -666,12 +822,14 @@ uint32_t prefill_tiles_max(uint32_t T, uint32_t top_k, uint32_t n_experts) {
     return (T * top_k + kPM - 1) / kPM + n_experts + (T + kPM - 1) / kPM;
 }
 
-bool prefill_supports(int f) { return f == F_Q4K || f == F_Q5K || f == F_Q6K; }
+bool prefill_supports(int f) { return f >= F_Q4K && f <= F_IQ3S; }
 
 int prefill_forward(const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) {
     if (L.hidden % 256 || L.inter % 256)
         return qw6_fail("batched path needs hidden, inter multiples of 256");
-    if (!prefill_supports(L.fmt_gu) || !prefill_supports(L.fmt_dn))
+    if (!prefill_supports(L.fmt_gu) || !prefill_supports(L.fmt_dn) ||
+        (L.sg.p && (!prefill_supports(L.sg.fmt) || !prefill_supports(L.sd.fmt) ||
+                    L.su.fmt != L.sg.fmt)))
         return qw6_fail("batched path: unsupported expert format");
     if (L.top_k == 0 || L.top_k > 8 || L.n_experts > 256)
         return qw6_fail("batched path: top_k / n_experts out of range");
@@ -692,9 +850,8 @@ int prefill_forward(const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) 
     k_pre_sort<<<1, 1024, 0, st>>>(Lx, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return qw6_fail("batched routing launch: %s", hipGetErrorString(e));
-    const uint32_t nt = prefill_tiles_max(L.T, L.top_k, L.n_experts);
-    if (launch_gemm<0>(L.fmt_gu, Lx, ws, nt, st)) return -1;
-    if (launch_gemm<1>(L.fmt_dn, Lx, ws, nt, st)) return -1;
+    if (launch_gemm<0>(L.fmt_gu, L.sg.fmt, Lx, ws, st)) return -1;
+    if (launch_gemm<1>(L.fmt_dn, L.sd.fmt, Lx, ws, st)) return -1;
     k_pre_combine<<<dim3(L.T, (L.hidden / 4 + 255) / 256), 256, 0, st>>>(Lx, ws);
     e = hipGetLastError();
     if (e != hipSuccess) return qw6_fail("batched combine launch: %s", hipGetErrorString(e));

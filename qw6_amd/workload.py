@@ -20,11 +20,15 @@ MIXES = {
     # further K-quant combinations (format coverage of the batched path)
     "q5k": (S.Q_Q5_K, lambda e: S.Q_Q5_K),
     "q6q4": (S.Q_Q6_K, lambda e: S.Q_Q4_K_M),
+    # one IQ format per matrix kind (as in a GGUF expert pack)
+    "iq2a": (S.Q_IQ2_XXS, lambda e: S.Q_IQ3_S),
+    "iq2b": (S.Q_IQ2_S, lambda e: S.Q_IQ2_S),
 }
 SHARED_Q = (S.Q_Q4_K_M, S.Q_Q4_K_M, S.Q_Q6_K)
 # shared expert formats where they differ from SHARED_Q: the same formats as
 # the routed experts
-SHARED_Q_MIX = {"q5k": (S.Q_Q5_K, S.Q_Q5_K, S.Q_Q5_K), "q6q4": (S.Q_Q6_K, S.Q_Q6_K, S.Q_Q4_K_M)}
+SHARED_Q_MIX = {"q5k": (S.Q_Q5_K, S.Q_Q5_K, S.Q_Q5_K), "q6q4": (S.Q_Q6_K, S.Q_Q6_K, S.Q_Q4_K_M),
+                "iq2b": (S.Q_IQ3_S, S.Q_IQ3_S, S.Q_IQ2_XXS)}
 
 
 def _align(n: int, a: int = 256) -> int:

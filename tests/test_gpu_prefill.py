@@ -99,10 +99,12 @@ def test_grouped_given_logits_vs_oracle(torch_dev, ctx, layer):
     assert np.mean(rels) <= TOL_MEAN
 
 
-@pytest.mark.parametrize("mix", ["q5k", "q6q4"])
+@pytest.mark.parametrize("mix", ["q5k", "q6q4", "iq2a", "iq2b"])
 def test_grouped_other_formats_vs_oracle(torch_dev, ctx, mix):
-    """Q5_K gate/up/down, and Q6_K gate/up with Q4_K down, through the grouped
-    kernels (T = 48, given logits, shared expert of the same formats)."""
+    """The other formats through the grouped kernels (T = 48, given logits):
+    Q5_K throughout; Q6_K gate/up with Q4_K down; IQ2_XXS gate/up with IQ3_S
+    down and a Q4_K / Q6_K shared expert (its own launches); IQ2_S throughout
+    with an IQ3_S / IQ2_XXS shared expert."""
     from qw6_amd.workload import SynthLayer
     L = SynthLayer(ctx, 71, 0, mix)
     try:
@@ -279,3 +281,24 @@ def test_grouped_in_place_residual_update(torch_dev, ctx, layer):
     finally:
         ctx.set_mode(0)
     assert torch.equal(h, ref)
+
+
+@pytest.mark.parametrize("mix", ["iq2a", "iq2b"])
+def test_grouped_iq_vs_per_token_kernels(torch_dev, ctx, mix):
+    """IQ layers, all 64 tokens of a batch: grouped kernels against the fp32
+    per-token kernels of the same library."""
+    from qw6_amd.workload import SynthLayer
+    L = SynthLayer(ctx, 73, 0, mix)
+    try:
+        T = 64
+        lg = S.zipf_logits(74, T)
+        xs = np.stack([cases.token_x(73, 6, t) for t in range(T)])
+        out_g, idx_g, _ = run(torch_dev, ctx, L, xs, logits=lg, mode=2)
+        out_p, idx_p, _ = run(torch_dev, ctx, L, xs, logits=lg, mode=1)
+        assert np.array_equal(idx_g, idx_p)
+        rels = [cases.rel_l2(out_g[t], out_p[t]) for t in range(T)]
+        say("%s grouped vs per-token rel-L2 max %.2e mean %.2e" % (mix, max(rels), np.mean(rels)))
+        assert max(rels) <= TOL_BF16
+        assert np.mean(rels) <= TOL_MEAN
+    finally:
+        L.free()
