@@ -30,7 +30,9 @@ sample of the same workload on this host, single thread as qw6 runs it.
   prefill_T512  512 tokens with Zipf(1.1)-skewed router logits through the
                 grouped bf16-MFMA kernels, Q4_K / Q6_K experts: us/layer,
                 TFLOP/s, MFMA fraction, HBM GB/s;
-  mtp_T2        two tokens (MTP draft verification) with the router GEMV.
+  mtp_T2        two tokens (MTP draft verification) with the router GEMV;
+  prefill_T512_iq2xxs_iq3s  the grouped kernels on an IQ layer (IQ2_XXS
+                gate/up, IQ3_S down, Q4_K / Q6_K shared expert).
 """
 from __future__ import annotations
 
@@ -315,9 +317,11 @@ def bench_stack(torch, Q, S, ctx, args):
     return res
 
 
-def bench_prefill(torch, Q, S, ctx, pool, args):
-    """T tokens with Zipf-skewed logits through the grouped MFMA kernels, plus the
-    T=2 MTP case through the per-token kernels with the router GEMV."""
+def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
+                  formats="Q4_K gate/up, Q6_K down"):
+    """T tokens with Zipf-skewed logits through the grouped MFMA kernels, plus
+    (with_t2) the T=2 MTP case through the per-token kernels with the router
+    GEMV."""
     import numpy as np
     T = args.prefill_tokens
     P = min(2, len(pool))
@@ -358,8 +362,10 @@ def bench_prefill(torch, Q, S, ctx, pool, args):
            "roofline_TFLOPs": round(roof, 1), "roofline_frac": round(tf / roof, 4),
            "flops": int(fl), "bytes": int(by), "hbm_GBps": round(by / us / 1e3, 1),
            "tokens_per_s": round(T / (us * 1e-6), 1),
-           "workload": "T=%d, hidden 2048, 256 experts top-8 + shared, Q4_K gate/up, Q6_K "
-                       "down; router logits given, Zipf(1.1)-skewed (Gumbel-top-k)" % T}
+           "workload": "T=%d, hidden 2048, 256 experts top-8 + shared, %s; router logits "
+                       "given, Zipf(1.1)-skewed (Gumbel-top-k)" % (T, formats)}
+    if not with_t2:
+        return res, None
 
     # T = 2 (MTP draft verification): router GEMV + per-token kernels
     X2 = torch.empty(len(pool), 2, HIDDEN, dtype=torch.float32, device="cuda")
@@ -461,6 +467,14 @@ def main():
         secondary["iq2m_decode"] = r2
         log("decode iq2m: %s" % json.dumps(r2))
         for L in pool2:
+            L.free()
+        # batched IQ layer: one IQ format per matrix kind, as in a GGUF expert pack
+        pool3 = [SynthLayer(ctx, 2500 + i, i, "iq2a") for i in range(2)]
+        pf3, _ = bench_prefill(torch, Q, S, ctx, pool3, args, with_t2=False,
+                               formats="IQ2_XXS gate/up, IQ3_S down, Q4_K/Q6_K shared")
+        secondary["prefill_T%d_iq2xxs_iq3s" % args.prefill_tokens] = pf3
+        log("prefill iq: %s" % json.dumps(pf3))
+        for L in pool3:
             L.free()
     if args.workload in ("all", "stack"):
         st = bench_stack(torch, Q, S, ctx, args)
