@@ -1,20 +1,22 @@
 // qw6_hip.hip -- gfx950 kernels and C ABI of the routed-expert MoE FFN path.
 //
-// Decode path (fp32 accumulation), four kernels per MoE layer:
-//   moe_router : router GEMV over all experts (one wave per expert row); extra
-//                workgroups run the shared expert's gate/up/SiLU, which does
-//                not depend on routing.
-//   moe_route  : one workgroup: softmax top-k of every token, distinct
-//                selected experts numbered in first-use order ("slots"),
-//                their matrices resolved into slot descriptors.
-//   moe_gate_up: one workgroup per (slot, row tile): each wave streams its
-//                rows into LDS with direct-to-LDS 16-byte loads and
-//                dequantizes step s while step s+1 is still in flight;
-//                writes silu(gate) * up.
-//   moe_down   : one workgroup per tile of output rows, one wave per selected
-//                expert (plus the shared one); per-expert row sums meet in LDS
-//                and are combined in selection order, with the residual --
-//                no atomics, deterministic.
+// Decode path (fp32 accumulation), three kernels per MoE layer (a kernel
+// boundary is the cheapest grid-wide dependency on this GPU):
+//   k_moe_router : router GEMV over all experts (one wave per expert row),
+//                  optional RMSNorm of the input, shared-expert gate weight.
+//   k_moe_gate_up: the shared expert's workgroups stream at once; every routed
+//                  workgroup routes the tokens itself from the logits (softmax
+//                  top-k; distinct selected experts numbered in first-use
+//                  order, "slots"), then streams gate/up rows of its slot's
+//                  expert into LDS with direct-to-LDS 16-byte loads,
+//                  dequantizing step s while step s+1 is in flight; writes
+//                  silu(gate) * up. One workgroup publishes the slot table.
+//   k_moe_down   : one workgroup per tile of output rows, one wave per
+//                  selected expert (plus the shared one); per-expert row sums
+//                  meet in LDS and are combined in selection order, with the
+//                  residual -- no atomics, deterministic.
+// Batches of 32 tokens or more take the grouped bf16-MFMA kernels of
+// qw6_prefill.hip.
 // Routing never leaves the device (qw6's Vulkan path reads idx/w back to the
 // host per layer, qw6_vk.c:3371-3374).
 //
