@@ -142,15 +142,23 @@ typedef struct {
  * [n_tok x n_experts] router logits (batched prefill). idx/w: optional device
  * outputs [n_tok x top_k] of the routing. residual: optional device
  * [n_tok x hidden] added to the output (hidden = resid + ffn, qw6.c:2482).
- * Tokens are processed by the decode kernels (fp32) when n_tok is small and
- * by the grouped bf16-MFMA kernels otherwise (see qw6_hip_set_mode). */
+ * Tokens are processed per launch of up to 4 tokens (decode, MTP
+ * verification) or by the grouped bf16-MFMA kernels (prefill); see
+ * qw6_hip_set_mode. */
 int qw6_hip_moe_forward(qw6_hip_ctx_t *ctx, const qw6_hip_moe_layer_t *layer,
                         const float *x, const float *logits,
                         const float *residual, uint32_t n_tok, float *out,
                         uint32_t *idx, float *w, void *stream);
 
-/* Path selection for qw6_hip_moe_forward: 0 = automatic (default),
- * 1 = always the fp32 decode kernels, 2 = always the grouped MFMA kernels. */
+/* Path selection for qw6_hip_moe_forward:
+ * 0 = automatic (default): the fp32 per-token kernels for launches of 1-2
+ *     tokens, the small-batch MFMA per-token kernels for 3-4, the grouped
+ *     MFMA kernels from 5 tokens on (when every matrix kind has one routed
+ *     format, else per-token launches);
+ * 1 = always the fp32 per-token kernels;
+ * 2 = always the grouped MFMA kernels;
+ * 3 = always the small-batch MFMA per-token kernels.
+ * Returns -1 for another value. */
 int qw6_hip_set_mode(qw6_hip_ctx_t *ctx, int mode);
 
 /* Per-kernel timing of qw6_hip_moe_forward on its launch stream (eager calls

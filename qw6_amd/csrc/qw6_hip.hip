@@ -32,12 +32,14 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <type_traits>
 #include <vector>
 
 #include "../../include/qw6_hip.h"
 #include "qw6_dev.h"
 #include "qw6_moe.h"
+#include "qw6_tile.h"
 
 using namespace qw6;
 
@@ -47,8 +49,10 @@ __device__ const IqTables g_tabs = make_tables();
 
 constexpr int kWG = 256;           // threads per workgroup (4 waves)
 constexpr uint32_t kMaxTok = 4;    // tokens per decode launch
-constexpr uint32_t kGroupedMinTokens = 32;   // automatic switch to the grouped MFMA path
+constexpr uint32_t kGroupedMinTokens = 5;    // automatic switch to the grouped MFMA path
+constexpr uint32_t kMxMinTokens = 3;         // per-token launches of 3-4 tokens: k_mx_*
 constexpr uint32_t kLdsBudget = 64 * 1024;   // dynamic LDS per workgroup
+constexpr uint32_t kMxLdsBudget = 150 * 1024;   // k_mx_*: gfx950 has 160 KB per workgroup
 constexpr int kProfEv = 6;         // events per profiled MoE call (3 kernels x start/stop)
 
 thread_local char g_err[512];
@@ -361,6 +365,14 @@ struct MoeArgs {
     uint32_t tmask_gu, tmask_dn;
     int xl_dn;                    // a format with every routed down matrix's
                                   // activation layout, or -1 (x_layout)
+    // small-batch MFMA path (k_mx_*): operands of the expert input and of mid
+    uint4* xa;                    // [hidden / 32][64]; k_moe_router writes it when set
+    uint16_t* xs;                 // [hidden / 256][2][4][3][8]
+    uint4* ma;                    // [max_u + 1][inter / 32][64], shared expert last
+    uint16_t* ms;                 // [max_u + 1][inter / 256][2][4][3][8]
+    uint32_t mx_gu_soff;          // k_mx_gate_up: LDS offset of the staged blocks
+    uint32_t mx_sb;               // k_mx_down: LDS bytes of one staged block
+    uint32_t mx_nsl;              // k_mx_down: staged blocks per round
 };
 
 __device__ __forceinline__ MatD expert_mat(const MoeArgs& a, uint32_t e, int k) {
@@ -457,74 +469,148 @@ __device__ __forceinline__ void route_prologue(const MoeArgs& a, uint32_t (&keys
     __syncthreads();
 }
 
+// ---- small-batch MFMA operands -------------------------------------------------------
+// The k_mx_* kernels multiply GGUF blocks decoded into bf16 MFMA operands
+// (qw6_tile.h) with the tokens as the 16 rows of the A operand: row m = 4 t + p
+// holds part p of token t's activation, p = 0, 1, 2 the bf16 hi / mid / lo
+// parts (their sum is the fp32 value to within 2^-24 of it); rows p = 3 and
+// t >= T are zero, so D[m][n] summed over p is token t's product with row n.
+//  - Sub-block operands (xa, ma): one 1 KB entry per 32-column sub-block;
+//    lane l = 16 q + m holds columns 8 q .. 8 q + 7 of row m.
+//  - Half-sum operands (xs, ms): per 256-column block, half (columns 0-15 or
+//    16-31 of each of its 8 sub-blocks) and token, the 3 bf16 parts of the 8
+//    half-sums, [block][half][t][part][sub-block]: the bias and minimum
+//    corrections take them in k-slots 8 part + sub-block (mx_load_a).
+
+// Part p (0: hi, 1: mid, 2: lo, 3: none) of v as bf16 bits.
+__device__ __forceinline__ uint32_t bf16_part(float v, uint32_t p) {
+    const __bf16 h = (__bf16)v;
+    const float r1 = v - (float)h;
+    const __bf16 m = (__bf16)r1;
+    const __bf16 l = (__bf16)(r1 - (float)m);
+    return p == 0 ? bfb(h) : p == 1 ? bfb(m) : p == 2 ? bfb(l) : 0u;
+}
+
+// Sub-block operand lane of eight values (columns 8 q .. 8 q + 7 of row m = 4 t + p).
+__device__ __forceinline__ uint4 mx_pack8(const float (&v)[8], uint32_t p) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) w[i] = bf16_part(v[2 * i], p) | (bf16_part(v[2 * i + 1], p) << 16);
+    return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// The 3 bf16 parts of half-sum hs of sub-block sb, half h, token t, into a
+// half-sum operand array of nkb blocks.
+__device__ __forceinline__ void mx_put_halfsum(uint16_t* dst, uint32_t sb, uint32_t h, uint32_t t, float hs) {
+    uint16_t p3[3];
+    split3(hs, p3);
+    uint16_t* o = dst + (((size_t)(sb >> 3) * 2 + h) * 4 + t) * 24 + (sb & 7u);
+    o[0] = p3[0];
+    o[8] = p3[1];
+    o[16] = p3[2];
+}
+
+// Operands of input sub-block e (one wave): the activations as the expert
+// kernels see them (RMSNorm applied with scale sc, this lane's token's, as the
+// per-token kernels' input), split into parts, and the two half-sums per token.
+template <int T>
+__device__ __forceinline__ void mx_input_operands(const MoeArgs& a, uint32_t e, float sc) {
+    const uint32_t lane = threadIdx.x & 63u, m = lane & 15u, q = lane >> 4, t = m >> 2, p = m & 3u;
+    const uint32_t c0 = 32u * e + 8u * q;
+    float v[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = 0.f;
+    if (t < (uint32_t)T) {
+        const float4* xr = (const float4*)(a.x + (size_t)t * a.hidden + c0);
+        const float4 x0 = xr[0], x1 = xr[1];
+        v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+        v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+        if (a.norm_w) {
+            const float4* wr = (const float4*)(a.norm_w + c0);
+            const float4 w0 = wr[0], w1 = wr[1];
+            const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = v[i] * sc * w[i];
+        }
+    }
+    a.xa[(size_t)e * 64 + lane] = mx_pack8(v, p);
+    float hs = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) hs += v[i];
+    hs += __shfl_xor(hs, 16);   // lanes q and q ^ 1: the half q / 2
+    if (p == 0 && (q & 1u) == 0) mx_put_halfsum(a.xs, e, q >> 1, t, hs);
+}
+
 // x (T tokens) -> optional RMSNorm (qw6_cpu_rmsnorm, qw6.c:2503-2513) ->
 // router logits; one wave per expert row. Each wave holds the whole input
 // in registers, so with norm_w set every wave computes the norm scale itself
 // and wave e writes its slice of the normalised input for the expert kernels.
 // Block n_experts (when present) computes the shared-expert gate weight
-// sigmoid(shared_router . x) (qw6.c:2267-2285).
-template <int T>
+// sigmoid(shared_router . x) (qw6.c:2267-2285). NV = hidden / 256 float4 per
+// lane, a template constant so that every load is unconditional. With a.xa
+// set, waves e < hidden / 32 also write the small-batch MFMA operands.
+template <int T, int NV>
 __global__ __launch_bounds__(64) void k_moe_router(MoeArgs a) {
     TRACE_SCOPE(0);
     const uint32_t lane = threadIdx.x, e = blockIdx.x;
-    const uint32_t H = a.hidden, n4 = H / 256;   // float4 per lane (H multiple of 256)
-    float4 xv[T][8];
+    const uint32_t H = 256 * NV;   // NV float4 per lane
+    float4 xv[T][NV];
 #pragma unroll
     for (int t = 0; t < T; t++)
 #pragma unroll
-        for (uint32_t i = 0; i < 8; i++)
-            if (i < n4) xv[t][i] = ((const float4*)(a.x + (size_t)t * H))[64 * i + lane];
+        for (uint32_t i = 0; i < NV; i++)
+            xv[t][i] = ((const float4*)(a.x + (size_t)t * H))[64 * i + lane];
     // the router row of expert e (or the shared-expert router); none when the
     // logits are given and this launch only normalises the input
-    const float* wrow = e < a.n_experts ? a.router : a.shared_router;
+    const float* wrow = e < a.n_experts ? a.router : e == a.n_experts ? a.shared_router : nullptr;
     if (wrow && e < a.n_experts) wrow += (size_t)e * H;
-    float4 wv[8];
+    float4 wv[NV];
 #pragma unroll
-    for (uint32_t i = 0; i < 8; i++)
-        if (wrow && i < n4) wv[i] = ((const float4*)wrow)[64 * i + lane];
+    for (uint32_t i = 0; i < NV; i++)
+        if (wrow) wv[i] = ((const float4*)wrow)[64 * i + lane];
+    float sc_l = 1.0f;   // the RMSNorm scale of token (lane % 16) / 4 (operand row)
     if (a.norm_w) {
-        float4 nw[8];
+        float4 nw[NV];
 #pragma unroll
-        for (uint32_t i = 0; i < 8; i++)
-            if (i < n4) nw[i] = ((const float4*)a.norm_w)[64 * i + lane];
+        for (uint32_t i = 0; i < NV; i++)
+            nw[i] = ((const float4*)a.norm_w)[64 * i + lane];
 #pragma unroll
         for (int t = 0; t < T; t++) {
             float ss = 0.f;
 #pragma unroll
-            for (uint32_t i = 0; i < 8; i++)
-                if (i < n4) {
-                    ss = fmaf(xv[t][i].x, xv[t][i].x, ss); ss = fmaf(xv[t][i].y, xv[t][i].y, ss);
-                    ss = fmaf(xv[t][i].z, xv[t][i].z, ss); ss = fmaf(xv[t][i].w, xv[t][i].w, ss);
-                }
+            for (uint32_t i = 0; i < NV; i++) {
+                ss = fmaf(xv[t][i].x, xv[t][i].x, ss); ss = fmaf(xv[t][i].y, xv[t][i].y, ss);
+                ss = fmaf(xv[t][i].z, xv[t][i].z, ss); ss = fmaf(xv[t][i].w, xv[t][i].w, ss);
+            }
             ss = group_sum<64>(ss);
             const float sc = 1.0f / sqrtf(ss / (float)H + a.norm_eps);
+            if ((uint32_t)t == (lane & 15u) >> 2) sc_l = sc;
 #pragma unroll
-            for (uint32_t i = 0; i < 8; i++)
-                if (i < n4) {
-                    xv[t][i].x = xv[t][i].x * sc * nw[i].x; xv[t][i].y = xv[t][i].y * sc * nw[i].y;
-                    xv[t][i].z = xv[t][i].z * sc * nw[i].z; xv[t][i].w = xv[t][i].w * sc * nw[i].w;
-                }
+            for (uint32_t i = 0; i < NV; i++) {
+                xv[t][i].x = xv[t][i].x * sc * nw[i].x; xv[t][i].y = xv[t][i].y * sc * nw[i].y;
+                xv[t][i].z = xv[t][i].z * sc * nw[i].z; xv[t][i].w = xv[t][i].w * sc * nw[i].w;
+            }
             // wave e writes float4s [e * per, (e + 1) * per) of the normalised input
             const uint32_t nq = H / 4, nwv = a.n_experts + (a.shared_router ? 1u : 0u);
             const uint32_t per = (nq + nwv - 1) / nwv;
 #pragma unroll
-            for (uint32_t i = 0; i < 8; i++) {
+            for (uint32_t i = 0; i < NV; i++) {
                 const uint32_t q = 64 * i + lane;
-                if (i < n4 && q >= e * per && q < (e + 1) * per)
+                if (q >= e * per && q < (e + 1) * per)
                     ((float4*)(a.xn + (size_t)t * H))[q] = xv[t][i];
             }
         }
     }
+    if (a.xa && e < H / 32) mx_input_operands<T>(a, e, sc_l);
     if (!wrow) return;
 #pragma unroll
     for (int t = 0; t < T; t++) {
         float acc = 0.f;
 #pragma unroll
-        for (uint32_t i = 0; i < 8; i++)
-            if (i < n4) {
-                acc = fmaf(wv[i].x, xv[t][i].x, acc); acc = fmaf(wv[i].y, xv[t][i].y, acc);
-                acc = fmaf(wv[i].z, xv[t][i].z, acc); acc = fmaf(wv[i].w, xv[t][i].w, acc);
-            }
+        for (uint32_t i = 0; i < NV; i++) {
+            acc = fmaf(wv[i].x, xv[t][i].x, acc); acc = fmaf(wv[i].y, xv[t][i].y, acc);
+            acc = fmaf(wv[i].z, xv[t][i].z, acc); acc = fmaf(wv[i].w, xv[t][i].w, acc);
+        }
         acc = group_sum<64>(acc);
         if (lane == 0) {
             if (e < a.n_experts) a.logits[(size_t)t * a.n_experts + e] = acc;
@@ -802,6 +888,358 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
     }
 }
 
+// ---- small-batch MFMA kernels ------------------------------------------------------
+// k_mx_gate_up and k_mx_down compute the same layer as k_moe_gate_up and
+// k_moe_down for T <= 4 tokens, with bf16 MFMA 16x16x32 on the operands above:
+// the weights' per-lane decode work (qw6_tile.h) no longer grows with T, and
+// the registers no longer hold every token's activations.
+
+// LDS of the bf16 lattice tables of the IQ formats in a fmt_table_mask: the
+// 256 sign masks, then the grids present (IQ2_XXS, IQ2_S, IQ3_S).
+struct MxTab {
+    uint32_t g[3];
+    uint32_t bytes;
+};
+__host__ __device__ inline MxTab mx_tab(uint32_t mask) {
+    MxTab t;
+    uint32_t o = mask ? 4096u : 0u;
+    const uint32_t gb[3] = {256u * 16u, 1024u * 16u, 512u * 8u};
+    for (int i = 0; i < 3; i++) {
+        t.g[i] = o;
+        if ((mask >> i) & 1u) o += gb[i];
+    }
+    t.bytes = o;
+    return t;
+}
+__device__ __forceinline__ void stage_mx_tables(uint8_t* tab, uint32_t mask, uint32_t nthr) {
+    if (!mask) return;
+    const MxTab tb = mx_tab(mask);
+    stage_iq_signs(tab, nthr);
+    if (mask & 1u) stage_iq_grid<F_IQ2XXS>(tab + tb.g[0], g_tabs, nthr);
+    if (mask & 2u) stage_iq_grid<F_IQ2S>(tab + tb.g[1], g_tabs, nthr);
+    if (mask & 4u) stage_iq_grid<F_IQ3S>(tab + tb.g[2], g_tabs, nthr);
+}
+
+// 16-byte loads per lane that stage one 256-column block of 16 rows.
+__host__ __device__ constexpr uint32_t mx_stage_loads(int f) { return (16u * raw_chunks(f) + 63u) / 64u; }
+__host__ __device__ constexpr uint32_t mx_stage_bytes(int f) { return 1024u * mx_stage_loads(f); }
+
+// Stage the block at byte offset boff of 16 rows (row r at src + r * rb) into
+// LDS dst (one wave): row r's chunk k (16 B from the line that holds the
+// block's start) lands at dst + 16 (r * raw_chunks(f) + k). Chunks past a row's
+// block reload its first chunk, so no load reaches past the block's last line.
+__device__ __forceinline__ void mx_stage(uint8_t* dst, const uint8_t* src, uint32_t rb, uint32_t boff,
+                                         int f) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t nch = raw_chunks(f), bb = fmt_block_bytes(f), nl = mx_stage_loads(f);
+    for (uint32_t i = 0; i < nl; i++) {
+        const uint32_t c = 64u * i + lane;
+        const bool in = c < 16u * nch;
+        const uint32_t r = in ? c / nch : 0u, k = in ? c % nch : 0u;
+        const uint8_t* p = src + (size_t)r * rb + boff;
+        const uint32_t off = (uint32_t)((uintptr_t)p & 15u);
+        const uint32_t kk = 16u * k < off + bb ? k : 0u;
+        __builtin_amdgcn_global_load_lds((glb_void_t*)(p - off + 16u * kk), (lds_void_t*)(dst + 1024u * i),
+                                         16, 0, 0);
+    }
+}
+// LDS byte offset of row n's block staged by mx_stage at LDS offset so.
+__device__ __forceinline__ uint32_t mx_row_off(uint32_t so, const uint8_t* src, uint32_t rb, uint32_t boff,
+                                               uint32_t n, int f) {
+    return so + 16u * raw_chunks(f) * n + (uint32_t)((uintptr_t)(src + (size_t)n * rb + boff) & 15u);
+}
+
+// A operands of block kb: sub-block entries 8 kb .. 8 kb + 7 of ea, and the
+// half-sum operands of es in lanes m = 4 t (k-slots 8 q + j, q < 3).
+__device__ __forceinline__ void mx_load_a(const uint4* ea, const uint16_t* es, uint32_t kb, uint32_t lane,
+                                          uint4 (&av)[8], uint4& c0, uint4& c1) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) av[j] = ea[(size_t)(8 * kb + j) * 64 + lane];
+    const uint32_t m = lane & 15u, q = lane >> 4;
+    c0 = make_uint4(0, 0, 0, 0);
+    c1 = c0;
+    if ((m & 3u) == 0 && q < 3) {
+        const uint16_t* b = es + (((size_t)kb * 2) * 4 + (m >> 2)) * 24 + 8 * q;
+        c0 = *(const uint4*)b;
+        c1 = *(const uint4*)(b + 4 * 24);
+    }
+}
+
+// mx_block for the runtime format f (uniform across the wave).
+__device__ __forceinline__ void mx_block_fmt(int f, const uint32_t* s, const uint8_t* tab, const MxTab& tb,
+                                             uint32_t R, uint32_t q, const uint4 (&av)[8], const uint4& c0,
+                                             const uint4& c1, f32x4& acc) {
+    switch (f) {
+    case F_Q4K: mx_block<F_Q4K>(s, tab, tab, R, q, av, c0, c1, acc); break;
+    case F_Q5K: mx_block<F_Q5K>(s, tab, tab, R, q, av, c0, c1, acc); break;
+    case F_Q6K: mx_block<F_Q6K>(s, tab, tab, R, q, av, c0, c1, acc); break;
+    case F_IQ2XXS: mx_block<F_IQ2XXS>(s, tab + tb.g[0], tab, R, q, av, c0, c1, acc); break;
+    case F_IQ2S: mx_block<F_IQ2S>(s, tab + tb.g[1], tab, R, q, av, c0, c1, acc); break;
+    default: mx_block<F_IQ3S>(s, tab + tb.g[2], tab, R, q, av, c0, c1, acc); break;
+    }
+}
+
+// Routing of one routed block of a gate/up kernel (tiles per slot: ntile):
+// its slot u and tile, the slot's expert e, and for the first routed block the
+// published selection and slot table (as k_moe_gate_up). False: unused slot.
+template <int T>
+__device__ __forceinline__ bool mx_route_block(const MoeArgs& a, uint32_t (&keys)[4], uint32_t ntile,
+                                               uint32_t& u, uint32_t& tile, uint32_t& e) {
+    __shared__ uint32_t s_idx[kMaxSlots], s_slot_e[kMaxSlots], s_n;
+    __shared__ float s_w[kMaxSlots], s_wt[kMaxSlots * kMaxTok];
+    const uint32_t wave = threadIdx.x >> 6;
+    const uint32_t b = blockIdx.x - a.n_sh_wg;
+    u = b / ntile;
+    tile = b % ntile;
+    if (T == 1 && b != 0) {   // one token: only the expert of rank u
+        __shared__ uint2 s_rt1[kRouteScr];
+        __shared__ uint32_t s_e1;
+        if (wave == 0) {
+            const uint32_t x = wave_route_select(keys, a.top_k, u, s_rt1);
+            if ((threadIdx.x & 63u) == 0) s_e1 = x;
+        }
+        __syncthreads();
+        e = s_e1;
+        return true;
+    }
+    route_prologue<T>(a, keys, s_idx, s_w, s_slot_e, s_wt, &s_n);   // ends with a barrier
+    const uint32_t nslot = s_n;
+    if (b == 0) {
+        const uint32_t tid = threadIdx.x;
+        if (tid < T * a.top_k) {
+            if (a.idx_out) a.idx_out[tid] = s_idx[tid];
+            if (a.w_out) a.w_out[tid] = s_w[tid];
+        }
+        if (tid < a.max_u) {
+            SlotTable* st = a.slots;
+            if (tid < nslot) {
+                const MatD D = expert_mat(a, s_slot_e[tid], 2);
+                st->p[tid] = D.p; st->fmt[tid] = D.fmt; st->rb[tid] = D.rb;
+            } else {
+                st->p[tid] = nullptr; st->fmt[tid] = 0; st->rb[tid] = 0;
+            }
+#pragma unroll
+            for (uint32_t t = 0; t < kMaxTok; t++) st->wt[tid][t] = s_wt[tid * kMaxTok + t];
+        }
+        if (tid == 0) a.slots->n = nslot;
+    }
+    if (u >= nslot) return false;
+    e = s_slot_e[u];
+    return true;
+}
+
+// Gate / up of 16 intermediate rows [row0, row0 + 16) of one matrix pair, all
+// waves: wave w takes the 256-column blocks w, w + nw, ...; their (gate, up)
+// bytes are staged at once. Leaves this lane's D sums in ag / au.
+template <int FW>
+__device__ __forceinline__ void mx_gu_blocks(const MoeArgs& a, const MatD& Gm, const MatD& Um, uint32_t row0,
+                                             uint8_t* smem, uint32_t soff, const MxTab& tb, f32x4& ag,
+                                             f32x4& au) {
+    uint4 av[8], c0, c1;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u, nw = blockDim.x >> 6;
+    const uint32_t n = lane & 15u, q = lane >> 4;
+    const uint32_t nkb = a.hidden / 256, nbw = (nkb + nw - 1) / nw;
+    constexpr uint32_t SB = mx_stage_bytes(FW), bb = fmt_block_bytes(FW);
+    const uint32_t so = soff + wave * nbw * 2 * SB;
+    const uint8_t* g0 = Gm.p + (size_t)row0 * Gm.rb;
+    const uint8_t* u0 = Um.p + (size_t)row0 * Um.rb;
+    for (uint32_t i = 0, kb = wave; kb < nkb; i++, kb += nw) {
+        mx_stage(smem + so + 2 * i * SB, g0, Gm.rb, kb * bb, FW);
+        mx_stage(smem + so + (2 * i + 1) * SB, u0, Um.rb, kb * bb, FW);
+    }
+    for (uint32_t i = 0, kb = wave; kb < nkb; i++, kb += nw) {
+        mx_load_a(a.xa, a.xs, kb, lane, av, c0, c1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        TRACE_MARK_IF(i == 0, 2, 1);
+        const uint32_t Rg = mx_row_off(so + 2 * i * SB, g0, Gm.rb, kb * bb, n, FW);
+        const uint32_t Ru = mx_row_off(so + (2 * i + 1) * SB, u0, Um.rb, kb * bb, n, FW);
+        const uint8_t* grid = smem + tb.g[FW >= F_IQ2XXS ? FW - F_IQ2XXS : 0];
+        mx_block<FW>((const uint32_t*)smem, grid, smem, Rg, q, av, c0, c1, ag);
+        __builtin_amdgcn_sched_barrier(0);   // gate then up: one block's temporaries live at a time
+        mx_block<FW>((const uint32_t*)smem, grid, smem, Ru, q, av, c0, c1, au);
+    }
+}
+
+// Routed + shared gate/up/SiLU: block (matrix pair, 16-row tile), shared
+// expert first (blocks [0, n_sh_wg)); writes the down kernel's operands of mid.
+template <int T>
+__global__ __launch_bounds__(512, 4) void k_mx_gate_up(MoeArgs a) {
+    TRACE_SCOPE(2);
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ float s_gu[2][kMaxTok][16];
+    __shared__ float s_mid[kMaxTok][16];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, nw = blockDim.x >> 6;
+    const uint32_t ntile = a.inter / 16;
+    const bool shared_wg = blockIdx.x < a.n_sh_wg;
+    const uint32_t nkb = a.hidden / 256;
+    // routing waves load their logits first; every wave then loads the A
+    // operands of its first block, which do not depend on the routing
+    uint32_t keys[4];
+    if (!shared_wg && wave < (uint32_t)T)
+        route_keys(a.route_logits + (size_t)wave * a.n_experts, a.n_experts, keys);
+    const uint32_t tmask = shared_wg ? fmt_table_mask(a.sg.fmt) : a.tmask_gu;
+    const MxTab tb = mx_tab(tmask);
+    stage_mx_tables(smem, tmask, blockDim.x);
+    MatD Gm, Um;
+    uint32_t row0, slot;
+    if (shared_wg) {
+        Gm = a.sg;
+        Um = a.su;
+        row0 = blockIdx.x * 16;
+        slot = a.max_u;
+        if (tmask) __syncthreads();   // the lattice tables are complete
+    } else {
+        uint32_t u, tile, e;
+        if (!mx_route_block<T>(a, keys, ntile, u, tile, e)) return;   // (barriers inside)
+        Gm = expert_mat(a, e, 0);
+        Um = expert_mat(a, e, 1);
+        row0 = tile * 16;
+        slot = u;
+    }
+    TRACE_MARK(2, 0);
+    f32x4 ag = {0.f, 0.f, 0.f, 0.f}, au = ag;
+    const uint32_t soff = a.mx_gu_soff;   // staging after the largest table set
+    switch (Gm.fmt) {
+    case F_Q4K: mx_gu_blocks<F_Q4K>(a, Gm, Um, row0, smem, soff, tb, ag, au); break;
+    case F_Q5K: mx_gu_blocks<F_Q5K>(a, Gm, Um, row0, smem, soff, tb, ag, au); break;
+    case F_Q6K: mx_gu_blocks<F_Q6K>(a, Gm, Um, row0, smem, soff, tb, ag, au); break;
+    case F_IQ2XXS: mx_gu_blocks<F_IQ2XXS>(a, Gm, Um, row0, smem, soff, tb, ag, au); break;
+    case F_IQ2S: mx_gu_blocks<F_IQ2S>(a, Gm, Um, row0, smem, soff, tb, ag, au); break;
+    default: mx_gu_blocks<F_IQ3S>(a, Gm, Um, row0, smem, soff, tb, ag, au); break;
+    }
+    TRACE_MARK(2, 2);
+    // the waves' partial sums meet in LDS (over the staged bytes), fixed order
+    __syncthreads();
+    float* red = (float*)(smem + soff);   // [nw][2][64][4]
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        red[((wave * 2 + 0) * 64 + lane) * 4 + i] = ag[i];
+        red[((wave * 2 + 1) * 64 + lane) * 4 + i] = au[i];
+    }
+    __syncthreads();
+    if (tid < 128) {
+        const uint32_t mat = tid >> 6, l = tid & 63u;
+        float v = 0.f;
+        for (uint32_t w = 0; w < nw; w++) {
+            const float* r = red + ((w * 2 + mat) * 64 + l) * 4;
+            v += (r[0] + r[1]) + r[2];
+        }
+        s_gu[mat][l >> 4][l & 15u] = v;
+    }
+    __syncthreads();
+    if (tid < 64) {
+        const uint32_t t = tid >> 4, nn = tid & 15u;
+        float y = 0.f;
+        if (t < (uint32_t)T) {
+            const float g = s_gu[0][t][nn], u = s_gu[1][t][nn];
+            y = g / (1.0f + expf(-g)) * u;
+        }
+        s_mid[t][nn] = y;
+    }
+    __syncthreads();
+    // mid rows [row0, row0 + 16) are half h of sub-block sb of the down input
+    const uint32_t sb = row0 >> 5, h = (row0 >> 4) & 1u;
+    if (tid < 32) {
+        const uint32_t qq = 2 * h + (tid >> 4), m = tid & 15u;
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = s_mid[m >> 2][8 * (tid >> 4) + i];
+        a.ma[((size_t)slot * (a.inter / 32) + sb) * 64 + 16 * qq + m] = mx_pack8(v, m & 3u);
+    } else if (tid < 32 + kMaxTok) {
+        const uint32_t t = tid - 32;
+        float hs = 0.f;
+        for (uint32_t nn = 0; nn < 16; nn++) hs += s_mid[t][nn];
+        mx_put_halfsum(a.ms + (size_t)slot * (a.inter / 256) * 192, sb, h, t, hs);
+    }
+}
+
+// Down projection + combine for hidden rows [r0, r0 + 16): the (matrix, block)
+// pairs -- matrix 0 the shared expert when present, then the slots -- go to
+// the waves in turn, staged a round of mx_nsl pairs at a time; per-pair sums
+// meet in LDS and are combined as out = sum_u wt[u] * y[u] + sw * y[shared]
+// (+ residual), a fixed order.
+template <int T>
+__global__ __launch_bounds__(1024) void k_mx_down(MoeArgs a) {
+    TRACE_SCOPE(3);
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ float s_wt[kMaxSlots * kMaxTok];
+    __shared__ const uint8_t* s_p[kMaxSlots];
+    __shared__ int32_t s_fmt[kMaxSlots];
+    __shared__ uint32_t s_rb[kMaxSlots];
+    const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, nw = blockDim.x >> 6;
+    const uint32_t n = lane & 15u, q = lane >> 4;
+    const uint32_t r0 = blockIdx.x * 16;
+    const uint32_t has_sh = a.sd.p != nullptr ? 1u : 0u;
+    const uint32_t nkb = a.inter / 256;
+    const MxTab tb = mx_tab(a.tmask_dn);
+    // the slot table in one round trip (entries past the count are null)
+    const uint32_t nslot = a.slots->n;
+    if (tid < kMaxSlots * kMaxTok) s_wt[tid] = a.slots->wt[tid / kMaxTok][tid % kMaxTok];
+    if (tid < kMaxSlots) {
+        s_p[tid] = a.slots->p[tid];
+        s_fmt[tid] = a.slots->fmt[tid];
+        s_rb[tid] = a.slots->rb[tid];
+    }
+    float resid = 0.f, shw = 1.0f;
+    if (tid < 16 * T) {
+        const uint32_t t = tid >> 4, nn = tid & 15u;
+        if (a.residual) resid = a.residual[(size_t)t * a.hidden + r0 + nn];
+        if (has_sh && a.shared_router) shw = a.sw[t];
+    }
+    stage_mx_tables(smem, a.tmask_dn, blockDim.x);
+    __syncthreads();   // slot table and lattice tables
+    TRACE_MARK(3, 0);
+    const uint32_t ntot = nslot + has_sh, npair = ntot * nkb;
+    const uint32_t soff = tb.bytes;
+    float* ybuf = (float*)(smem + soff + a.mx_nsl * a.mx_sb);   // [pair][4][16]
+    auto mat = [&](uint32_t m) -> MatD {
+        if (has_sh && m == 0) return a.sd;
+        const uint32_t u = m - has_sh;
+        return MatD{s_p[u], s_fmt[u], a.hidden, a.inter, s_rb[u]};
+    };
+    for (uint32_t base = 0; base < npair; base += a.mx_nsl) {
+        const uint32_t end = min(base + a.mx_nsl, npair);
+        for (uint32_t pr = base + wave; pr < end; pr += nw) {
+            const MatD D = mat(pr / nkb);
+            const uint32_t kb = pr % nkb;
+            mx_stage(smem + soff + (pr - base) * a.mx_sb, D.p + (size_t)r0 * D.rb, D.rb,
+                     kb * fmt_block_bytes(D.fmt), D.fmt);
+        }
+        for (uint32_t pr = base + wave; pr < end; pr += nw) {
+            const uint32_t m = pr / nkb, kb = pr % nkb;
+            const bool sh = has_sh && m == 0;
+            const MatD D = mat(m);
+            const uint32_t slot = sh ? a.max_u : m - has_sh;
+            uint4 av[8], c0, c1;
+            mx_load_a(a.ma + (size_t)slot * (a.inter / 32) * 64, a.ms + (size_t)slot * nkb * 192, kb, lane,
+                      av, c0, c1);
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            TRACE_MARK_IF(pr == wave, 3, 1);
+            const uint32_t R = mx_row_off(soff + (pr - base) * a.mx_sb, D.p + (size_t)r0 * D.rb, D.rb,
+                                          kb * fmt_block_bytes(D.fmt), n, D.fmt);
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            mx_block_fmt(D.fmt, (const uint32_t*)smem, smem, tb, R, q, av, c0, c1, acc);
+            ybuf[(pr * 4 + q) * 16 + n] = (acc[0] + acc[1]) + acc[2];
+        }
+        if (end < npair) __syncthreads();   // the next round reuses the staging slots
+    }
+    TRACE_MARK(3, 2);
+    __syncthreads();
+    if (tid < 16 * T) {
+        const uint32_t t = tid >> 4, nn = tid & 15u;
+        auto y = [&](uint32_t m) {
+            float v = 0.f;
+            for (uint32_t kb = 0; kb < nkb; kb++) v += ybuf[((m * nkb + kb) * 4 + t) * 16 + nn];
+            return v;
+        };
+        float v = 0.f;
+        for (uint32_t u = 0; u < nslot; u++) v = fmaf(s_wt[u * kMaxTok + t], y(u + has_sh), v);
+        if (has_sh) v = fmaf(shw, y(0), v);
+        if (a.residual) v += resid;
+        a.out[(size_t)t * a.hidden + r0 + nn] = v;
+    }
+}
+
 // ---- small elementwise kernels ---------------------------------------------------
 
 __global__ void k_silu_mul(const float* g, const float* u, float* o, uint32_t n) {
@@ -896,6 +1334,12 @@ struct qw6_hip_ctx_s {
     SlotTable* slots;
     float* mid;
     uint32_t ws_hidden, ws_inter;
+    // small-batch MFMA operands (k_mx_*)
+    uint4* mxa;
+    uint16_t* mxs;
+    uint4* mma;
+    uint16_t* mms;
+    uint32_t mx_hidden, mx_inter;
     // batched (grouped MFMA) workspace, sized for max_tokens
     PrefillWs pre;
     uint32_t pre_hidden, pre_inter, pre_experts;
@@ -1230,7 +1674,7 @@ int qw6_hip_alloc(qw6_hip_ctx_t* c, size_t bytes, void** dev) {
 }
 
 int qw6_hip_set_mode(qw6_hip_ctx_t* c, int mode) {
-    if (!c || mode < 0 || mode > 2) return fail("bad mode");
+    if (!c || mode < 0 || mode > 3) return fail("bad mode");
     c->mode = mode;
     return 0;
 }
@@ -1351,6 +1795,24 @@ int ensure_ws(qw6_hip_ctx_t* c, uint32_t hidden, uint32_t inter) {
     return 0;
 }
 
+int ensure_mx_ws(qw6_hip_ctx_t* c, uint32_t hidden, uint32_t inter) {
+    if (c->mxa && c->mx_hidden >= hidden && c->mx_inter >= inter) return 0;
+    hidden = hidden > c->mx_hidden ? hidden : c->mx_hidden;
+    inter = inter > c->mx_inter ? inter : c->mx_inter;
+    void* p;
+    if (alloc_owned(c, (size_t)(hidden / 32) * 64 * 16, &p)) return -1;
+    c->mxa = (uint4*)p;
+    if (alloc_owned(c, (size_t)(hidden / 256) * 192 * 2, &p)) return -1;
+    c->mxs = (uint16_t*)p;
+    if (alloc_owned(c, (size_t)(kMaxSlots + 1) * (inter / 32) * 64 * 16, &p)) return -1;
+    c->mma = (uint4*)p;
+    if (alloc_owned(c, (size_t)(kMaxSlots + 1) * (inter / 256) * 192 * 2, &p)) return -1;
+    c->mms = (uint16_t*)p;
+    c->mx_hidden = hidden;
+    c->mx_inter = inter;
+    return 0;
+}
+
 int ensure_prefill_ws(qw6_hip_ctx_t* c, uint32_t hidden, uint32_t inter, uint32_t n_experts,
                       uint32_t top_k) {
     (void)top_k;
@@ -1417,10 +1879,11 @@ int launch_k(void (*kern)(Args...), uint32_t grid, uint32_t block, size_t lds, h
 
 struct MoeLaunch {
     bool router;             // k_moe_router runs
+    bool mx;                 // the small-batch MFMA kernels (k_mx_*)
     uint32_t grid_r;
     int fg, fd;              // format of the gate/up (down) kernels, -1: mixed
     size_t lds_b, lds_c;
-    uint32_t grid_b, grid_c, nw_c;
+    uint32_t grid_b, grid_c, nw_b, nw_c;
 };
 
 // Run fn(IC<T>, IC<F>, IC<KU>) for the expert-kernel instantiation of T
@@ -1452,11 +1915,20 @@ void launch_expert_kernel(int f, uint32_t T, uint32_t KU, Fn fn) {
 int launch_moe(const MoeArgs& a, const MoeLaunch& m, hipStream_t st, hipEvent_t* ev) {
     if (m.router) {
         int rc = 0;
+        auto by_nv = [&](auto tc) {
+            constexpr int T = decltype(tc)::value;
+            switch (a.hidden / 256) {
+            case 1: rc = launch_k(k_moe_router<T, 1>, m.grid_r, 64, 0, st, ev, a); break;
+            case 2: rc = launch_k(k_moe_router<T, 2>, m.grid_r, 64, 0, st, ev, a); break;
+            case 4: rc = launch_k(k_moe_router<T, 4>, m.grid_r, 64, 0, st, ev, a); break;
+            default: rc = launch_k(k_moe_router<T, 8>, m.grid_r, 64, 0, st, ev, a); break;
+            }
+        };
         switch (a.T) {
-        case 1: rc = launch_k(k_moe_router<1>, m.grid_r, 64, 0, st, ev, a); break;
-        case 2: rc = launch_k(k_moe_router<2>, m.grid_r, 64, 0, st, ev, a); break;
-        case 3: rc = launch_k(k_moe_router<3>, m.grid_r, 64, 0, st, ev, a); break;
-        default: rc = launch_k(k_moe_router<4>, m.grid_r, 64, 0, st, ev, a); break;
+        case 1: by_nv(IC<1>{}); break;
+        case 2: by_nv(IC<2>{}); break;
+        case 3: by_nv(IC<3>{}); break;
+        default: by_nv(IC<4>{}); break;
         }
         if (rc) return rc;
     } else if (ev) {
@@ -1464,6 +1936,22 @@ int launch_moe(const MoeArgs& a, const MoeLaunch& m, hipStream_t st, hipEvent_t*
         CK(hipEventRecord(ev[1], st));
     }
     int rc = 0;
+    if (m.mx) {
+        switch (a.T) {
+        case 1: rc = launch_k(k_mx_gate_up<1>, m.grid_b, 64 * m.nw_b, m.lds_b, st, ev ? ev + 2 : nullptr, a); break;
+        case 2: rc = launch_k(k_mx_gate_up<2>, m.grid_b, 64 * m.nw_b, m.lds_b, st, ev ? ev + 2 : nullptr, a); break;
+        case 3: rc = launch_k(k_mx_gate_up<3>, m.grid_b, 64 * m.nw_b, m.lds_b, st, ev ? ev + 2 : nullptr, a); break;
+        default: rc = launch_k(k_mx_gate_up<4>, m.grid_b, 64 * m.nw_b, m.lds_b, st, ev ? ev + 2 : nullptr, a); break;
+        }
+        if (rc) return rc;
+        switch (a.T) {
+        case 1: rc = launch_k(k_mx_down<1>, m.grid_c, 64 * m.nw_c, m.lds_c, st, ev ? ev + 4 : nullptr, a); break;
+        case 2: rc = launch_k(k_mx_down<2>, m.grid_c, 64 * m.nw_c, m.lds_c, st, ev ? ev + 4 : nullptr, a); break;
+        case 3: rc = launch_k(k_mx_down<3>, m.grid_c, 64 * m.nw_c, m.lds_c, st, ev ? ev + 4 : nullptr, a); break;
+        default: rc = launch_k(k_mx_down<4>, m.grid_c, 64 * m.nw_c, m.lds_c, st, ev ? ev + 4 : nullptr, a); break;
+        }
+        return rc;
+    }
     launch_expert_kernel<64>(m.fg, a.T, a.hidden / 32, [&](auto tc, auto fc, auto kc) {
         rc = launch_k(k_moe_gate_up<decltype(tc)::value, decltype(fc)::value, decltype(kc)::value>,
                       m.grid_b, kWG, m.lds_b, st, ev ? ev + 2 : nullptr, a);
@@ -1547,6 +2035,10 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
         return prefill_forward(P, c->pre, st);
     }
     if (ensure_ws(c, L->hidden, L->inter)) return -1;
+    // per-token path: the fp32 kernels (k_moe_*) or the small-batch MFMA
+    // kernels (k_mx_*: mode 3, or automatic for more than one token per launch)
+    const bool mx_any = c->mode == 3 || c->mode == 0;
+    if (mx_any && ensure_mx_ws(c, L->hidden, L->inter)) return -1;
 
     MoeArgs a;
     memset(&a, 0, sizeof a);
@@ -1564,6 +2056,21 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
     a.tmask_gu = mgu;
     a.tmask_dn = mdn;
     a.xl_dn = E->xl_dn;
+    a.xs = c->mxs; a.ma = c->mma; a.ms = c->mms;
+    // k_mx_* launch shape: the staged block of a format (largest of those in use)
+    auto sb_of = [](int f) {
+        if (f >= 0) return mx_stage_bytes(f);
+        uint32_t b = 0;
+        for (int k = 0; k < F_NFMT; k++) b = b > mx_stage_bytes(k) ? b : mx_stage_bytes(k);
+        return b;
+    };
+    const uint32_t sb_gu = std::max(sb_of(E->fmt_gu), has_sh ? sb_of(sg.fmt) : 0u);
+    const uint32_t sb_dn = std::max(sb_of(E->fmt_dn), has_sh ? sb_of(sd.fmt) : 0u);
+    const uint32_t nkb_gu = L->hidden / 256, nkb_dn = L->inter / 256;
+    const uint32_t mx_nw_b = nkb_gu < 8 ? nkb_gu : 8;
+    const uint32_t mx_tab_gu = mx_tab(mgu).bytes, mx_tab_dn = mx_tab(mdn).bytes;
+    a.mx_gu_soff = mx_tab_gu;
+    a.mx_sb = sb_dn;
 
     MoeLaunch m;
     m.fg = (has_sh && sg.fmt != E->fmt_gu) ? -1 : E->fmt_gu;
@@ -1581,10 +2088,17 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
     m.grid_r = E->n + (L->shared_router ? 1u : 0u);
     if (m.lds_b > kLdsBudget) return fail("gate/up tile exceeds the LDS budget");
 
+    const uint32_t n_sh_valu = a.n_sh_wg, grid_c_valu = m.grid_c;
+    const size_t lds_b_valu = m.lds_b;
     for (uint32_t t0 = 0; t0 < n_tok; t0 += kMaxTok) {
         const uint32_t T = n_tok - t0 < kMaxTok ? n_tok - t0 : kMaxTok;
         a.T = T;
         a.max_u = T * L->top_k;
+        m.mx = c->mode == 3 || (c->mode == 0 && T >= kMxMinTokens);
+        a.xa = m.mx ? c->mxa : nullptr;   // k_moe_router writes the operands
+        a.n_sh_wg = n_sh_valu;
+        m.grid_c = grid_c_valu;
+        m.lds_b = lds_b_valu;
         a.x = x + (size_t)t0 * L->hidden;
         a.xin = L->norm_w ? c->xn : a.x;
         a.router = logits ? nullptr : L->router;
@@ -1599,7 +2113,30 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
         m.nw_c = ntot < nw_max ? ntot : nw_max;
         m.lds_c = (size_t)tab_bytes(mdn) + (size_t)m.nw_c * kStepsDn * kSlotBytes +
                   (size_t)ntot * R_c * T * 4 + 16;
-        if (m.lds_c > kLdsBudget) return fail("down tile exceeds the LDS budget");
+        if (!m.mx && m.lds_c > kLdsBudget) return fail("down tile exceeds the LDS budget");
+        m.router = (!logits && L->router) || L->shared_router != nullptr || L->norm_w != nullptr;
+        m.grid_r = E->n + (L->shared_router ? 1u : 0u);
+        if (m.mx) {
+            // gate/up: blocks of 16 rows, one wave per 256-column block (up to 8)
+            const uint32_t nbw = (nkb_gu + mx_nw_b - 1) / mx_nw_b;
+            a.n_sh_wg = has_sh ? L->inter / 16 : 0u;
+            m.grid_b = a.n_sh_wg + a.max_u * (L->inter / 16);
+            m.nw_b = mx_nw_b;
+            m.lds_b = (size_t)mx_tab_gu + (size_t)mx_nw_b * nbw * 2 * sb_gu;
+            // down: blocks of 16 rows, the (matrix, 256-column block) pairs
+            // staged a round at a time
+            const uint32_t npair = ntot * nkb_dn;
+            const uint32_t fixed = mx_tab_dn + npair * 256u;   // tables + per-pair sums
+            if (fixed + sb_dn > kMxLdsBudget) return fail("small-batch down tile exceeds the LDS budget");
+            a.mx_nsl = std::min(npair, (kMxLdsBudget - fixed) / sb_dn);
+            m.grid_c = L->hidden / 16;
+            m.nw_c = npair < 16 ? npair : 16;
+            m.lds_c = (size_t)fixed + (size_t)a.mx_nsl * sb_dn;
+            // the router kernel always runs: it writes the input operands
+            m.router = true;
+            m.grid_r = std::max(m.grid_r, L->hidden / 32);
+            if (m.lds_b > kMxLdsBudget) return fail("small-batch gate/up tile exceeds the LDS budget");
+        }
         hipEvent_t* ev = nullptr;
         if (c->prof_calls < c->prof_cap) ev = &c->prof_ev[kProfEv * c->prof_calls++];
         const int rc = launch_moe(a, m, st, ev);

@@ -8,19 +8,17 @@
 //   k_pre_route   one wave per token: softmax top-k (wave_route), the
 //                 shared-expert weight, the shared entries.
 //   k_pre_sort    one workgroup: counting sort of the (token, k) pairs by
-//                 expert into "entries", and a tile list of <= 32 entries of
+//                 expert into "entries", and a tile list of <= 16 entries of
 //                 one expert (the shared expert last, with every token).
 //   k_pre_gemm<0> gate and up for 128 intermediate rows of one tile (64
-//                 for Q6_K): mid[entry] = silu(x.gate) * (x.up).
-//   k_pre_gemm<1> down for 256 hidden rows of one tile (128 for Q6_K), times
-//                 the entry's gate weight -> ybuf[entry].
+//                 for Q6_K and IQ3_S): mid[entry] = silu(x.gate) * (x.up).
+//   k_pre_gemm<1> down for 256 hidden rows of one tile (128 for Q6_K and
+//                 IQ3_S), times the entry's gate weight -> ybuf[entry].
 //   k_pre_combine out[t] = sum_k ybuf[entry(t, k)] + ybuf[shared entry(t)]
 //                 (+ residual), a fixed order: deterministic, no atomics.
 //
 // Numerics of the contraction (rel-L2 ~1e-5 against the fp32 CPU path):
-//  - weights enter the MFMA as their integer codes, exact in bf16: 128 + q
-//    for a 4/5/6-bit code q (the byte pair {q, 0x43} is bf16 128 + q, one
-//    v_perm per two codes);
+//  - weights enter the MFMA as their integer codes (qw6_tile.h);
 //  - activations enter as bf16 hi + lo (hi = bf16(x), lo = bf16(x - hi)), two
 //    MFMAs per 32-column sub-block;
 //  - the fp32 sub-block scale d*sc multiplies each sub-block's 16x16 MFMA
@@ -39,42 +37,15 @@
 
 #include "qw6_dev.h"
 #include "qw6_moe.h"
+#include "qw6_tile.h"
 
 namespace qw6 {
 namespace {
 
 __device__ const IqTables g_tabs_pre = make_tables();
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));   // register-resident 16 B
-
 constexpr uint32_t kPM = 16;      // entries per tile (one MFMA row group)
 constexpr uint32_t kPWG = 256;    // threads per workgroup (4 waves)
-
-// 16-B chunks per staged row block: Q4_K / Q5_K blocks (144 / 176 B) of
-// 16-byte aligned rows are 16-byte aligned; Q6_K (210 B) and IQ blocks (66,
-// 82, 110 B) may start at any even offset within their first chunk.
-__host__ __device__ constexpr uint32_t raw_chunks(int f) {
-    return (f == F_Q4K || f == F_Q5K) ? fmt_block_bytes(f) / 16
-                                      : (fmt_block_bytes(f) + 14 + 15) / 16;
-}
-__host__ __device__ constexpr bool is_iq(int f) {
-    return f == F_IQ2XXS || f == F_IQ2S || f == F_IQ3S;
-}
-// LDS of the bf16 lattice tables of an IQ format: the grid (8 or 4 values
-// per entry, 16 or 8 B) then 256 sign masks (16 B: bit j of the sign byte ->
-// the sign bit of bf16 value j).
-__host__ __device__ constexpr uint32_t iq_grid_bytes(int f) {
-    return f == F_IQ2XXS ? 256 * 16 : f == F_IQ2S ? 1024 * 16 : f == F_IQ3S ? 512 * 8 : 0;
-}
-__host__ __device__ constexpr uint32_t iq_tab_bytes(int f) {
-    return is_iq(f) ? iq_grid_bytes(f) + 256 * 16 : 0;
-}
-
-// ---- bf16 operand preparation -----------------------------------------------------
-
-__device__ __forceinline__ uint32_t bfb(__bf16 b) { return (uint32_t)__builtin_bit_cast(uint16_t, b); }
 
 // Eight floats -> bf16 hi and lo parts (hi = bf16(x), lo = bf16(x - hi)), packed
 // in MFMA operand order; returns sum(hi + lo) in fp32.
@@ -93,16 +64,6 @@ __device__ __forceinline__ float split8(const float (&v)[8], uint4& h, uint4& l)
     h = make_uint4(hw[0], hw[1], hw[2], hw[3]);
     l = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     return sum;
-}
-
-// A sub-block sum as three bf16 parts (hi, mid, lo), exact to fp32 precision.
-__device__ __forceinline__ void split3(float x, uint16_t (&p)[3]) {
-#pragma unroll
-    for (int i = 0; i < 3; i++) {
-        const __bf16 b = (__bf16)x;
-        p[i] = __builtin_bit_cast(uint16_t, b);
-        x -= (float)b;
-    }
 }
 
 // ---- routing -----------------------------------------------------------------------
@@ -214,209 +175,6 @@ __global__ __launch_bounds__(1024) void k_pre_sort(PrefillLayer L, PrefillWs ws)
 
 // ---- the grouped contraction --------------------------------------------------------
 
-__device__ __forceinline__ uint4 u4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
-    return make_uint4(a, b, c, d);
-}
-// Byte pairs {b0, 0x43}, {b1, 0x43} of the low half (hi = 0) or {b2,..}, {b3,..}
-// (hi = 1) of w: bf16 values 128 + b.
-__device__ __forceinline__ uint32_t codes2(uint32_t w, int hi) {
-    return __builtin_amdgcn_perm(0x43434343u, w, hi ? 0x04030402u : 0x04010400u);
-}
-// Eight codes 128 + byte of (w0, w1) in MFMA operand order.
-__device__ __forceinline__ uint4 codes8(uint32_t w0, uint32_t w1) {
-    return u4(codes2(w0, 0), codes2(w0, 1), codes2(w1, 0), codes2(w1, 1));
-}
-__device__ __forceinline__ uint32_t bf16_bits(float f) {   // exact for the small integers used here
-    return __float_as_uint(f) >> 16;
-}
-__device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, const f32x4& c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
-}
-
-// ---- B-tile decoding ----------------------------------------------------------------
-// A wave works on RT tiles of 16 weight rows. For one 256-column block, lane
-// (n = l % 16, q = l / 16) of tile r reads row n's raw block bytes from LDS
-// (s = LDS words, R = byte offset of the row's block) and produces, per
-// sub-block s, the B operand: codes 128 + q (bf16) of columns 32 s + 8 q .. + 8.
-
-// Per-tile scale state of one block: d * sc per sub-block, and d, dmin.
-struct TileScales {
-    float dsc[8];
-    float d, dmin;
-};
-
-// The sub-block scales (and minimums) of row n as B operands over k =
-// 8 q' + j (j = sub-block): lanes q' = 0, 1, 2 pair them with the three bf16
-// parts of the activation sums; lanes q' = 3 meet a zero A operand.
-// bf16 pair of two small integral floats (their low 16 bits are zero).
-__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
-    return __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x07060302u);
-}
-
-template <int F>
-__device__ __forceinline__ void tile_scales(const uint32_t* s, uint32_t R, TileScales& ts,
-                                            uint4& bsc, uint4& bmin) {
-    float sc[8], mn[8];
-    if (F == F_Q4K || F == F_Q5K) {
-        const uint4 hd = *(const uint4*)(s + (R >> 2));   // 16-byte aligned block
-        ts.d = h2f(hd.x & 0xffffu);
-        ts.dmin = h2f(hd.x >> 16);
-        // qw6_get_scale_min_k4 (qw6.c:1480-1490) for all eight sub-blocks at
-        // once, four 6-bit values per word: j < 4 from the low 6 bits of bytes
-        // 0-3 (scales) and 4-7 (minimums); j >= 4 from the nibbles of bytes
-        // 8-11 with the top two bits of bytes j - 4 and j
-        const uint32_t A = hd.y, B = hd.z, C = hd.w;
-        const uint32_t sc_lo = A & 0x3f3f3f3fu, mn_lo = B & 0x3f3f3f3fu;
-        const uint32_t sc_hi = (C & 0x0f0f0f0fu) | ((A >> 2) & 0x30303030u);
-        const uint32_t mn_hi = ((C >> 4) & 0x0f0f0f0fu) | ((B >> 2) & 0x30303030u);
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            sc[j] = ub(sc_lo, j);
-            sc[j + 4] = ub(sc_hi, j);
-            mn[j] = ub(mn_lo, j);
-            mn[j + 4] = ub(mn_hi, j);
-        }
-    } else {   // Q6_K: sub-block 4h + k uses scale 8h + 2k (qw6.c:1550-1578)
-        ts.d = h2f(lds16(s, R + 208));
-        ts.dmin = 0.f;
-#pragma unroll
-        for (int h = 0; h < 2; h++) {
-            const uint32_t w0 = lds32(s, R + 192 + 8 * h), w1 = lds32(s, R + 196 + 8 * h);
-            sc[4 * h + 0] = (float)(int8_t)(w0 & 0xffu);
-            sc[4 * h + 1] = (float)(int8_t)((w0 >> 16) & 0xffu);
-            sc[4 * h + 2] = (float)(int8_t)(w1 & 0xffu);
-            sc[4 * h + 3] = (float)(int8_t)((w1 >> 16) & 0xffu);
-        }
-#pragma unroll
-        for (int j = 0; j < 8; j++) mn[j] = 0.f;
-    }
-#pragma unroll
-    for (int j = 0; j < 8; j++) ts.dsc[j] = ts.d * sc[j];
-    bsc = u4(pk_bf16(sc[0], sc[1]), pk_bf16(sc[2], sc[3]), pk_bf16(sc[4], sc[5]), pk_bf16(sc[6], sc[7]));
-    bmin = F != F_Q6K ? u4(pk_bf16(mn[0], mn[1]), pk_bf16(mn[2], mn[3]), pk_bf16(mn[4], mn[5]),
-                           pk_bf16(mn[6], mn[7]))
-                      : u4(0, 0, 0, 0);
-}
-
-// Codes of sub-blocks 2p and 2p + 1 of row n (this lane's 8 columns of each).
-template <int F>
-__device__ __forceinline__ void tile_codes(const uint32_t* s, uint32_t R, uint32_t q, int p,
-                                           uint4& b0, uint4& b1) {
-    if (F == F_Q4K || F == F_Q5K) {
-        // qs byte 32 p + l: low nibble column 64 p + l, high nibble 64 p + 32 + l
-        const uint32_t qo = F == F_Q4K ? 16u : 48u;
-        const uint2 wq = *(const uint2*)(s + ((R + qo + 32 * p + 8 * q) >> 2));
-        uint32_t l0 = wq.x & 0x0f0f0f0fu, l1 = wq.y & 0x0f0f0f0fu;
-        uint32_t h0 = (wq.x >> 4) & 0x0f0f0f0fu, h1 = (wq.y >> 4) & 0x0f0f0f0fu;
-        if (F == F_Q5K) {   // qh byte l: bit 2p -> column 64 p + l, bit 2p + 1 -> + 32
-            const uint2 hq = *(const uint2*)(s + ((R + 16 + 8 * q) >> 2));
-            l0 |= ((hq.x >> (2 * p)) & 0x01010101u) << 4;
-            l1 |= ((hq.y >> (2 * p)) & 0x01010101u) << 4;
-            h0 |= ((hq.x >> (2 * p + 1)) & 0x01010101u) << 4;
-            h1 |= ((hq.y >> (2 * p + 1)) & 0x01010101u) << 4;
-        }
-        b0 = codes8(l0, l1);
-        b1 = codes8(h0, h1);
-    } else {
-        // half h = p / 2; sub-blocks 4h + 2i, 4h + 2i + 1 (i = p % 2): ql bytes
-        // 64 h + l (a) and 64 h + 32 + l (b), low nibbles for i = 0, high for
-        // i = 1; 2-bit fields 2k of qh byte 128 + 32 h + l (k = 2i, 2i + 1)
-        const uint32_t h = (uint32_t)p >> 1, i = (uint32_t)p & 1u;
-        const uint32_t a0 = lds32(s, R + 64 * h + 8 * q), a1 = lds32(s, R + 64 * h + 8 * q + 4);
-        const uint32_t c0 = lds32(s, R + 64 * h + 32 + 8 * q), c1 = lds32(s, R + 64 * h + 36 + 8 * q);
-        const uint32_t x0 = lds32(s, R + 128 + 32 * h + 8 * q), x1 = lds32(s, R + 132 + 32 * h + 8 * q);
-        const uint32_t sh = 4 * i;   // nibble shift; also the qh shift 2k of k = 2i
-        b0 = codes8(((a0 >> sh) & 0x0f0f0f0fu) | (((x0 >> sh) & 0x03030303u) << 4),
-                    ((a1 >> sh) & 0x0f0f0f0fu) | (((x1 >> sh) & 0x03030303u) << 4));
-        b1 = codes8(((c0 >> sh) & 0x0f0f0f0fu) | (((x0 >> (sh + 2)) & 0x03030303u) << 4),
-                    ((c1 >> sh) & 0x0f0f0f0fu) | (((x1 >> (sh + 2)) & 0x03030303u) << 4));
-    }
-}
-
-// ---- IQ formats -------------------------------------------------------------------
-// The lattice values are small integers (IQ2: 8, 25, 43; IQ3: odd 1 .. 15),
-// exact in bf16, and every weight is db * (+-value): the B operand is the
-// bf16 grid entry with the sign bits flipped, with no bias or minimum term.
-
-// Expand the lattice tables of format F into LDS as bf16 (all threads).
-template <int F>
-__device__ __forceinline__ void stage_iq_tables(uint8_t* tab) {
-    const uint32_t tid = threadIdx.x;
-    auto bf = [](uint32_t v) { return bf16_bits((float)v); };
-    if (F == F_IQ2XXS || F == F_IQ2S) {
-        const uint32_t n = F == F_IQ2XXS ? 256u : 1024u;
-        const uint64_t* g = F == F_IQ2XXS ? g_tabs_pre.iq2xxs : g_tabs_pre.iq2s;
-        for (uint32_t i = tid; i < n; i += kPWG) {
-            const uint64_t v = g[i];
-            uint32_t w[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++)
-                w[k] = bf((uint32_t)(v >> (16 * k)) & 255u) | (bf((uint32_t)(v >> (16 * k + 8)) & 255u) << 16);
-            ((uint4*)tab)[i] = u4(w[0], w[1], w[2], w[3]);
-        }
-    } else {
-        for (uint32_t i = tid; i < 512; i += kPWG) {
-            const uint32_t v = g_tabs_pre.iq3s[i];
-            ((uint2*)tab)[i] = make_uint2(bf(v & 255u) | (bf((v >> 8) & 255u) << 16),
-                                          bf((v >> 16) & 255u) | (bf(v >> 24) << 16));
-        }
-    }
-    uint4* sg = (uint4*)(tab + iq_grid_bytes(F));
-    for (uint32_t s8 = tid; s8 < 256; s8 += kPWG) {
-        uint32_t w[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++)
-            w[k] = (((s8 >> (2 * k)) & 1u) << 15) | (((s8 >> (2 * k + 1)) & 1u) << 31);
-        sg[s8] = u4(w[0], w[1], w[2], w[3]);
-    }
-}
-
-__device__ __forceinline__ uint4 xor4(const uint4& a, const uint4& b) {
-    return u4(a.x ^ b.x, a.y ^ b.y, a.z ^ b.z, a.w ^ b.w);
-}
-
-// B operand of sub-block sb of row n (this lane's 8 weights, group q of the
-// sub-block) and its scale(s): db for all 32 weights, or (IQ2_S) db for
-// groups 0-1 and db2 for groups 2-3 (qw6.c:1580-1672).
-template <int F>
-__device__ __forceinline__ void tile_iq(const uint32_t* s, const uint8_t* tab, uint32_t R,
-                                        uint32_t q, int sb, float d, uint4& b, float& db,
-                                        float& db2) {
-    const uint4* sgn = (const uint4*)(tab + iq_grid_bytes(F));
-    if (F == F_IQ2XXS) {   // 8 B per 32 weights: 4 grid indices, 4 x 7 sign bits + scale
-        const uint32_t aux0 = lds32(s, R + 2 + 8 * sb), aux1 = lds32(s, R + 6 + 8 * sb);
-        const uint32_t idx = (aux0 >> (8 * q)) & 255u;
-        const uint32_t s7 = (aux1 >> (7 * q)) & 127u;
-        const uint32_t sg = s7 | ((__builtin_popcount(s7) & 1u) << 7);   // ksigns_iq2xs
-        b = xor4(((const uint4*)tab)[idx], sgn[sg]);
-        db = d * (0.5f + (float)(aux1 >> 28)) * 0.25f;
-        db2 = db;
-    } else if (F == F_IQ2S) {   // grid index: qs byte + 2 bits of qh; own sign byte
-        const uint32_t qsb = lds8(s, R + 2 + 4 * sb + q);
-        const uint32_t qh = lds8(s, R + 66 + sb);
-        const uint32_t sg = lds8(s, R + 34 + 4 * sb + q);
-        const uint32_t sc = lds8(s, R + 74 + sb);
-        const uint32_t gi = qsb | ((qh << (8 - 2 * q)) & 0x300u);
-        b = xor4(((const uint4*)tab)[gi], sgn[sg]);
-        db = d * (0.5f + (float)(sc & 15u)) * 0.25f;
-        db2 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
-    } else {   // IQ3_S: two 4-value grid entries per 8 weights, 9-bit indices
-        const uint32_t qw = lds32(s, R + 2 + 8 * sb + 4 * (q >> 1));
-        const uint32_t qh = lds8(s, R + 66 + sb);
-        const uint32_t sg = lds8(s, R + 74 + 4 * sb + q);
-        const uint32_t scb = lds8(s, R + 106 + (sb >> 1));
-        const uint32_t nib = (sb & 1) ? (scb >> 4) : (scb & 15u);
-        const uint32_t sh = 16 * (q & 1u);
-        const uint32_t i1 = ((qw >> sh) & 255u) | ((qh << (8 - 2 * q)) & 256u);
-        const uint32_t i2 = ((qw >> (sh + 8)) & 255u) | ((qh << (7 - 2 * q)) & 256u);
-        const uint2 g1 = ((const uint2*)tab)[i1], g2 = ((const uint2*)tab)[i2];
-        b = xor4(u4(g1.x, g1.y, g2.x, g2.y), sgn[sg]);
-        db = d * (float)(1 + 2 * (int)nib);
-        db2 = db;
-    }
-}
-
 // Shared memory of k_pre_gemm: the A operands of the tile for one 256-column
 // block, operand-major so the operand reads (lane l reads 16 B at l) are
 // conflict-free; then the raw weight block bytes of the workgroup's rows.
@@ -449,7 +207,8 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
             uint4 b[RT];
             float db[RT], db2[RT];
 #pragma unroll
-            for (int r = 0; r < RT; r++) tile_iq<F>(S.raw, tab, R[r], q, sb, d[r], b[r], db[r], db2[r]);
+            for (int r = 0; r < RT; r++)
+                tile_iq<F>(S.raw, tab, tab + iq_grid_bytes(F), R[r], q, sb, d[r], b[r], db[r], db2[r]);
             const uint4 ah = S.a[0][sb][lane], al = S.a[1][sb][lane];
 #pragma unroll
             for (int r = 0; r < RT; r++) {
@@ -624,7 +383,7 @@ __global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs 
     }
     u32x4 rawv[NR], av[4], sxv;
     uint8_t* tab = (uint8_t*)S.raw + (size_t)NR * kPWG * 16;   // IQ lattice tables
-    if constexpr (is_iq(F)) stage_iq_tables<F>(tab);   // visible after the loop's first barrier
+    if constexpr (is_iq(F)) stage_iq_tables<F>(tab, g_tabs_pre, kPWG);   // visible after the loop's first barrier
     f32x4 acc[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
