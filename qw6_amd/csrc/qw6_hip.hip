@@ -324,7 +324,10 @@ __global__ __launch_bounds__(64) void k_route(const float* __restrict__ logits, 
 //                  row sums meet in LDS and are combined in a fixed order with
 //                  the residual -- no atomics, deterministic.
 
-constexpr int kStepsGu = 2;     // row steps per wave, gate/up
+// Row steps per wave of k_moe_gate_up: 4 for two tokens, whose 17 matrix
+// pairs then take 544 workgroups, all resident at once (3 per CU).
+template <int T>
+__host__ __device__ constexpr int gu_steps() { return T == 2 ? 4 : 2; }
 constexpr int kStepsDn = 2;     // row steps per wave, down
 constexpr uint32_t kMaxSlots = kMaxTok * 8;
 constexpr uint32_t kSlotBytes = 2048;   // LDS slot of one step group (8 blocks <= 1680 B)
@@ -363,6 +366,7 @@ struct MoeArgs {
     uint32_t* idx_out;
     float* w_out;
     uint32_t tmask_gu, tmask_dn;
+    uint32_t gu_pb;               // k_moe_gate_up: LDS bytes of one (gate, up) step pair
     int xl_dn;                    // a format with every routed down matrix's
                                   // activation layout, or -1 (x_layout)
     // small-batch MFMA path (k_mx_*): operands of the expert input and of mid
@@ -400,15 +404,35 @@ __device__ __forceinline__ void stage_group(uint8_t* slot, const uint8_t* src, u
     }
 }
 
+// Loads per lane that stage one (gate, up) step pair of format f (2 x 8 blocks).
+__host__ __device__ constexpr uint32_t pair_loads(int f) { return (16u * fmt_block_bytes(f) + 1023u) / 1024u; }
+
+// Stage the step groups g (gate) and u (up) of gbytes each (8 blocks, a
+// multiple of 16 bytes) into one LDS pair slot, gate at +0 and up at +gbytes,
+// with nl 16-byte direct-to-LDS loads per lane; lanes past the pair's end
+// reload the gate group's first chunk into the slot's tail.
+__device__ __forceinline__ void stage_pair(uint8_t* slot, const uint8_t* g, const uint8_t* u,
+                                           uint32_t gbytes, uint32_t nl) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t n16 = gbytes >> 4;
+    for (uint32_t i = 0; i < nl; i++) {
+        const uint32_t c = 64u * i + lane;
+        const uint8_t* src = c < n16 ? g + 16ull * c : c < 2 * n16 ? u + 16ull * (c - n16) : g;
+        __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(slot + 1024u * i), 16, 0, 0);
+    }
+}
+
 // Wait until at most n of this wave's vector-memory loads are outstanding
 // (n a compile-time constant after unrolling: the switch folds away).
 __device__ __forceinline__ void wait_vm(uint32_t n) {
     switch (n) {
     case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
     case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
+    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
     case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
     case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
     case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
+    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
     case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
     case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
     case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
@@ -541,6 +565,45 @@ __device__ __forceinline__ void mx_input_operands(const MoeArgs& a, uint32_t e, 
     if (p == 0 && (q & 1u) == 0) mx_put_halfsum(a.xs, e, q >> 1, t, hs);
 }
 
+// The expert of slot u (the u-th distinct selected expert in first-use order
+// over tokens, then ranks, as route_prologue numbers them) for a block that
+// publishes nothing: waves t < T rank token t's logits (route_rank; no gate
+// weights), then every wave finds the slot from the T * top_k selections
+// with lane reads -- one barrier. Returns false if fewer than u + 1 slots.
+template <int T>
+__device__ __forceinline__ bool route_slot_select(const MoeArgs& a, uint32_t (&keys)[4], uint32_t u,
+                                                  uint32_t& e_out) {
+    __shared__ uint2 s_rs[kMaxTok][kRouteScr];
+    __shared__ uint32_t s_sel[kMaxSlots];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    if (wave < (uint32_t)T) {
+        uint2 me2;
+        uint32_t rank, ncand;
+        if (route_rank(keys, a.top_k, s_rs[wave], me2, rank, ncand)) {
+            if (lane < ncand && rank < a.top_k)   // only -inf left: qw6 picks index 0
+                s_sel[wave * a.top_k + rank] = me2.y > kKeyNegInf ? ~me2.x : 0u;
+        } else if (lane < a.top_k) {
+            const uint2 me = s_rs[wave][32 + lane];
+            s_sel[wave * a.top_k + lane] = me.y > kKeyNegInf ? ~me.x : 0u;
+        }
+    }
+    __syncthreads();
+    const uint32_t ne = T * a.top_k;
+    const uint32_t e = lane < ne ? s_sel[lane] : 0xffffffffu;
+    uint32_t first = lane;
+    for (uint32_t j = 0; j < ne; j++) {
+        const uint32_t v = (uint32_t)__builtin_amdgcn_readlane((int)e, (int)j);
+        if (j < first && v == e) first = j;
+    }
+    const bool is_first = lane < ne && first == lane;
+    const uint64_t mask = __ballot(is_first);
+    const uint32_t slot = __popcll(mask & ((1ull << lane) - 1ull));
+    const uint64_t hit = __ballot(is_first && slot == u);
+    if (!hit) return false;
+    e_out = (uint32_t)__builtin_amdgcn_readlane((int)e, __ffsll((unsigned long long)hit) - 1);
+    return true;
+}
+
 // x (T tokens) -> optional RMSNorm (qw6_cpu_rmsnorm, qw6.c:2503-2513) ->
 // router logits; one wave per expert row. Each wave holds the whole input
 // in registers, so with norm_w set every wave computes the norm scale itself
@@ -620,15 +683,15 @@ __global__ __launch_bounds__(64) void k_moe_router(MoeArgs a) {
 }
 
 // gate/up/silu of one wave: S steps of rps rows starting at row0 of the pair
-// (G, Up) -> mid[T][inter]. slots: 2*S LDS slots of kSlotBytes. xr/sx: this
+// (G, Up) -> mid[T][inter]. slots: S LDS pair slots of pb bytes. xr/sx: this
 // lane's activations, loaded before the weights' addresses were known.
 template <int T, int FF, int KU>
 __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint32_t row0,
                                              const float (&xr)[T][32], const float (&sx)[T][4],
                                              float* mid, uint32_t inter, uint8_t* slots,
-                                             const uint32_t* lds, uint32_t slot_off,
+                                             const uint32_t* lds, uint32_t slot_off, uint32_t pb,
                                              const uint32_t* tab) {
-    constexpr int S = kStepsGu;
+    constexpr int S = gu_steps<T>();
     const int f = FF >= 0 ? FF : G.fmt;
     constexpr uint32_t U = KU, rps = 64 / KU;
     const uint32_t lane = threadIdx.x & 63;
@@ -636,23 +699,23 @@ __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint
     const int j = (int)(unit & 7);
     const uint32_t bb = fmt_block_bytes(f);
     const uint32_t gbytes = rps * G.rb;   // one step group (8 blocks)
+    const uint32_t nl = FF >= 0 ? pair_loads(FF) : pair_loads(f);
 #pragma unroll
     for (int s = 0; s < S; s++) {
         const size_t r = row0 + (size_t)s * rps;
-        stage_group(slots + (2 * s) * kSlotBytes, G.p + r * G.rb, gbytes);
-        stage_group(slots + (2 * s + 1) * kSlotBytes, Up.p + r * Up.rb, gbytes);
+        stage_pair(slots + s * pb, G.p + r * G.rb, Up.p + r * Up.rb, gbytes, nl);
     }
     const uint32_t boff = slot_off + q * G.rb + blk * bb;
     float ag[T][S], au[T][S];
 #pragma unroll
     for (int s = 0; s < S; s++) {
-        wait_vm(4u * (S - 1 - s));
+        wait_vm(nl * (S - 1 - s));
         TRACE_MARK_IF(s == 0, 2, 1);
         float g[T], u[T];
 #pragma unroll
         for (int t = 0; t < T; t++) { g[t] = 0.f; u[t] = 0.f; }
-        unit_dot<T>(f, lds, (2 * s) * kSlotBytes + boff, j, tab, xr, sx, g);
-        unit_dot<T>(f, lds, (2 * s + 1) * kSlotBytes + boff, j, tab, xr, sx, u);
+        unit_dot<T>(f, lds, s * pb + boff, j, tab, xr, sx, g);
+        unit_dot<T>(f, lds, s * pb + gbytes + boff, j, tab, xr, sx, u);
 #pragma unroll
         for (int t = 0; t < T; t++) { ag[t][s] = g[t]; au[t][s] = u[t]; }
     }
@@ -683,12 +746,13 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
     __shared__ uint32_t s_idx[kMaxSlots], s_slot_e[kMaxSlots], s_n;
     __shared__ float s_w[kMaxSlots], s_wt[kMaxSlots * kMaxTok];
     const uint32_t wave = threadIdx.x >> 6;
+    constexpr int S = gu_steps<T>();
     constexpr uint32_t rps = 64 / KU;
-    constexpr uint32_t rows_wg = 4 * kStepsGu * rps;
+    constexpr uint32_t rows_wg = 4 * S * rps;
     const uint32_t ntile = (a.inter + rows_wg - 1) / rows_wg;
     const uint32_t toff = tab_bytes(a.tmask_gu);
-    uint8_t* wslots = smem + toff + wave * 2 * kStepsGu * kSlotBytes;
-    const uint32_t slot_off = toff + wave * 2 * kStepsGu * kSlotBytes;
+    uint8_t* wslots = smem + toff + wave * S * a.gu_pb;
+    const uint32_t slot_off = toff + wave * S * a.gu_pb;
     const bool shared_wg = blockIdx.x < a.n_sh_wg;
     // Waves t < T of a routed block route token t. Their logits load is the
     // block's first memory operation (loads complete in issue order, so
@@ -720,8 +784,20 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
     if (shared_wg) {
         G = a.sg;
         Up = a.su;
-        row0 = (blockIdx.x * 4 + wave) * kStepsGu * rps;
+        row0 = (blockIdx.x * 4 + wave) * S * rps;
         midp = a.mid + (size_t)a.max_u * T * a.inter;
+    } else if (T > 1 && blockIdx.x != a.n_sh_wg) {
+        // several tokens, not the publishing block: only this block's slot
+        const uint32_t b = blockIdx.x - a.n_sh_wg;
+        const uint32_t u = b / ntile, tile = b % ntile;
+        uint32_t e;
+        if (!route_slot_select<T>(a, keys, u, e)) return;
+        TRACE_MARK(2, 0);
+        G = expert_mat(a, e, 0);
+        Up = expert_mat(a, e, 1);
+        row0 = (tile * 4 + wave) * S * rps;
+        midp = a.mid + (size_t)u * T * a.inter;
+        if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr, sx);
     } else if (T == 1 && blockIdx.x != a.n_sh_wg) {
         // one token, not the publishing block: only the expert of this block's
         // rank is needed (no gate weights, no slot table)
@@ -738,7 +814,7 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
         const uint32_t e = s_e1;
         G = expert_mat(a, e, 0);
         Up = expert_mat(a, e, 1);
-        row0 = (tile * 4 + wave) * kStepsGu * rps;
+        row0 = (tile * 4 + wave) * S * rps;
         midp = a.mid + (size_t)u * T * a.inter;
         if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr, sx);
     } else {
@@ -770,13 +846,13 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
         const uint32_t e = s_slot_e[u];
         G = expert_mat(a, e, 0);
         Up = expert_mat(a, e, 1);
-        row0 = (tile * 4 + wave) * kStepsGu * rps;
+        row0 = (tile * 4 + wave) * S * rps;
         midp = a.mid + (size_t)u * T * a.inter;
         if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr, sx);
     }
     if (row0 >= a.inter) return;
     wave_gate_up<T, FG, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, (const uint32_t*)smem,
-                            slot_off, (const uint32_t*)smem);
+                            slot_off, a.gu_pb, (const uint32_t*)smem);
 }
 
 // Down projection + combine for rows [r0, r0 + R), R = S * rps. Matrix m of
@@ -1002,6 +1078,7 @@ __device__ __forceinline__ bool mx_route_block(const MoeArgs& a, uint32_t (&keys
         e = s_e1;
         return true;
     }
+    if (b != 0) return route_slot_select<T>(a, keys, u, e);
     route_prologue<T>(a, keys, s_idx, s_w, s_slot_e, s_wt, &s_n);   // ends with a barrier
     const uint32_t nslot = s_n;
     if (b == 0) {
@@ -2076,29 +2153,33 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
     m.fg = (has_sh && sg.fmt != E->fmt_gu) ? -1 : E->fmt_gu;
     m.fd = (has_sh && sd.fmt != E->fmt_dn) ? -1 : E->fmt_dn;
     const uint32_t rpsg = 64 / (L->hidden / 32), rpsd = 64 / (L->inter / 32);
-    const uint32_t rows_wg = 4 * kStepsGu * rpsg;          // gate/up rows per workgroup
-    const uint32_t ntile_b = (L->inter + rows_wg - 1) / rows_wg;
-    a.n_sh_wg = has_sh ? ntile_b : 0;
-    m.lds_b = (size_t)tab_bytes(mgu) + 4 * 2 * kStepsGu * kSlotBytes;
+    // k_moe_gate_up: LDS pair slot of the widest (gate, up) step pair in use
+    uint32_t pl = has_sh ? pair_loads(sg.fmt) : 1u;
+    for (int f = 0; f < F_NFMT; f++)
+        if (E->fmt_gu < 0 || E->fmt_gu == f) pl = std::max(pl, pair_loads(f));
+    a.gu_pb = 1024u * pl;
     const uint32_t R_c = kStepsDn * rpsd;
     m.grid_c = (L->hidden + R_c - 1) / R_c;
     // the router kernel runs when it has work: the router GEMV (no logits
     // given), the shared-expert weight, or the input RMSNorm
     m.router = (!logits && L->router) || L->shared_router != nullptr || L->norm_w != nullptr;
     m.grid_r = E->n + (L->shared_router ? 1u : 0u);
-    if (m.lds_b > kLdsBudget) return fail("gate/up tile exceeds the LDS budget");
 
-    const uint32_t n_sh_valu = a.n_sh_wg, grid_c_valu = m.grid_c;
-    const size_t lds_b_valu = m.lds_b;
+    const uint32_t grid_c_valu = m.grid_c;
     for (uint32_t t0 = 0; t0 < n_tok; t0 += kMaxTok) {
         const uint32_t T = n_tok - t0 < kMaxTok ? n_tok - t0 : kMaxTok;
         a.T = T;
         a.max_u = T * L->top_k;
-        m.mx = c->mode == 3 || (c->mode == 0 && T >= kMxMinTokens);
+        // automatic: the MFMA kernels from 3 tokens on, and for 2 when the fp32
+        // kernels would be the format-generic ones (mixed formats)
+        m.mx = c->mode == 3 || (c->mode == 0 && (T >= kMxMinTokens || (T == 2 && (m.fg < 0 || m.fd < 0))));
         a.xa = m.mx ? c->mxa : nullptr;   // k_moe_router writes the operands
-        a.n_sh_wg = n_sh_valu;
+        const uint32_t S = T == 2 ? 4u : 2u;                   // gu_steps<T>()
+        const uint32_t rows_wg = 4 * S * rpsg;                 // gate/up rows per workgroup
+        const uint32_t ntile_b = (L->inter + rows_wg - 1) / rows_wg;
+        a.n_sh_wg = has_sh ? ntile_b : 0;
+        m.lds_b = (size_t)tab_bytes(mgu) + 4 * S * a.gu_pb;
         m.grid_c = grid_c_valu;
-        m.lds_b = lds_b_valu;
         a.x = x + (size_t)t0 * L->hidden;
         a.xin = L->norm_w ? c->xn : a.x;
         a.router = logits ? nullptr : L->router;
@@ -2114,6 +2195,7 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
         m.lds_c = (size_t)tab_bytes(mdn) + (size_t)m.nw_c * kStepsDn * kSlotBytes +
                   (size_t)ntot * R_c * T * 4 + 16;
         if (!m.mx && m.lds_c > kLdsBudget) return fail("down tile exceeds the LDS budget");
+        if (!m.mx && m.lds_b > kMxLdsBudget) return fail("gate/up tile exceeds the LDS budget");
         m.router = (!logits && L->router) || L->shared_router != nullptr || L->norm_w != nullptr;
         m.grid_r = E->n + (L->shared_router ? 1u : 0u);
         if (m.mx) {
