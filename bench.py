@@ -30,7 +30,8 @@ sample of the same workload on this host, single thread as qw6 runs it.
   prefill_T512  512 tokens with Zipf(1.1)-skewed router logits through the
                 grouped bf16-MFMA kernels, Q4_K / Q6_K experts: us/layer,
                 TFLOP/s, MFMA fraction, HBM GB/s;
-  mtp_T2        two tokens (MTP draft verification) with the router GEMV;
+  mtp_T2        two tokens (MTP draft verification) with the router GEMV, and
+                small batches (3, 4, 8 tokens) through the automatic path;
   prefill_T512_iq2xxs_iq3s  the grouped kernels on an IQ layer (IQ2_XXS
                 gate/up, IQ3_S down, Q4_K / Q6_K shared expert).
 """
@@ -391,6 +392,21 @@ def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
               "distinct_experts_mean": round(float(np.mean([len(np.unique(s)) for s in sel])), 2),
               "workload": "T=2 through the per-token fp32 kernels with the router GEMV, "
                           "Q4_K/Q6_K layer pool"}
+    # small batches through the automatic path: 3-4 tokens per launch take the
+    # small-batch MFMA kernels, 8 the grouped ones
+    small = {}
+    for Ts in (3, 4, 8):
+        Xs = torch.empty(len(pool), Ts, HIDDEN, dtype=torch.float32, device="cuda")
+        for j in range(len(pool)):
+            Q.synth_normal(Xs[j], Ts * HIDDEN, 1.0, 4010 + Ts, S.stream_id(j, S.K_X))
+        os_ = torch.empty_like(Xs)
+
+        def fwds(sp, Ts=Ts, Xs=Xs, os_=os_):
+            for j in range(len(pool)):
+                ctx.moe_forward(pool[j].desc, Xs[j], os_[j], n_tok=Ts, stream=sp)
+        secs, _ = graph_time(torch, fwds, max(1, args.steps // len(pool)))
+        small["T%d" % Ts] = round(1e6 * secs / len(pool), 3)
+    res_t2["small_batch_us_per_layer"] = small
     return res, res_t2
 
 

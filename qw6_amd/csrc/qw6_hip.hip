@@ -451,14 +451,13 @@ __device__ __forceinline__ void wait_vm(uint32_t n) {
 // for token t, 0 if unused), s_idx / s_w (per-token selection) and *s_n.
 // keys: token `wave`'s logit keys, loaded by route_keys in waves < T.
 template <int T>
-__device__ __forceinline__ void route_prologue(const MoeArgs& a, uint32_t (&keys)[4],
+__device__ __forceinline__ void route_prologue(const MoeArgs& a, uint32_t (&keys)[4], uint2* scr,
                                                uint32_t* s_idx, float* s_w,
                                                uint32_t* s_slot_e, float* s_wt, uint32_t* s_n) {
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
-    __shared__ uint2 s_rt[4][kRouteScr];
     if (T == 1) {   // one token: the slots are the selection itself
         if (wave == 0) {
-            wave_route_keys(keys, a.top_k, s_rt[0], s_idx, s_w);
+            wave_route_keys(keys, a.top_k, scr, s_idx, s_w);
             __builtin_amdgcn_wave_barrier();
             if (lane < a.top_k) {
                 s_slot_e[lane] = s_idx[lane];
@@ -472,7 +471,7 @@ __device__ __forceinline__ void route_prologue(const MoeArgs& a, uint32_t (&keys
         return;
     }
     if (wave < (uint32_t)T)
-        wave_route_keys(keys, a.top_k, s_rt[wave], s_idx + wave * a.top_k, s_w + wave * a.top_k);
+        wave_route_keys(keys, a.top_k, scr + wave * kRouteScr, s_idx + wave * a.top_k, s_w + wave * a.top_k);
     __syncthreads();
     if (wave == 0) {
         const uint32_t ne = T * a.top_k;
@@ -570,20 +569,19 @@ __device__ __forceinline__ void mx_input_operands(const MoeArgs& a, uint32_t e, 
 // publishes nothing: waves t < T rank token t's logits (route_rank; no gate
 // weights), then every wave finds the slot from the T * top_k selections
 // with lane reads -- one barrier. Returns false if fewer than u + 1 slots.
+// scr: T * kRouteScr routing scratch, s_sel: T * top_k words (LDS).
 template <int T>
 __device__ __forceinline__ bool route_slot_select(const MoeArgs& a, uint32_t (&keys)[4], uint32_t u,
-                                                  uint32_t& e_out) {
-    __shared__ uint2 s_rs[kMaxTok][kRouteScr];
-    __shared__ uint32_t s_sel[kMaxSlots];
+                                                  uint32_t& e_out, uint2* scr, uint32_t* s_sel) {
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     if (wave < (uint32_t)T) {
         uint2 me2;
         uint32_t rank, ncand;
-        if (route_rank(keys, a.top_k, s_rs[wave], me2, rank, ncand)) {
+        if (route_rank(keys, a.top_k, scr + wave * kRouteScr, me2, rank, ncand)) {
             if (lane < ncand && rank < a.top_k)   // only -inf left: qw6 picks index 0
                 s_sel[wave * a.top_k + rank] = me2.y > kKeyNegInf ? ~me2.x : 0u;
         } else if (lane < a.top_k) {
-            const uint2 me = s_rs[wave][32 + lane];
+            const uint2 me = scr[wave * kRouteScr + 32 + lane];
             s_sel[wave * a.top_k + lane] = me.y > kKeyNegInf ? ~me.x : 0u;
         }
     }
@@ -745,6 +743,7 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ uint32_t s_idx[kMaxSlots], s_slot_e[kMaxSlots], s_n;
     __shared__ float s_w[kMaxSlots], s_wt[kMaxSlots * kMaxTok];
+    __shared__ uint2 s_route[T * kRouteScr];   // routing scratch, one per routing wave
     const uint32_t wave = threadIdx.x >> 6;
     constexpr int S = gu_steps<T>();
     constexpr uint32_t rps = 64 / KU;
@@ -791,7 +790,7 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
         const uint32_t b = blockIdx.x - a.n_sh_wg;
         const uint32_t u = b / ntile, tile = b % ntile;
         uint32_t e;
-        if (!route_slot_select<T>(a, keys, u, e)) return;
+        if (!route_slot_select<T>(a, keys, u, e, s_route, s_idx)) return;
         TRACE_MARK(2, 0);
         G = expert_mat(a, e, 0);
         Up = expert_mat(a, e, 1);
@@ -801,24 +800,22 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
     } else if (T == 1 && blockIdx.x != a.n_sh_wg) {
         // one token, not the publishing block: only the expert of this block's
         // rank is needed (no gate weights, no slot table)
-        __shared__ uint2 s_rt1[kRouteScr];
-        __shared__ uint32_t s_e1;
         const uint32_t b = blockIdx.x - a.n_sh_wg;
         const uint32_t u = b / ntile, tile = b % ntile;
         if (wave == 0) {
-            const uint32_t e = wave_route_select(keys, a.top_k, u, s_rt1);
-            if ((threadIdx.x & 63u) == 0) s_e1 = e;
+            const uint32_t e = wave_route_select(keys, a.top_k, u, s_route);
+            if ((threadIdx.x & 63u) == 0) s_n = e;
         }
         __syncthreads();
         TRACE_MARK(2, 0);
-        const uint32_t e = s_e1;
+        const uint32_t e = s_n;
         G = expert_mat(a, e, 0);
         Up = expert_mat(a, e, 1);
         row0 = (tile * 4 + wave) * S * rps;
         midp = a.mid + (size_t)u * T * a.inter;
         if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr, sx);
     } else {
-        route_prologue<T>(a, keys, s_idx, s_w, s_slot_e, s_wt, &s_n);   // ends with a barrier
+        route_prologue<T>(a, keys, s_route, s_idx, s_w, s_slot_e, s_wt, &s_n);   // ends with a barrier
         TRACE_MARK(2, 0);
         const uint32_t b = blockIdx.x - a.n_sh_wg;
         const uint32_t u = b / ntile, tile = b % ntile;
@@ -861,7 +858,7 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
 // Wave w takes matrices w, w + nw, ...; row sums meet in LDS and are
 // combined as out = sum_u wt[u] * y[u] + sw * y[shared] (+ residual).
 template <int T>
-__host__ __device__ constexpr uint32_t down_waves() { return T == 1 ? 9u : 8u; }
+__host__ __device__ constexpr uint32_t down_waves() { return T <= 2 ? 9u : 8u; }
 
 template <int T, int FD, int KU>
 __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
@@ -1063,23 +1060,22 @@ __device__ __forceinline__ bool mx_route_block(const MoeArgs& a, uint32_t (&keys
                                                uint32_t& u, uint32_t& tile, uint32_t& e) {
     __shared__ uint32_t s_idx[kMaxSlots], s_slot_e[kMaxSlots], s_n;
     __shared__ float s_w[kMaxSlots], s_wt[kMaxSlots * kMaxTok];
+    __shared__ uint2 s_route[T * kRouteScr];
     const uint32_t wave = threadIdx.x >> 6;
     const uint32_t b = blockIdx.x - a.n_sh_wg;
     u = b / ntile;
     tile = b % ntile;
     if (T == 1 && b != 0) {   // one token: only the expert of rank u
-        __shared__ uint2 s_rt1[kRouteScr];
-        __shared__ uint32_t s_e1;
         if (wave == 0) {
-            const uint32_t x = wave_route_select(keys, a.top_k, u, s_rt1);
-            if ((threadIdx.x & 63u) == 0) s_e1 = x;
+            const uint32_t x = wave_route_select(keys, a.top_k, u, s_route);
+            if ((threadIdx.x & 63u) == 0) s_n = x;
         }
         __syncthreads();
-        e = s_e1;
+        e = s_n;
         return true;
     }
-    if (b != 0) return route_slot_select<T>(a, keys, u, e);
-    route_prologue<T>(a, keys, s_idx, s_w, s_slot_e, s_wt, &s_n);   // ends with a barrier
+    if (b != 0) return route_slot_select<T>(a, keys, u, e, s_route, s_idx);
+    route_prologue<T>(a, keys, s_route, s_idx, s_w, s_slot_e, s_wt, &s_n);   // ends with a barrier
     const uint32_t nslot = s_n;
     if (b == 0) {
         const uint32_t tid = threadIdx.x;
