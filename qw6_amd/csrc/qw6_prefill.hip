@@ -513,25 +513,33 @@ __global__ __launch_bounds__(256) void k_pre_rmsnorm(const float* x, const float
 }
 
 // Router logits of T tokens: block (expert e, tokens 4c .. 4c+3), one wave.
+// NV = hidden / 256 float4 per lane, a template constant, so the router row
+// and the four tokens' inputs are requested at once (one memory round trip).
+template <int NV>
 __global__ __launch_bounds__(64) void k_pre_router(const float* __restrict__ router,
                                                    const float* __restrict__ x, float* logits,
-                                                   uint32_t n_experts, uint32_t hidden, uint32_t T) {
+                                                   uint32_t n_experts, uint32_t T) {
+    constexpr uint32_t hidden = 256 * NV;
     const uint32_t e = blockIdx.x, t0 = 4 * blockIdx.y, lane = threadIdx.x;
-    const float* wr = router + (size_t)e * hidden;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    for (uint32_t c = lane; c < hidden / 4; c += 64) {
-        const float4 w = ((const float4*)wr)[c];
+    const float4* wr = (const float4*)(router + (size_t)e * hidden);
+    float4 w[NV], xv[4][NV];
 #pragma unroll
-        for (uint32_t t = 0; t < 4; t++)
-            if (t0 + t < T) {
-                const float4 xv = ((const float4*)(x + (size_t)(t0 + t) * hidden))[c];
-                acc[t] = fmaf(w.x, xv.x, acc[t]); acc[t] = fmaf(w.y, xv.y, acc[t]);
-                acc[t] = fmaf(w.z, xv.z, acc[t]); acc[t] = fmaf(w.w, xv.w, acc[t]);
-            }
+    for (int i = 0; i < NV; i++) w[i] = wr[64 * i + lane];
+#pragma unroll
+    for (uint32_t t = 0; t < 4; t++) {
+        const float4* xr = (const float4*)(x + (size_t)min(t0 + t, T - 1) * hidden);
+#pragma unroll
+        for (int i = 0; i < NV; i++) xv[t][i] = xr[64 * i + lane];
     }
 #pragma unroll
     for (uint32_t t = 0; t < 4; t++) {
-        const float v = group_sum<64>(acc[t]);
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            acc = fmaf(w[i].x, xv[t][i].x, acc); acc = fmaf(w[i].y, xv[t][i].y, acc);
+            acc = fmaf(w[i].z, xv[t][i].z, acc); acc = fmaf(w[i].w, xv[t][i].w, acc);
+        }
+        const float v = group_sum<64>(acc);
         if (lane == 0 && t0 + t < T) logits[(size_t)(t0 + t) * n_experts + e] = v;
     }
 }
@@ -599,8 +607,14 @@ int prefill_forward(const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) 
     }
     const float* logits = L.logits;
     if (!logits) {
-        k_pre_router<<<dim3(L.n_experts, (L.T + 3) / 4), 64, 0, st>>>(L.router, xin, ws.logits,
-                                                                    L.n_experts, L.hidden, L.T);
+        const dim3 g(L.n_experts, (L.T + 3) / 4);
+        switch (L.hidden / 256) {
+        case 1: k_pre_router<1><<<g, 64, 0, st>>>(L.router, xin, ws.logits, L.n_experts, L.T); break;
+        case 2: k_pre_router<2><<<g, 64, 0, st>>>(L.router, xin, ws.logits, L.n_experts, L.T); break;
+        case 4: k_pre_router<4><<<g, 64, 0, st>>>(L.router, xin, ws.logits, L.n_experts, L.T); break;
+        case 8: k_pre_router<8><<<g, 64, 0, st>>>(L.router, xin, ws.logits, L.n_experts, L.T); break;
+        default: return qw6_fail("batched router needs hidden in {256, 512, 1024, 2048}");
+        }
         logits = ws.logits;
     }
     PrefillLayer Lx = L;
