@@ -62,6 +62,9 @@ def parse():
                     choices=["all", "q4k", "iq2m", "stack", "prefill"])
     ap.add_argument("--stack-steps", type=int, default=128)
     ap.add_argument("--prefill-tokens", type=int, default=512)
+    ap.add_argument("--no-small-batch", action="store_true",
+                    help="with --workload prefill: time the prefill_T512 case only (no T=2 and "
+                         "small-batch cases), for a kernel profile of that workload alone")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
@@ -456,11 +459,12 @@ def main():
             res_main = bench_decode(torch, Q, S, ctx, pool, X, out, idx, args)
             log("decode %s: %s" % (mix, json.dumps(res_main)))
     if want_prefill:
-        pf, t2 = bench_prefill(torch, Q, S, ctx, pool, args)
+        pf, t2 = bench_prefill(torch, Q, S, ctx, pool, args, with_t2=not args.no_small_batch)
         secondary["prefill_T%d" % args.prefill_tokens] = pf
-        secondary["mtp_T2"] = t2
         log("prefill: %s" % json.dumps(pf))
-        log("T=2: %s" % json.dumps(t2))
+        if t2 is not None:
+            secondary["mtp_T2"] = t2
+            log("T=2: %s" % json.dumps(t2))
 
     cpu = None
     if res_main is not None and not args.no_cpu:
