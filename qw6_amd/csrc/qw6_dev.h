@@ -56,15 +56,25 @@ __host__ __device__ inline uint32_t fmt_table_mask(int f) {
 
 // ---- IQ lattice tables --------------------------------------------------------
 
+// Per-token decoders read the tables from LDS at these offsets. Besides the
+// lattice grids they hold byte sign masks: entry s has byte n = 0xff when
+// weight n of the group of 8 is negative, else 0 (sgnxx is indexed by the
+// 7-bit IQ2_XXS sign field, whose eighth sign makes the count of negative
+// signs even, qw6.c:1590-1596; sgn8 by a plain sign byte). With them a
+// group's 8 signed grid values come from two integer ops per 4 bytes.
 struct IqTables {
+    uint64_t sgnxx[128];
     uint64_t iq2xxs[256];
-    uint64_t iq2s[1024];
+    uint64_t sgn8[256];
     uint32_t iq3s[512];
+    uint64_t iq2s[1024];
 };
-constexpr uint32_t kTabOffIq2xxs = 0;
-constexpr uint32_t kTabOffIq2s = 256 * 8;
-constexpr uint32_t kTabOffIq3s = kTabOffIq2s + 1024 * 8;
-constexpr uint32_t kTabBytes = kTabOffIq3s + 512 * 4;   // 12 KB
+constexpr uint32_t kTabOffSgnXX = 0;
+constexpr uint32_t kTabOffIq2xxs = 128 * 8;
+constexpr uint32_t kTabOffSgn8 = kTabOffIq2xxs + 256 * 8;
+constexpr uint32_t kTabOffIq3s = kTabOffSgn8 + 256 * 8;
+constexpr uint32_t kTabOffIq2s = kTabOffIq3s + 512 * 4;
+constexpr uint32_t kTabBytes = kTabOffIq2s + 1024 * 8;   // 15 KB
 
 constexpr uint64_t expand_iq2(uint16_t c) {
     uint64_t v = 0;
@@ -76,13 +86,31 @@ constexpr uint32_t expand_iq3(uint16_t c) {
     for (int j = 0; j < 4; j++) v |= (uint32_t)(2 * ((c >> (3 * j)) & 7) + 1) << (8 * j);
     return v;
 }
+constexpr uint64_t sign_mask8(uint32_t s) {
+    uint64_t v = 0;
+    for (int n = 0; n < 8; n++)
+        if ((s >> n) & 1u) v |= (uint64_t)0xffu << (8 * n);
+    return v;
+}
+constexpr uint32_t parity7(uint32_t s) {
+    uint32_t p = 0;
+    for (int n = 0; n < 7; n++) p ^= (s >> n) & 1u;
+    return p;
+}
 constexpr IqTables make_tables() {
     IqTables t{};
+    for (uint32_t i = 0; i < 128; i++) t.sgnxx[i] = sign_mask8(i | (parity7(i) << 7));
+    for (uint32_t i = 0; i < 256; i++) t.sgn8[i] = sign_mask8(i);
     for (int i = 0; i < 256; i++) t.iq2xxs[i] = expand_iq2(qw6_iq2xxs_codes[i]);
     for (int i = 0; i < 1024; i++) t.iq2s[i] = expand_iq2(qw6_iq2s_codes[i]);
     for (int i = 0; i < 512; i++) t.iq3s[i] = expand_iq3(qw6_iq3s_codes[i]);
     return t;
 }
+static_assert(__builtin_offsetof(IqTables, iq2xxs) == kTabOffIq2xxs &&
+              __builtin_offsetof(IqTables, sgn8) == kTabOffSgn8 &&
+              __builtin_offsetof(IqTables, iq3s) == kTabOffIq3s &&
+              __builtin_offsetof(IqTables, iq2s) == kTabOffIq2s && sizeof(IqTables) == kTabBytes,
+              "LDS table offsets");
 
 // ---- scalar helpers ------------------------------------------------------------
 
@@ -146,10 +174,17 @@ __device__ __forceinline__ float ub(uint32_t w, int n) {
     }
     return r;
 }
-// ±v where bit n of `signs` set means negative.
-__device__ __forceinline__ float sgn(float v, uint32_t signs, int n) {
-    return __uint_as_float(__float_as_uint(v) ^ (((signs >> n) & 1u) << 31));
+// Four grid bytes g (each 1..63) with the signs of byte mask m (0xff =
+// negative) as int8: (g ^ 0xff) + 1 = 256 - g per negated byte, no carry
+// between bytes since g > 0 (v_and + v_xad_u32).
+__device__ __forceinline__ uint32_t signed_bytes(uint32_t g, uint32_t m) {
+    uint32_t r;
+    asm("v_xad_u32 %0, %1, %2, %3" : "=v"(r) : "v"(g), "v"(m), "v"(m & 0x01010101u));
+    return r;
 }
+// Signed byte n of w as a float: one v_cvt_f32_i32 with a sign-extending
+// byte source select.
+__device__ __forceinline__ float sb(uint32_t w, int n) { return (float)(int8_t)(w >> (8 * n)); }
 
 // ---- activations for a unit ------------------------------------------------------
 
@@ -365,14 +400,14 @@ __device__ __forceinline__ void unit_iq2xxs(const uint32_t* s, uint32_t bo, int 
 #pragma unroll
     for (int l = 0; l < 4; l++) {
         const uint64_t g = lds64_tab(tab, kTabOffIq2xxs + 8 * ((aux0 >> (8 * l)) & 0xffu));
-        const uint32_t s7 = (aux1 >> (7 * l)) & 127u;
-        const uint32_t signs = s7 | ((__builtin_popcount(s7) & 1u) << 7);
-        const uint32_t g0 = (uint32_t)g, g1 = (uint32_t)(g >> 32);
+        const uint64_t m = lds64_tab(tab, kTabOffSgnXX + 8 * ((aux1 >> (7 * l)) & 127u));
+        const uint32_t w0 = signed_bytes((uint32_t)g, (uint32_t)m);
+        const uint32_t w1 = signed_bytes((uint32_t)(g >> 32), (uint32_t)(m >> 32));
 #pragma unroll
         for (int n = 0; n < 8; n++) {
-            const float gv = ub(n < 4 ? g0 : g1, n & 3);
+            const float gv = sb(n < 4 ? w0 : w1, n & 3);
 #pragma unroll
-            for (int t = 0; t < T; t++) sum[t] = fmaf(gv, sgn(xr[t][8 * l + n], signs, n), sum[t]);
+            for (int t = 0; t < T; t++) sum[t] = fmaf(gv, xr[t][8 * l + n], sum[t]);
         }
     }
 #pragma unroll
@@ -396,15 +431,16 @@ __device__ __forceinline__ void unit_iq2s(const uint32_t* s, uint32_t bo, int j,
     for (int l = 0; l < 4; l++) {
         const uint32_t gi = ((qs4 >> (8 * l)) & 0xffu) | ((qh << (8 - 2 * l)) & 0x300u);
         const uint64_t g = lds64_tab(tab, kTabOffIq2s + 8 * gi);
-        const uint32_t signs = (sg4 >> (8 * l)) & 0xffu;
-        const uint32_t g0 = (uint32_t)g, g1 = (uint32_t)(g >> 32);
+        const uint64_t m = lds64_tab(tab, kTabOffSgn8 + 8 * ((sg4 >> (8 * l)) & 0xffu));
+        const uint32_t w0 = signed_bytes((uint32_t)g, (uint32_t)m);
+        const uint32_t w1 = signed_bytes((uint32_t)(g >> 32), (uint32_t)(m >> 32));
 #pragma unroll
         for (int n = 0; n < 8; n++) {
-            const float gv = ub(n < 4 ? g0 : g1, n & 3);
+            const float gv = sb(n < 4 ? w0 : w1, n & 3);
 #pragma unroll
             for (int t = 0; t < T; t++) {
-                if (l < 2) s0[t] = fmaf(gv, sgn(xr[t][8 * l + n], signs, n), s0[t]);
-                else s1[t] = fmaf(gv, sgn(xr[t][8 * l + n], signs, n), s1[t]);
+                if (l < 2) s0[t] = fmaf(gv, xr[t][8 * l + n], s0[t]);
+                else s1[t] = fmaf(gv, xr[t][8 * l + n], s1[t]);
             }
         }
     }
@@ -432,16 +468,16 @@ __device__ __forceinline__ void unit_iq3s(const uint32_t* s, uint32_t bo, int j,
         const uint32_t qw = l < 2 ? qa : qb;
         const uint32_t i1 = ((qw >> (16 * (l & 1))) & 0xffu) | ((qh << (8 - 2 * l)) & 256u);
         const uint32_t i2 = ((qw >> (16 * (l & 1) + 8)) & 0xffu) | ((qh << (7 - 2 * l)) & 256u);
-        const uint32_t g1 = tab[(kTabOffIq3s >> 2) + i1];
-        const uint32_t g2 = tab[(kTabOffIq3s >> 2) + i2];
-        const uint32_t signs = (sg4 >> (8 * l)) & 0xffu;
+        const uint64_t m = lds64_tab(tab, kTabOffSgn8 + 8 * ((sg4 >> (8 * l)) & 0xffu));
+        const uint32_t w1 = signed_bytes(tab[(kTabOffIq3s >> 2) + i1], (uint32_t)m);
+        const uint32_t w2 = signed_bytes(tab[(kTabOffIq3s >> 2) + i2], (uint32_t)(m >> 32));
 #pragma unroll
         for (int n = 0; n < 4; n++) {
-            const float v1 = ub(g1, n), v2 = ub(g2, n);
+            const float v1 = sb(w1, n), v2 = sb(w2, n);
 #pragma unroll
             for (int t = 0; t < T; t++) {
-                sum[t] = fmaf(v1, sgn(xr[t][8 * l + n], signs, n), sum[t]);
-                sum[t] = fmaf(v2, sgn(xr[t][8 * l + 4 + n], signs, n + 4), sum[t]);
+                sum[t] = fmaf(v1, xr[t][8 * l + n], sum[t]);
+                sum[t] = fmaf(v2, xr[t][8 * l + 4 + n], sum[t]);
             }
         }
     }

@@ -154,16 +154,17 @@ __device__ __forceinline__ void stage_wait() {
 __device__ __forceinline__ void stage_tables_from(uint8_t* tab, uint32_t mask, uint32_t w0) {
     const uint8_t* g = (const uint8_t*)&g_tabs;
     const uint32_t nw = w0 ? 4u - w0 : 0xffffu;
-    if (mask & 1u) stage(tab + kTabOffIq2xxs, g + kTabOffIq2xxs, 256 * 8, w0, nw);
-    if (mask & 2u) stage(tab + kTabOffIq2s, g + kTabOffIq2s, 1024 * 8, w0, nw);
-    if (mask & 4u) stage(tab + kTabOffIq3s, g + kTabOffIq3s, 512 * 4, w0, nw);
+    if (mask & 1u) stage(tab, g, kTabOffSgn8, w0, nw);   // IQ2_XXS signs + grid
+    if (mask & 6u) stage(tab + kTabOffSgn8, g + kTabOffSgn8, kTabOffIq3s - kTabOffSgn8, w0, nw);
+    if (mask & 4u) stage(tab + kTabOffIq3s, g + kTabOffIq3s, kTabOffIq2s - kTabOffIq3s, w0, nw);
+    if (mask & 2u) stage(tab + kTabOffIq2s, g + kTabOffIq2s, kTabBytes - kTabOffIq2s, w0, nw);
 }
 __device__ __forceinline__ void stage_tables(uint8_t* tab, uint32_t mask) {
     stage_tables_from(tab, mask, 0);
 }
 
 __host__ __device__ inline uint32_t tab_bytes(uint32_t mask) {
-    return mask & 4u ? kTabBytes : mask & 2u ? kTabOffIq3s : mask & 1u ? kTabOffIq2s : 0u;
+    return mask & 2u ? kTabBytes : mask & 4u ? kTabOffIq2s : mask & 1u ? kTabOffSgn8 : 0u;
 }
 
 __host__ __device__ inline uint32_t align16(uint32_t n) { return (n + 15u) & ~15u; }
@@ -1513,8 +1514,7 @@ int launch_matvec(const MatD& W, const float* x, float* y, uint32_t n_tok, hipSt
             }
         } else {
             const uint32_t tmask = fmt_table_mask(W.fmt);
-            const uint32_t toff = tmask & 4u ? kTabBytes : tmask & 2u ? kTabOffIq3s
-                                : tmask & 1u ? kTabOffIq2s : 0u;
+            const uint32_t toff = tab_bytes(tmask);
             if (fast_k(W.cols)) {
                 const uint32_t U = W.cols / 32, rps = 64 / U;
                 const uint32_t R = 4 * rps * kStepsMv;   // multiple of 16 bytes: 32*steps*bb
