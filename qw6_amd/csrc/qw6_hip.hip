@@ -849,8 +849,19 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
         if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr, sx);
     }
     if (row0 >= a.inter) return;
-    wave_gate_up<T, FG, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, (const uint32_t*)smem,
-                            slot_off, a.gu_pb, (const uint32_t*)smem);
+    const uint32_t* lds = (const uint32_t*)smem;
+    if (FG >= 0) {
+        wave_gate_up<T, FG, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds);
+        return;
+    }
+    switch (G.fmt) {   // mixed formats: one switch per wave, each body specialised
+    case F_Q4K: wave_gate_up<T, F_Q4K, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_Q5K: wave_gate_up<T, F_Q5K, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_Q6K: wave_gate_up<T, F_Q6K, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_IQ2XXS: wave_gate_up<T, F_IQ2XXS, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_IQ2S: wave_gate_up<T, F_IQ2S, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    default: wave_gate_up<T, F_IQ3S, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    }
 }
 
 // Down projection + combine for rows [r0, r0 + R), R = S * rps. Matrix m of
@@ -860,6 +871,39 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
 // combined as out = sum_u wt[u] * y[u] + sw * y[shared] (+ residual).
 template <int T>
 __host__ __device__ constexpr uint32_t down_waves() { return T <= 2 ? 9u : 8u; }
+
+// The kStepsDn row steps of one down matrix staged in LDS, the lane's row at
+// byte offset boff0: per-lane unit dot products, reduced over the row's
+// lanes; ym[rl * T + t] = row rl's sum for token t.
+template <int T, int F, int KU>
+__device__ __forceinline__ void down_rows(const uint32_t* lds, uint32_t boff0, int j,
+                                          const float (&xr)[T][32], const float (&sx)[T][4],
+                                          float* ym) {
+    constexpr int S = kStepsDn;
+    constexpr uint32_t U = KU, rps = 64 / KU;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t unit = lane & (U - 1), q = lane / U;
+    const uint32_t boff = boff0 + (unit >> 3) * fmt_block_bytes(F);
+    float acc[T][S];
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        wait_vm(2u * (S - 1 - s));
+        float v[T];
+#pragma unroll
+        for (int t = 0; t < T; t++) v[t] = 0.f;
+        unit_dot<T>(F, lds, s * kSlotBytes + boff, j, lds, xr, sx, v);
+#pragma unroll
+        for (int t = 0; t < T; t++) acc[t][s] = v[t];
+    }
+    float r[T];
+#pragma unroll
+    for (int t = 0; t < T; t++) r[t] = reduce_scatter_k<S, KU>(acc[t]);
+    if ((unit & (U / S - 1)) == 0) {
+        const uint32_t rl = scatter_step<S>(lane, U) * rps + q;
+#pragma unroll
+        for (int t = 0; t < T; t++) ym[rl * T + t] = r[t];
+    }
+}
 
 template <int T, int FD, int KU>
 __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
@@ -878,7 +922,7 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
     float* ybuf = (float*)(smem + toff + nw * S * kSlotBytes);   // [m][R][T]
     uint8_t* slots = smem + toff + wave * S * kSlotBytes;
     const uint32_t slot_off = toff + wave * S * kSlotBytes;
-    const uint32_t unit = lane & (U - 1), blk = unit >> 3, q = lane / U;
+    const uint32_t unit = lane & (U - 1), q = lane / U;
     const int j = (int)(unit & 7);
     // The slot table is read in one round trip: the count, this wave's first
     // slot (speculatively: entries past the count are null) and the gate
@@ -924,28 +968,19 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
             wait_vm(8u * T + 2u * S);   // this wave's table loads (its oldest) have landed
             __syncthreads();            // and every other wave's: the tables are complete
         }
-        const uint32_t bb = fmt_block_bytes(f);
-        const uint32_t boff = slot_off + q * D.rb + blk * bb;
-        float acc[T][S];
-#pragma unroll
-        for (int s = 0; s < S; s++) {
-            wait_vm(2u * (S - 1 - s));
-            TRACE_MARK_IF(s == 0 && m == wave, 3, 1);
-            float v[T];
-#pragma unroll
-            for (int t = 0; t < T; t++) v[t] = 0.f;
-            unit_dot<T>(f, (const uint32_t*)smem, s * kSlotBytes + boff, j, (const uint32_t*)smem,
-                        xr, sx, v);
-#pragma unroll
-            for (int t = 0; t < T; t++) acc[t][s] = v[t];
-        }
-        float r[T];
-#pragma unroll
-        for (int t = 0; t < T; t++) r[t] = reduce_scatter_k<S, KU>(acc[t]);
-        if ((unit & (U / S - 1)) == 0) {
-            const uint32_t rl = scatter_step<S>(lane, U) * rps + q;
-#pragma unroll
-            for (int t = 0; t < T; t++) ybuf[(m * R + rl) * T + t] = r[t];
+        const uint32_t boff = slot_off + q * D.rb;   // the lane's row; + its block below
+        float* ym = ybuf + m * R * T;
+        if (FD >= 0) {
+            down_rows<T, FD, KU>((const uint32_t*)smem, boff, j, xr, sx, ym);
+        } else {   // mixed formats: one switch per matrix, each body specialised
+            switch (f) {
+            case F_Q4K: down_rows<T, F_Q4K, KU>((const uint32_t*)smem, boff, j, xr, sx, ym); break;
+            case F_Q5K: down_rows<T, F_Q5K, KU>((const uint32_t*)smem, boff, j, xr, sx, ym); break;
+            case F_Q6K: down_rows<T, F_Q6K, KU>((const uint32_t*)smem, boff, j, xr, sx, ym); break;
+            case F_IQ2XXS: down_rows<T, F_IQ2XXS, KU>((const uint32_t*)smem, boff, j, xr, sx, ym); break;
+            case F_IQ2S: down_rows<T, F_IQ2S, KU>((const uint32_t*)smem, boff, j, xr, sx, ym); break;
+            default: down_rows<T, F_IQ3S, KU>((const uint32_t*)smem, boff, j, xr, sx, ym); break;
+            }
         }
     }
     TRACE_MARK(3, 2);
