@@ -195,36 +195,34 @@ __host__ __device__ inline int x_layout(int f) {
 }
 
 // Load the 32 activations of unit j of block blk for format f from x (one
-// token, contiguous), and the partial sums the decoders use.
+// token, contiguous). The partial sums the K-quant decoders use come from
+// unit_x_sums, separately, so that a caller can issue further loads before
+// it waits for these.
 __device__ __forceinline__ void load_unit_x(int f, const float* __restrict__ x, uint32_t blk,
-                                            int j, float (&xr)[32], float (&sx)[4]) {
-    const float* b = x + blk * 256;
-    if (f == F_Q4K || f == F_Q5K) {
-        const float4* p0 = (const float4*)(b + 64 * (j >> 1) + 16 * (j & 1));
-        const float4* p1 = (const float4*)(b + 64 * (j >> 1) + 32 + 16 * (j & 1));
+                                            int j, float (&xr)[32]) {
+    // Load i fills xr[4i .. 4i+3] in every layout; only the addresses differ:
+    // Q4_K/Q5_K the runs 64(j/2) + 16(j%2) and +32 (16 values each), Q6_K
+    // the 8-runs 128(j/4) + 8(j%4) + 32k, IQ 32 contiguous values at 32j. The
+    // offsets are selected, not branched on, so a run-time format leaves one
+    // straight load sequence (no merge of alternative loads into the same
+    // registers, which would make the compiler wait for them).
+    const int lay = x_layout(f);
+    const uint32_t ju = (uint32_t)j;
+    const uint32_t base = lay == 0 ? 64u * (ju >> 1) + 16u * (ju & 1)
+                        : lay == 1 ? 128u * (ju >> 2) + 8u * (ju & 3) : 32u * ju;
+    const float* b = x + blk * 256 + base;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            float4 a = p0[i], c = p1[i];
-            xr[4 * i] = a.x; xr[4 * i + 1] = a.y; xr[4 * i + 2] = a.z; xr[4 * i + 3] = a.w;
-            xr[16 + 4 * i] = c.x; xr[17 + 4 * i] = c.y; xr[18 + 4 * i] = c.z; xr[19 + 4 * i] = c.w;
-        }
-    } else if (f == F_Q6K) {
-        const float* base = b + 128 * (j >> 2) + 8 * (j & 3);
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-            float4 a = *(const float4*)(base + 32 * k);
-            float4 c = *(const float4*)(base + 32 * k + 4);
-            xr[8 * k] = a.x; xr[8 * k + 1] = a.y; xr[8 * k + 2] = a.z; xr[8 * k + 3] = a.w;
-            xr[8 * k + 4] = c.x; xr[8 * k + 5] = c.y; xr[8 * k + 6] = c.z; xr[8 * k + 7] = c.w;
-        }
-    } else {
-        const float4* p = (const float4*)(b + 32 * j);
-#pragma unroll
-        for (int i = 0; i < 8; i++) {
-            float4 a = p[i];
-            xr[4 * i] = a.x; xr[4 * i + 1] = a.y; xr[4 * i + 2] = a.z; xr[4 * i + 3] = a.w;
-        }
+    for (uint32_t i = 0; i < 8; i++) {
+        const uint32_t add = lay == 0 ? 4u * i + (i >= 4 ? 16u : 0u)
+                           : lay == 1 ? 32u * (i >> 1) + 4u * (i & 1) : 4u * i;
+        const float4 v = *(const float4*)(b + add);
+        xr[4 * i] = v.x; xr[4 * i + 1] = v.y; xr[4 * i + 2] = v.z; xr[4 * i + 3] = v.w;
     }
+}
+
+// Partial activation sums of a unit for format f (Q4_K/Q5_K: the two 16-runs;
+// Q6_K: the four 8-runs; the IQ decoders use none).
+__device__ __forceinline__ void unit_x_sums(int f, const float (&xr)[32], float (&sx)[4]) {
     if (f == F_Q6K) {
 #pragma unroll
         for (int k = 0; k < 4; k++) {

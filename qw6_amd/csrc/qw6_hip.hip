@@ -144,6 +144,13 @@ __device__ __forceinline__ void stage(uint8_t* dst, const uint8_t* src, uint32_t
 
 __device__ __forceinline__ void wave_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Workgroup barrier without a memory fence, for LDS data whose writers have
+// each waited for their own LDS-direct loads (vmcnt) before it: the global
+// loads a wave still has in flight stay in flight (__syncthreads would wait
+// for all of them). The memory clobber keeps the compiler from moving LDS
+// accesses across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
 __device__ __forceinline__ void stage_wait() {
     wave_wait();
     __syncthreads();
@@ -210,12 +217,18 @@ __device__ __forceinline__ void tile_rows(int f_rt, const uint32_t* lds, uint32_
 
 template <int T, int FF>
 __device__ __forceinline__ void load_x_all(int f_rt, const float* x, uint32_t ldx, uint32_t K,
-                                           float (&xr)[T][32], float (&sx)[T][4]) {
+                                           float (&xr)[T][32]) {
     const int f = FF >= 0 ? FF : f_rt;
     const uint32_t U = K >> 5;
     const uint32_t unit = (threadIdx.x & 63) & (U - 1);
 #pragma unroll
-    for (int t = 0; t < T; t++) load_unit_x(f, x + (size_t)t * ldx, unit >> 3, (int)(unit & 7), xr[t], sx[t]);
+    for (int t = 0; t < T; t++) load_unit_x(f, x + (size_t)t * ldx, unit >> 3, (int)(unit & 7), xr[t]);
+}
+
+template <int T>
+__device__ __forceinline__ void x_sums_all(int f, const float (&xr)[T][32], float (&sx)[T][4]) {
+#pragma unroll
+    for (int t = 0; t < T; t++) unit_x_sums(f, xr[t], sx[t]);
 }
 
 // ---- single-matrix matvec --------------------------------------------------------
@@ -237,7 +250,8 @@ __global__ __launch_bounds__(kWG) void k_matvec(MatD W, const float* __restrict_
     stage_wait();
     const uint32_t* s = (const uint32_t*)smem;
     float xr[T][32], sx[T][4];
-    load_x_all<T, FF>(W.fmt, (const float*)(smem + xoff), W.cols, W.cols, xr, sx);
+    load_x_all<T, FF>(W.fmt, (const float*)(smem + xoff), W.cols, W.cols, xr);
+    x_sums_all<T>(FF >= 0 ? FF : W.fmt, xr, sx);
     tile_rows<T, kStepsMv, FF>(W.fmt, s, toff, W.rb, W.cols, xr, sx, nv, threadIdx.x >> 6,
                            [&](uint32_t rl, const float(&v)[T]) {
 #pragma unroll
@@ -267,7 +281,10 @@ __global__ __launch_bounds__(64) void k_matvec_generic(MatD W, const float* __re
         const int j = (int)(u & 7);
         float xr[T][32], sx[T][4];
 #pragma unroll
-        for (int t = 0; t < T; t++) load_unit_x(W.fmt, x + (size_t)t * W.cols, blk, j, xr[t], sx[t]);
+        for (int t = 0; t < T; t++) {
+            load_unit_x(W.fmt, x + (size_t)t * W.cols, blk, j, xr[t]);
+            unit_x_sums(W.fmt, xr[t], sx[t]);
+        }
         unit_dot<T>(W.fmt, s, toff + blk * bb, j, s, xr, sx, acc);
     }
 #pragma unroll
@@ -686,7 +703,7 @@ __global__ __launch_bounds__(64) void k_moe_router(MoeArgs a) {
 // lane's activations, loaded before the weights' addresses were known.
 template <int T, int FF, int KU>
 __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint32_t row0,
-                                             const float (&xr)[T][32], const float (&sx)[T][4],
+                                             const float (&xr)[T][32],
                                              float* mid, uint32_t inter, uint8_t* slots,
                                              const uint32_t* lds, uint32_t slot_off, uint32_t pb,
                                              const uint32_t* tab) {
@@ -704,6 +721,8 @@ __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint
         const size_t r = row0 + (size_t)s * rps;
         stage_pair(slots + s * pb, G.p + r * G.rb, Up.p + r * Up.rb, gbytes, nl);
     }
+    float sx[T][4];
+    x_sums_all<T>(f, xr, sx);
     const uint32_t boff = slot_off + q * G.rb + blk * bb;
     float ag[T][S], au[T][S];
 #pragma unroll
@@ -769,8 +788,8 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
     // gate/up format): their loads overlap the logits round trip.
     const bool early = !rwave && (FG >= 0 || shared_wg || a.pk[0].regular);
     const int fx = FG >= 0 ? FG : shared_wg ? a.sg.fmt : a.pk[0].fmt;
-    float xr[T][32], sx[T][4];
-    if (early) load_x_all<T, FG>(fx, a.xin, a.hidden, a.hidden, xr, sx);
+    float xr[T][32];
+    if (early) load_x_all<T, FG>(fx, a.xin, a.hidden, a.hidden, xr);
     if (a.tmask_gu && (!rwave || tw0 == 0)) {   // this wave's table loads have landed
         if (early) wait_vm(8u * T);
         else wait_vm(0);
@@ -797,7 +816,7 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
         Up = expert_mat(a, e, 1);
         row0 = (tile * 4 + wave) * S * rps;
         midp = a.mid + (size_t)u * T * a.inter;
-        if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr, sx);
+        if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr);
     } else if (T == 1 && blockIdx.x != a.n_sh_wg) {
         // one token, not the publishing block: only the expert of this block's
         // rank is needed (no gate weights, no slot table)
@@ -814,7 +833,7 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
         Up = expert_mat(a, e, 1);
         row0 = (tile * 4 + wave) * S * rps;
         midp = a.mid + (size_t)u * T * a.inter;
-        if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr, sx);
+        if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr);
     } else {
         route_prologue<T>(a, keys, s_route, s_idx, s_w, s_slot_e, s_wt, &s_n);   // ends with a barrier
         TRACE_MARK(2, 0);
@@ -846,21 +865,21 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
         Up = expert_mat(a, e, 1);
         row0 = (tile * 4 + wave) * S * rps;
         midp = a.mid + (size_t)u * T * a.inter;
-        if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr, sx);
+        if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr);
     }
     if (row0 >= a.inter) return;
     const uint32_t* lds = (const uint32_t*)smem;
     if (FG >= 0) {
-        wave_gate_up<T, FG, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds);
+        wave_gate_up<T, FG, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds);
         return;
     }
     switch (G.fmt) {   // mixed formats: one switch per wave, each body specialised
-    case F_Q4K: wave_gate_up<T, F_Q4K, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_Q5K: wave_gate_up<T, F_Q5K, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_Q6K: wave_gate_up<T, F_Q6K, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_IQ2XXS: wave_gate_up<T, F_IQ2XXS, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_IQ2S: wave_gate_up<T, F_IQ2S, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    default: wave_gate_up<T, F_IQ3S, KU>(G, Up, row0, xr, sx, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_Q4K: wave_gate_up<T, F_Q4K, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_Q5K: wave_gate_up<T, F_Q5K, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_Q6K: wave_gate_up<T, F_Q6K, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_IQ2XXS: wave_gate_up<T, F_IQ2XXS, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_IQ2S: wave_gate_up<T, F_IQ2S, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    default: wave_gate_up<T, F_IQ3S, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
     }
 }
 
@@ -877,13 +896,14 @@ __host__ __device__ constexpr uint32_t down_waves() { return T <= 2 ? 9u : 8u; }
 // lanes; ym[rl * T + t] = row rl's sum for token t.
 template <int T, int F, int KU>
 __device__ __forceinline__ void down_rows(const uint32_t* lds, uint32_t boff0, int j,
-                                          const float (&xr)[T][32], const float (&sx)[T][4],
-                                          float* ym) {
+                                          const float (&xr)[T][32], float* ym) {
     constexpr int S = kStepsDn;
     constexpr uint32_t U = KU, rps = 64 / KU;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t unit = lane & (U - 1), q = lane / U;
     const uint32_t boff = boff0 + (unit >> 3) * fmt_block_bytes(F);
+    float sx[T][4];
+    x_sums_all<T>(F, xr, sx);
     float acc[T][S];
 #pragma unroll
     for (int s = 0; s < S; s++) {
@@ -915,19 +935,16 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
     constexpr uint32_t R = S * rps;
     const uint32_t r0 = blockIdx.x * R;
     const uint32_t nw = blockDim.x >> 6;
-    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // wave index as a wave-uniform value: the slot-table reads below then
+    // become scalar loads
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const uint32_t has_sh = a.sd.p != nullptr ? 1u : 0u;
-    const uint32_t toff = tab_bytes(a.tmask_dn);
-    stage_tables(smem, a.tmask_dn);
-    float* ybuf = (float*)(smem + toff + nw * S * kSlotBytes);   // [m][R][T]
-    uint8_t* slots = smem + toff + wave * S * kSlotBytes;
-    const uint32_t slot_off = toff + wave * S * kSlotBytes;
-    const uint32_t unit = lane & (U - 1), q = lane / U;
-    const int j = (int)(unit & 7);
-    // The slot table is read in one round trip: the count, this wave's first
-    // slot (speculatively: entries past the count are null) and the gate
-    // weights are independent loads. The combine's residual and shared weight
-    // are fetched now too, not after the products.
+    // The slot table is read in one round trip: the count and this wave's
+    // first slot (speculatively: entries past the count are null) are scalar
+    // loads issued before anything else. Issued after the lattice tables'
+    // LDS-direct loads they would be vector loads whose use waits for every
+    // earlier vector load (the counter retires in order). The gate weights,
+    // the combine's residual and shared weight are fetched now too.
     const uint32_t nslot = a.slots->n;
     const uint32_t u0 = wave - has_sh;
     const bool first_sh = has_sh && wave == 0;
@@ -935,8 +952,17 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
     const uint8_t* p0 = a.slots->p[u0c];
     const int f0 = a.slots->fmt[u0c];
     const uint32_t rb0 = a.slots->rb[u0c];
-    if (threadIdx.x < kMaxSlots * kMaxTok)
-        s_wt[threadIdx.x] = a.slots->wt[threadIdx.x / kMaxTok][threadIdx.x % kMaxTok];
+    const uint32_t toff = tab_bytes(a.tmask_dn);
+    stage_tables(smem, a.tmask_dn);
+    float* ybuf = (float*)(smem + toff + nw * S * kSlotBytes);   // [m][R][T]
+    uint8_t* slots = smem + toff + wave * S * kSlotBytes;
+    const uint32_t slot_off = toff + wave * S * kSlotBytes;
+    const uint32_t unit = lane & (U - 1), q = lane / U;
+    const int j = (int)(unit & 7);
+    // (the gate weights go to LDS only after the products: an LDS write here
+    // would wait for every vector load issued before it)
+    const float wt_l = threadIdx.x < kMaxSlots * kMaxTok
+                           ? a.slots->wt[threadIdx.x / kMaxTok][threadIdx.x % kMaxTok] : 0.f;
     float resid = 0.f, shw = 1.0f;
     if (threadIdx.x < R * T) {
         const uint32_t rl = threadIdx.x / T, t = threadIdx.x % T;
@@ -944,46 +970,52 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
         if (has_sh && a.shared_router) shw = a.sw[t];
     }
     const uint32_t ntot = nslot + has_sh;
-    // every wave has at least one matrix (nw <= ntot): each issues its first
-    // matrix's loads before the barrier that makes the lattice tables visible
-    for (uint32_t m = wave; m < ntot; m += nw) {
+    // One matrix of this wave. The first is peeled off the loop below: every
+    // wave has at least one (nw <= ntot) and issues its loads before the
+    // barrier that makes the lattice tables visible, and a loop around it
+    // would make the compiler wait for all earlier vector loads (the gate
+    // weights, residual, lattice tables) before its activation loads.
+    auto matrix = [&](uint32_t m, bool first) {
         const bool sh = has_sh && m == 0;
         const uint32_t u = m - has_sh;
         const float* xm = a.mid + (size_t)(sh ? a.max_u : u) * T * a.inter;
-        float xr[T][32], sx[T][4];
+        float xr[T][32];
         // activations before the slot table's answer when their layout is
         // known already (one format, the shared expert, or one layout class)
         const int fx = FD >= 0 ? FD : sh ? a.sd.fmt : a.xl_dn;
-        if (fx >= 0) load_x_all<T, FD>(fx, xm, a.inter, a.inter, xr, sx);
+        if (fx >= 0) load_x_all<T, FD>(fx, xm, a.inter, a.inter, xr);
         const MatD D = sh ? a.sd
-                          : m == wave ? MatD{p0, f0, a.hidden, a.inter, rb0}
-                                      : MatD{a.slots->p[u], a.slots->fmt[u], a.hidden, a.inter,
-                                             a.slots->rb[u]};
+                          : first ? MatD{p0, f0, a.hidden, a.inter, rb0}
+                                  : MatD{a.slots->p[u], a.slots->fmt[u], a.hidden, a.inter,
+                                         a.slots->rb[u]};
         const int f = FD >= 0 ? FD : D.fmt;
-        if (fx < 0) load_x_all<T, FD>(f, xm, a.inter, a.inter, xr, sx);
+        if (fx < 0) load_x_all<T, FD>(f, xm, a.inter, a.inter, xr);
 #pragma unroll
         for (int s = 0; s < S; s++)
             stage_group(slots + s * kSlotBytes, D.p + (size_t)(r0 + s * rps) * D.rb, rps * D.rb);
-        if (a.tmask_dn && m == wave) {
+        if (a.tmask_dn && first) {
             wait_vm(8u * T + 2u * S);   // this wave's table loads (its oldest) have landed
-            __syncthreads();            // and every other wave's: the tables are complete
+            lds_barrier();              // and every other wave's: the tables are complete
         }
         const uint32_t boff = slot_off + q * D.rb;   // the lane's row; + its block below
         float* ym = ybuf + m * R * T;
         if (FD >= 0) {
-            down_rows<T, FD, KU>((const uint32_t*)smem, boff, j, xr, sx, ym);
+            down_rows<T, FD, KU>((const uint32_t*)smem, boff, j, xr, ym);
         } else {   // mixed formats: one switch per matrix, each body specialised
             switch (f) {
-            case F_Q4K: down_rows<T, F_Q4K, KU>((const uint32_t*)smem, boff, j, xr, sx, ym); break;
-            case F_Q5K: down_rows<T, F_Q5K, KU>((const uint32_t*)smem, boff, j, xr, sx, ym); break;
-            case F_Q6K: down_rows<T, F_Q6K, KU>((const uint32_t*)smem, boff, j, xr, sx, ym); break;
-            case F_IQ2XXS: down_rows<T, F_IQ2XXS, KU>((const uint32_t*)smem, boff, j, xr, sx, ym); break;
-            case F_IQ2S: down_rows<T, F_IQ2S, KU>((const uint32_t*)smem, boff, j, xr, sx, ym); break;
-            default: down_rows<T, F_IQ3S, KU>((const uint32_t*)smem, boff, j, xr, sx, ym); break;
+            case F_Q4K: down_rows<T, F_Q4K, KU>((const uint32_t*)smem, boff, j, xr, ym); break;
+            case F_Q5K: down_rows<T, F_Q5K, KU>((const uint32_t*)smem, boff, j, xr, ym); break;
+            case F_Q6K: down_rows<T, F_Q6K, KU>((const uint32_t*)smem, boff, j, xr, ym); break;
+            case F_IQ2XXS: down_rows<T, F_IQ2XXS, KU>((const uint32_t*)smem, boff, j, xr, ym); break;
+            case F_IQ2S: down_rows<T, F_IQ2S, KU>((const uint32_t*)smem, boff, j, xr, ym); break;
+            default: down_rows<T, F_IQ3S, KU>((const uint32_t*)smem, boff, j, xr, ym); break;
             }
         }
-    }
+    };
+    matrix(wave, true);
+    for (uint32_t m = wave + nw; m < ntot; m += nw) matrix(m, false);
     TRACE_MARK(3, 2);
+    if (threadIdx.x < kMaxSlots * kMaxTok) s_wt[threadIdx.x] = wt_l;
     __syncthreads();
     static_assert(R * T <= 64, "one combine output per thread of the smallest block");
     if (threadIdx.x < R * T) {
