@@ -72,12 +72,16 @@ struct TraceScope {
 #define TRACE_SCOPE(k) TraceScope trace_scope_(k)
 __device__ unsigned long long g_mark[4][4096][6];
 #ifdef QW6_TRACE_MARKS
-// Phase marks: wave 0's clock after its outstanding memory operations have
-// completed (the wait changes the kernel's timing; diagnostic builds only).
+#ifndef QW6_MARK_TID
+#define QW6_MARK_TID 0
+#endif
+// Phase marks: the clock of thread QW6_MARK_TID when it reaches the mark (no
+// added wait: a mark placed after a use of loaded data records when that data
+// arrived). Diagnostic builds only.
 #define TRACE_MARK(k, i)                                                            \
     do {                                                                            \
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");                 \
-        if (threadIdx.x == 0 && blockIdx.x < 4096) g_mark[k][blockIdx.x][i] = wall_clock64(); \
+        if (threadIdx.x == QW6_MARK_TID && blockIdx.x < 4096)                       \
+            g_mark[k][blockIdx.x][i] = wall_clock64();                              \
     } while (0)
 #else
 #define TRACE_MARK(k, i) do {} while (0)
@@ -404,6 +408,19 @@ __device__ __forceinline__ MatD expert_mat(const MoeArgs& a, uint32_t e, int k) 
     const ExpertEnt& E = a.experts[e];
     return MatD{E.p[k], E.fmt[k], rows, cols, E.rb[k]};
 }
+// The same for an expert index e that is equal on every lane of the wave.
+// The table does not change during a launch: read through the constant
+// address space, the uniform index gives scalar loads, which a later wait on
+// vector loads does not have to cover.
+__device__ __forceinline__ MatD expert_mat_wave(const MoeArgs& a, uint32_t e, int k) {
+    const PackRef& P = a.pk[k];
+    const uint32_t rows = k < 2 ? a.inter : a.hidden, cols = k < 2 ? a.hidden : a.inter;
+    e = __builtin_amdgcn_readfirstlane(e);
+    if (P.regular) return MatD{P.base + P.stride * e, P.fmt, rows, cols, P.rb};
+    using CE = __attribute__((address_space(4))) const ExpertEnt;
+    const CE& E = ((CE*)a.experts)[e];
+    return MatD{E.p[k], E.fmt[k], rows, cols, E.rb[k]};
+}
 
 // Stage one step group (the rows one wave step covers: 8 GGUF blocks, a
 // multiple of 16 bytes, <= 1680 B) into a 2 KB LDS slot with exactly two
@@ -441,26 +458,33 @@ __device__ __forceinline__ void stage_pair(uint8_t* slot, const uint8_t* g, cons
 }
 
 // Wait until at most n of this wave's vector-memory loads are outstanding
-// (n a compile-time constant after unrolling: the switch folds away).
+// (n a compile-time constant after unrolling). An s_waitcnt instruction the
+// compiler knows of: it counts the wait in its own bookkeeping, so later uses
+// of those loads' registers get no stricter wait of its making. gfx9
+// encoding: vmcnt bits 3:0 and 15:14; expcnt (7) and lgkmcnt (15) not waited.
+#define QW6_VMCNT(n) (((n) & 15u) | (((n) >> 4) << 14) | 0xf70u)
 __device__ __forceinline__ void wait_vm(uint32_t n) {
     switch (n) {
-    case 0: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-    case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
-    case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
-    case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
-    case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
-    case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-    case 9: asm volatile("s_waitcnt vmcnt(9)" ::: "memory"); break;
-    case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
-    case 12: asm volatile("s_waitcnt vmcnt(12)" ::: "memory"); break;
-    case 16: asm volatile("s_waitcnt vmcnt(16)" ::: "memory"); break;
-    case 20: asm volatile("s_waitcnt vmcnt(20)" ::: "memory"); break;
-    case 24: asm volatile("s_waitcnt vmcnt(24)" ::: "memory"); break;
-    case 28: asm volatile("s_waitcnt vmcnt(28)" ::: "memory"); break;
-    case 32: asm volatile("s_waitcnt vmcnt(32)" ::: "memory"); break;
-    case 36: asm volatile("s_waitcnt vmcnt(36)" ::: "memory"); break;
-    default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
+    case 2: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(2u)); break;
+    case 3: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(3u)); break;
+    case 4: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(4u)); break;
+    case 6: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(6u)); break;
+    case 8: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(8u)); break;
+    case 9: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(9u)); break;
+    case 10: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(10u)); break;
+    case 12: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(12u)); break;
+    case 14: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(14u)); break;
+    case 16: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(16u)); break;
+    case 20: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(20u)); break;
+    case 24: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(24u)); break;
+    case 28: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(28u)); break;
+    case 32: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(32u)); break;
+    case 36: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(36u)); break;
+    default: __builtin_amdgcn_s_waitcnt(QW6_VMCNT(0u)); break;
     }
+    // compiler barrier: no memory access (the LDS reads of what the waited
+    // loads wrote, in particular) moves across the wait
+    asm volatile("" ::: "memory");
 }
 
 // Routing of all T tokens inside one workgroup: wave t routes token t; the
@@ -699,11 +723,14 @@ __global__ __launch_bounds__(64) void k_moe_router(MoeArgs a) {
 }
 
 // gate/up/silu of one wave: S steps of rps rows starting at row0 of the pair
-// (G, Up) -> mid[T][inter]. slots: S LDS pair slots of pb bytes. xr/sx: this
-// lane's activations, loaded before the weights' addresses were known.
+// (G, Up) -> mid[T][inter]. slots: S LDS pair slots of pb bytes. x: the T
+// input rows (hidden values each); this lane's activations are requested
+// just before the weights, so both round trips overlap. bar: wait for the
+// block's earlier LDS-direct loads (the lattice tables) and meet the other
+// waves before reading them.
 template <int T, int FF, int KU>
 __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint32_t row0,
-                                             const float (&xr)[T][32],
+                                             const float* x, uint32_t hidden, bool bar,
                                              float* mid, uint32_t inter, uint8_t* slots,
                                              const uint32_t* lds, uint32_t slot_off, uint32_t pb,
                                              const uint32_t* tab) {
@@ -716,19 +743,29 @@ __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint
     const uint32_t bb = fmt_block_bytes(f);
     const uint32_t gbytes = rps * G.rb;   // one step group (8 blocks)
     const uint32_t nl = FF >= 0 ? pair_loads(FF) : pair_loads(f);
+    float xr[T][32];
+    load_x_all<T, FF>(f, x, hidden, hidden, xr);
 #pragma unroll
     for (int s = 0; s < S; s++) {
         const size_t r = row0 + (size_t)s * rps;
         stage_pair(slots + s * pb, G.p + r * G.rb, Up.p + r * Up.rb, gbytes, nl);
     }
-    float sx[T][4];
-    x_sums_all<T>(f, xr, sx);
+    TRACE_MARK(2, 5);
+    // nothing that reads the activations may be scheduled among the staging
+    // loads (its wait would hold back the loads after it)
+    __builtin_amdgcn_sched_barrier(0);
+    if (bar) {   // the block's earlier LDS-direct loads (the tables) are complete
+        wait_vm(nl * S + 8u * T);
+        lds_barrier();
+    }
     const uint32_t boff = slot_off + q * G.rb + blk * bb;
+    float sx[T][4];
     float ag[T][S], au[T][S];
 #pragma unroll
     for (int s = 0; s < S; s++) {
         wait_vm(nl * (S - 1 - s));
         TRACE_MARK_IF(s == 0, 2, 1);
+        if (s == 0) x_sums_all<T>(f, xr, sx);   // the activations landed before step 0's weights
         float g[T], u[T];
 #pragma unroll
         for (int t = 0; t < T; t++) { g[t] = 0.f; u[t] = 0.f; }
@@ -776,7 +813,7 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
     // Waves t < T of a routed block route token t. Their logits load is the
     // block's first memory operation (loads complete in issue order, so
     // nothing queued ahead of it delays the routing); the other waves stage
-    // the lattice tables and load their activations meanwhile.
+    // the lattice tables meanwhile.
     const bool rwave = !shared_wg && wave < (uint32_t)T;
     uint32_t keys[4];
     if (rwave) route_keys(a.route_logits + (size_t)wave * a.n_experts, a.n_experts, keys);
@@ -784,19 +821,15 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
     // (with T = 4 every wave routes, and the routing waves stage the tables too)
     const uint32_t tw0 = shared_wg || T >= 4 ? 0u : (uint32_t)T;
     stage_tables_from(smem, a.tmask_gu, tw0);
-    // Activations before the routing when their unit layout is known then (one
-    // gate/up format): their loads overlap the logits round trip.
-    const bool early = !rwave && (FG >= 0 || shared_wg || a.pk[0].regular);
-    const int fx = FG >= 0 ? FG : shared_wg ? a.sg.fmt : a.pk[0].fmt;
-    float xr[T][32];
-    if (early) load_x_all<T, FG>(fx, a.xin, a.hidden, a.hidden, xr);
-    if (a.tmask_gu && (!rwave || tw0 == 0)) {   // this wave's table loads have landed
-        if (early) wait_vm(8u * T);
-        else wait_vm(0);
-    }
-    // the lattice tables are in LDS before any wave reads them: the barrier
-    // below, or the one that ends route_prologue
-    if (a.tmask_gu && shared_wg) __syncthreads();
+    // Routed blocks: the staging waves wait for their table loads before the
+    // routing's barrier, which then makes the tables visible. Shared blocks
+    // issue their weight loads first and wait afterwards (wave_gate_up's bar).
+    // The activations are loaded in one place, wave_gate_up, just ahead of the
+    // weights: loads at several sites would meet in register copies that wait
+    // for every load in flight.
+    if (a.tmask_gu && !shared_wg && (!rwave || tw0 == 0)) wait_vm(0);
+    const bool bar = a.tmask_gu != 0 && shared_wg;
+    const float* xw = a.xin;
     MatD G, Up;
     uint32_t row0;
     float* midp;
@@ -812,11 +845,10 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
         uint32_t e;
         if (!route_slot_select<T>(a, keys, u, e, s_route, s_idx)) return;
         TRACE_MARK(2, 0);
-        G = expert_mat(a, e, 0);
-        Up = expert_mat(a, e, 1);
+        G = expert_mat_wave(a, e, 0);
+        Up = expert_mat_wave(a, e, 1);
         row0 = (tile * 4 + wave) * S * rps;
         midp = a.mid + (size_t)u * T * a.inter;
-        if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr);
     } else if (T == 1 && blockIdx.x != a.n_sh_wg) {
         // one token, not the publishing block: only the expert of this block's
         // rank is needed (no gate weights, no slot table)
@@ -829,11 +861,10 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
         __syncthreads();
         TRACE_MARK(2, 0);
         const uint32_t e = s_n;
-        G = expert_mat(a, e, 0);
-        Up = expert_mat(a, e, 1);
+        G = expert_mat_wave(a, e, 0);
+        Up = expert_mat_wave(a, e, 1);
         row0 = (tile * 4 + wave) * S * rps;
         midp = a.mid + (size_t)u * T * a.inter;
-        if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr);
     } else {
         route_prologue<T>(a, keys, s_route, s_idx, s_w, s_slot_e, s_wt, &s_n);   // ends with a barrier
         TRACE_MARK(2, 0);
@@ -861,25 +892,30 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
         }
         if (u >= nslot) return;
         const uint32_t e = s_slot_e[u];
-        G = expert_mat(a, e, 0);
-        Up = expert_mat(a, e, 1);
+        G = expert_mat_wave(a, e, 0);
+        Up = expert_mat_wave(a, e, 1);
         row0 = (tile * 4 + wave) * S * rps;
         midp = a.mid + (size_t)u * T * a.inter;
-        if (!early) load_x_all<T, FG>(G.fmt, a.xin, a.hidden, a.hidden, xr);
     }
-    if (row0 >= a.inter) return;
+    if (row0 >= a.inter) {   // (not for the shapes the host accepts)
+        if (bar) {   // still take part in the shared block's barrier
+            wait_vm(0);
+            lds_barrier();
+        }
+        return;
+    }
     const uint32_t* lds = (const uint32_t*)smem;
     if (FG >= 0) {
-        wave_gate_up<T, FG, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds);
+        wave_gate_up<T, FG, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds);
         return;
     }
     switch (G.fmt) {   // mixed formats: one switch per wave, each body specialised
-    case F_Q4K: wave_gate_up<T, F_Q4K, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_Q5K: wave_gate_up<T, F_Q5K, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_Q6K: wave_gate_up<T, F_Q6K, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_IQ2XXS: wave_gate_up<T, F_IQ2XXS, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_IQ2S: wave_gate_up<T, F_IQ2S, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    default: wave_gate_up<T, F_IQ3S, KU>(G, Up, row0, xr, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_Q4K: wave_gate_up<T, F_Q4K, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_Q5K: wave_gate_up<T, F_Q5K, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_Q6K: wave_gate_up<T, F_Q6K, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_IQ2XXS: wave_gate_up<T, F_IQ2XXS, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_IQ2S: wave_gate_up<T, F_IQ2S, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    default: wave_gate_up<T, F_IQ3S, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
     }
 }
 
@@ -993,6 +1029,7 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
 #pragma unroll
         for (int s = 0; s < S; s++)
             stage_group(slots + s * kSlotBytes, D.p + (size_t)(r0 + s * rps) * D.rb, rps * D.rb);
+        TRACE_MARK_IF(first, 3, 0);
         if (a.tmask_dn && first) {
             wait_vm(8u * T + 2u * S);   // this wave's table loads (its oldest) have landed
             lds_barrier();              // and every other wave's: the tables are complete
@@ -1011,6 +1048,7 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
             default: down_rows<T, F_IQ3S, KU>((const uint32_t*)smem, boff, j, xr, ym); break;
             }
         }
+        TRACE_MARK_IF(first, 3, 1);
     };
     matrix(wave, true);
     for (uint32_t m = wave + nw; m < ntot; m += nw) matrix(m, false);
