@@ -395,8 +395,9 @@ def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
               "distinct_experts_mean": round(float(np.mean([len(np.unique(s)) for s in sel])), 2),
               "workload": "T=2 through the per-token fp32 kernels with the router GEMV, "
                           "Q4_K/Q6_K layer pool"}
-    # small batches through the automatic path: 3-4 tokens per launch take the
-    # small-batch MFMA kernels, 8 the grouped ones
+    # small batches through the automatic path: 3 tokens per launch take the
+    # fp32 per-token kernels (one format per matrix kind), 4 the small-batch
+    # MFMA kernels, 8 the grouped ones
     small = {}
     for Ts in (3, 4, 8):
         Xs = torch.empty(len(pool), Ts, HIDDEN, dtype=torch.float32, device="cuda")

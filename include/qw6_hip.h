@@ -152,7 +152,8 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t *ctx, const qw6_hip_moe_layer_t *layer,
 
 /* Path selection for qw6_hip_moe_forward:
  * 0 = automatic (default): the fp32 per-token kernels for launches of 1-2
- *     tokens, the small-batch MFMA per-token kernels for 3-4, the grouped
+ *     tokens (and 3 when each matrix kind has one format), the small-batch
+ *     MFMA per-token kernels for 4 (and 3 with mixed formats), the grouped
  *     MFMA kernels from 5 tokens on (when every matrix kind has one routed
  *     format, else per-token launches);
  * 1 = always the fp32 per-token kernels;

@@ -50,7 +50,7 @@ __device__ const IqTables g_tabs = make_tables();
 constexpr int kWG = 256;           // threads per workgroup (4 waves)
 constexpr uint32_t kMaxTok = 4;    // tokens per decode launch
 constexpr uint32_t kGroupedMinTokens = 5;    // automatic switch to the grouped MFMA path
-constexpr uint32_t kMxMinTokens = 3;         // per-token launches of 3-4 tokens: k_mx_*
+constexpr uint32_t kMxMinTokens = 4;         // per-token launches of 4 tokens: k_mx_*
 constexpr uint32_t kLdsBudget = 64 * 1024;   // dynamic LDS per workgroup
 constexpr uint32_t kMxLdsBudget = 150 * 1024;   // k_mx_*: gfx950 has 160 KB per workgroup
 constexpr int kProfEv = 6;         // events per profiled MoE call (3 kernels x start/stop)
@@ -2271,9 +2271,10 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
         const uint32_t T = n_tok - t0 < kMaxTok ? n_tok - t0 : kMaxTok;
         a.T = T;
         a.max_u = T * L->top_k;
-        // automatic: the MFMA kernels from 3 tokens on, and for 2 when the fp32
-        // kernels would be the format-generic ones (mixed formats)
-        m.mx = c->mode == 3 || (c->mode == 0 && (T >= kMxMinTokens || (T == 2 && (m.fg < 0 || m.fd < 0))));
+        // automatic: the MFMA kernels for 4 tokens, and for 3 when the layer's
+        // formats are mixed (the fp32 kernels then dispatch per matrix)
+        m.mx = c->mode == 3 ||
+               (c->mode == 0 && (T >= kMxMinTokens || (T == kMxMinTokens - 1 && (m.fg < 0 || m.fd < 0))));
         a.xa = m.mx ? c->mxa : nullptr;   // k_moe_router writes the operands
         const uint32_t S = T == 2 ? 4u : 2u;                   // gu_steps<T>()
         const uint32_t rows_wg = 4 * S * rpsg;                 // gate/up rows per workgroup

@@ -1,6 +1,6 @@
 """Small-batch MFMA kernels (k_mx_gate_up / k_mx_down; qw6_hip_set_mode 3, and
-the automatic choice for 2-4 tokens per launch) against the oracle, through
-the C ABI.
+the automatic choice for 4 tokens per launch, 3 with mixed formats) against
+the oracle, through the C ABI.
 
 Same bars as the fp32 per-token kernels: expert indices bit-exact, outputs
 rel-L2 <= 1e-5 (the activations enter as three bf16 parts and the weights as
@@ -238,7 +238,8 @@ def test_mx_graph_replay_matches_eager(torch_dev, ctx):
 
 def test_auto_mode_mixed_chunks_vs_oracle(torch_dev, ctx):
     """Automatic path selection on 5 and 7 tokens: launches of 4 tokens (MFMA
-    kernels) followed by 1 (fp32 kernels) or 3 (MFMA) in one call."""
+    kernels) followed by 1 or 3 (fp32 kernels, one format per matrix kind) in
+    one call."""
     from qw6_amd.workload import SynthLayer
     L = SynthLayer(ctx, 67, 0, "q4k")
     try:
@@ -249,5 +250,24 @@ def test_auto_mode_mixed_chunks_vs_oracle(torch_dev, ctx):
             out, idx = run(torch_dev, ctx, L, xs, 0)
             n += check_tokens(L, xs, out, idx, router=router)
         assert n >= 10
+    finally:
+        L.free()
+
+
+def test_auto_mode_mixed_formats_vs_oracle(torch_dev, ctx):
+    """Automatic path selection on a mixed-format layer (IQ2_XXS routed with a
+    Q4_K shared gate/up, IQ3_S / IQ2_S routed down with a Q6_K shared down):
+    2 tokens take the fp32 kernels' per-matrix format dispatch, 3 and 4 the
+    MFMA kernels."""
+    from qw6_amd.workload import SynthLayer
+    L = SynthLayer(ctx, 68, 0, "iq2m")
+    try:
+        router = L.router_host()
+        n = 0
+        for T in (2, 3, 4):
+            xs = np.stack([cases.token_x(680 + T, 1, t) for t in range(T)])
+            out, idx = run(torch_dev, ctx, L, xs, 0)
+            n += check_tokens(L, xs, out, idx, router=router)
+        assert n >= 8
     finally:
         L.free()
