@@ -177,6 +177,30 @@ int qw6_hip_rmsnorm(qw6_hip_ctx_t *ctx, const float *x, const float *w,
                     float *y, uint32_t n, uint32_t n_tok, float eps,
                     void *stream);
 
+/* ---- output head: greedy next token ------------------------------------- */
+
+/* Index of the maximum of x[0..n), n >= 1, bit-exact with qw6_cpu_argmax
+ * (qw6.c:2858-2863): the first index whose value is strictly greater than
+ * every earlier one (ties -> lowest index; NaNs never win; a NaN at index 0
+ * gives 0). Device op, the role of qw6's argmax.comp dispatch
+ * (qw6_vk_pipe_sample_greedy, qw6_vk.c:3467-3478): x and *out device
+ * pointers, asynchronous on `stream`. Uses a 4 KB context workspace
+ * allocated on first use. */
+int qw6_hip_argmax(qw6_hip_ctx_t *ctx, const float *x, uint32_t n,
+                   uint32_t *out, void *stream);
+/* The same, synchronous, host buffers in and out. */
+int qw6_hip_argmax_host(const float *x, uint32_t n, uint32_t *out);
+
+/* Greedy token of the output head (qw6_forward_token's tail, qw6.c:2490-2493,
+ * then qw6_cpu_argmax; the GPU path of qw6_vk_pipe_forward_greedy,
+ * qw6_vk.c:3447-3478): logits = deq(W) rmsnorm(x) * norm_w, *token =
+ * argmax(logits). W: [vocab x hidden] (GGUF format or F32); norm_w NULL skips
+ * the norm; logits: device buffer of W->rows floats (written, as qw6's
+ * scr_logits); token: one device uint32. Asynchronous on `stream`. */
+int qw6_hip_output_greedy(qw6_hip_ctx_t *ctx, const qw6_hip_matrix_t *w,
+                          const float *x, const float *norm_w, float eps,
+                          float *logits, uint32_t *token, void *stream);
+
 /* ---- seeded synthetic data on the device -------------------------------- */
 
 /* Fill `nblocks` GGUF blocks of format `quant` from (seed, stream), starting

@@ -51,6 +51,8 @@ def lib():
         L.orc_matvec.argtypes = [_f32p, C.POINTER(OrcMat), _f32p, C.c_uint32, C.c_int]
         L.orc_moe_route.argtypes = [_i32p, _f32p, _f32p, C.c_int, C.c_int]
         L.orc_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_float]
+        L.orc_argmax.restype = C.c_int
+        L.orc_argmax.argtypes = [_f32p, C.c_int]
         L.orc_silu.restype = C.c_float
         L.orc_silu.argtypes = [C.c_float]
         L.orc_silu_mul.argtypes = [_f32p, _f32p, _f32p, C.c_uint32]
@@ -83,6 +85,8 @@ def ref():
                                     C.c_void_p, C.c_int, C.c_void_p, C.c_int,
                                     C.c_void_p, C.c_int, _f32p]
         R.ref_moe_layer_logits.argtypes = R.ref_moe_layer.argtypes
+        R.qw6_cpu_argmax.restype = C.c_int
+        R.qw6_cpu_argmax.argtypes = [_f32p, C.c_int]
         _ref = R
     return _ref
 
@@ -125,6 +129,11 @@ def moe_route(logits: np.ndarray, top_k: int):
     w = np.zeros(top_k, np.float32)
     lib().orc_moe_route(idx, w, logits, logits.size, top_k)
     return idx, w
+
+
+def argmax(x: np.ndarray) -> int:
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    return int(lib().orc_argmax(x, x.size))
 
 
 def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:

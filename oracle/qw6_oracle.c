@@ -374,6 +374,21 @@ void orc_silu_mul(const float *gate, const float *up, float *out, uint32_t n) {
     for (uint32_t i = 0; i < n; i++) out[i] = orc_silu(gate[i]) * up[i];
 }
 
+/* qw6_cpu_argmax (qw6.c:2858-2863): a running maximum that only a strictly
+ * greater value replaces, so ties keep the lowest index, NaNs are never
+ * taken, and a NaN at index 0 is never replaced. */
+int orc_argmax(const float *x, int n) {
+    int best = 0;
+    float bv = x[0];
+    for (int i = 1; i < n; i++) {
+        if (x[i] > bv) {
+            bv = x[i];
+            best = i;
+        }
+    }
+    return best;
+}
+
 /* out[i] = sum_e w_e * E[e][i] (+ s * shared[i]) in expert order
  * (vulkan/moe_gather.comp; host wrapper qw6_vk.c:929-970). */
 void orc_moe_gather(const float *expert_out, const float *expert_weights,

@@ -57,6 +57,9 @@ void orc_moe_route(int *idx, float *weights, const float *logits,
                    int n_experts, int top_k);
 void orc_rmsnorm(float *out, const float *x, const float *w, int dim,
                  float eps);
+/* Greedy next token: the first index whose value is strictly greater than
+ * every earlier one (qw6_cpu_argmax, qw6.c:2858-2863). n >= 1. */
+int orc_argmax(const float *x, int n);
 float orc_silu(float x);
 float orc_sigmoid(float x);
 void orc_silu_mul(const float *gate, const float *up, float *out, uint32_t n);

@@ -92,6 +92,11 @@ def lib():
                                            C.POINTER(C.c_uint32)]
         L.qw6_hip_rmsnorm.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                       C.c_uint32, C.c_uint32, C.c_float, C.c_void_p]
+        L.qw6_hip_argmax.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p]
+        L.qw6_hip_argmax_host.argtypes = [_f32p, C.c_uint32, _u32p]
+        L.qw6_hip_output_greedy.argtypes = [C.c_void_p, C.POINTER(Matrix), C.c_void_p,
+                                            C.c_void_p, C.c_float, C.c_void_p, C.c_void_p,
+                                            C.c_void_p]
         L.qw6_hip_synth_blocks.argtypes = [C.c_void_p, C.c_int32, C.c_uint64, C.c_uint64,
                                            C.c_uint64, C.c_uint64, C.c_void_p]
         L.qw6_hip_synth_normal.argtypes = [C.c_void_p, C.c_uint64, C.c_float, C.c_float,
@@ -156,6 +161,14 @@ def rmsnorm_host(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
     _check(lib().qw6_hip_rmsnorm_host(np.ascontiguousarray(x, np.float32),
                                       np.ascontiguousarray(w, np.float32), y, x.size, eps))
     return y
+
+
+def argmax_host(x: np.ndarray) -> int:
+    """First index of the maximum, qw6_cpu_argmax semantics (qw6.c:2858-2863)."""
+    x = np.ascontiguousarray(x, np.float32).reshape(-1)
+    out = np.zeros(1, np.uint32)
+    _check(lib().qw6_hip_argmax_host(x, x.size, out))
+    return int(out[0])
 
 
 # ---- device-resident API ----------------------------------------------------------
@@ -254,6 +267,17 @@ class Context:
     def rmsnorm(self, x, w, y, n: int, n_tok: int = 1, eps: float = 1e-6, stream=None):
         _check(lib().qw6_hip_rmsnorm(self.handle, _addr(x), _addr(w), _addr(y), n, n_tok, eps,
                                      _stream(stream)))
+
+    def argmax(self, x, n: int, out, stream=None):
+        """out[0] = first index of the maximum of x[:n] (device buffers)."""
+        _check(lib().qw6_hip_argmax(self.handle, _addr(x), n, _addr(out), _stream(stream)))
+
+    def output_greedy(self, w: tuple, x, logits, token, norm_w=None, eps: float = 1e-6,
+                      stream=None):
+        """logits = W rmsnorm(x) * norm_w (no norm without norm_w); token[0] = argmax."""
+        m = Matrix(*w)
+        _check(lib().qw6_hip_output_greedy(self.handle, C.byref(m), _addr(x), _addr(norm_w), eps,
+                                           _addr(logits), _addr(token), _stream(stream)))
 
 
 def make_layer(hidden: int, inter: int, top_k: int, experts: Experts, router=None,

@@ -1426,6 +1426,72 @@ __global__ void k_silu_mul(const float* g, const float* u, float* o, uint32_t n)
     if (i < n) o[i] = g[i] / (1.0f + expf(-g[i])) * u[i];
 }
 
+// ---- greedy argmax (qw6_cpu_argmax, qw6.c:2858-2863) ----------------------------
+// qw6 scans i = 1 .. n-1 and keeps the first index whose value is strictly
+// greater than the best so far: ties go to the lowest index, a NaN never
+// wins, and a NaN at index 0 is never replaced (every comparison with it is
+// false). Each value becomes the 64-bit key (order key of the value, ~index),
+// a NaN the order key 0 (below -inf), so the largest key is the first maximum;
+// the NaN-at-0 rule is applied at the end. The maximum is exact and
+// associative: how the range is split over blocks cannot change the result.
+constexpr uint32_t kArgmaxBlocks = 512;   // partial maxima of the first pass
+
+__device__ __forceinline__ uint64_t amax_key(float v, uint32_t i) {
+    const uint32_t k = v != v ? 0u : route_key(v);
+    return ((uint64_t)k << 32) | (uint32_t)~i;
+}
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+// Maximum over the 64 lanes of a wave; every lane receives it.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    const uint32_t lane = threadIdx.x & 63u;
+#pragma unroll
+    for (int i = 0; i < 6; i++) {
+        const uint32_t m = 32u >> i;
+        const uint32_t lo = __float_as_uint(partner(__uint_as_float((uint32_t)v), m, lane));
+        const uint32_t hi = __float_as_uint(partner(__uint_as_float((uint32_t)(v >> 32)), m, lane));
+        v = max_u64(v, ((uint64_t)hi << 32) | lo);
+    }
+    return v;
+}
+// Maximum over a 256-thread block, returned to thread 0.
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* s4) {
+    v = wave_max_u64(v);
+    if ((threadIdx.x & 63u) == 0) s4[threadIdx.x >> 6] = v;
+    __syncthreads();
+    return max_u64(max_u64(s4[0], s4[1]), max_u64(s4[2], s4[3]));
+}
+
+// First pass: block b takes every gridDim.x-th float4 (then the tail).
+__global__ __launch_bounds__(256) void k_argmax_part(const float* __restrict__ x, uint32_t n,
+                                                     uint64_t* __restrict__ part) {
+    __shared__ uint64_t s4[4];
+    uint64_t best = 0;   // below every element's key (index 0xffffffff)
+    const uint32_t t0 = blockIdx.x * 256 + threadIdx.x, stride = gridDim.x * 256;
+    const uint32_t n4 = ((uintptr_t)x & 15u) ? 0u : n / 4;
+    for (uint32_t i = t0; i < n4; i += stride) {
+        const float4 v = ((const float4*)x)[i];
+        best = max_u64(best, max_u64(max_u64(amax_key(v.x, 4 * i), amax_key(v.y, 4 * i + 1)),
+                                     max_u64(amax_key(v.z, 4 * i + 2), amax_key(v.w, 4 * i + 3))));
+    }
+    for (uint32_t i = 4 * n4 + t0; i < n; i += stride) best = max_u64(best, amax_key(x[i], i));
+    best = block_max_u64(best, s4);
+    if (threadIdx.x == 0) part[blockIdx.x] = best;
+}
+
+// Second pass: one block over the nb partial maxima.
+__global__ __launch_bounds__(256) void k_argmax_final(const float* __restrict__ x,
+                                                      const uint64_t* __restrict__ part,
+                                                      uint32_t nb, uint32_t* out) {
+    __shared__ uint64_t s4[4];
+    uint64_t best = 0;
+    for (uint32_t i = threadIdx.x; i < nb; i += 256) best = max_u64(best, part[i]);
+    best = block_max_u64(best, s4);
+    if (threadIdx.x == 0) {
+        const float x0 = x[0];
+        out[0] = x0 != x0 ? 0u : ~(uint32_t)best;
+    }
+}
+
 __global__ void k_gather(const float* eo, const float* ew, const float* sh, float sw,
                          float* o, uint32_t dim, uint32_t top_k) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1525,6 +1591,10 @@ struct qw6_hip_ctx_s {
     // per-kernel timing (qw6_hip_profile)
     std::vector<hipEvent_t> prof_ev;
     uint32_t prof_cap, prof_calls;
+    // argmax partial maxima; output head's normalised input
+    uint64_t* amax_part;
+    float* head_x;
+    uint32_t head_hidden;
 };
 
 struct qw6_hip_experts_s {
@@ -1646,6 +1716,16 @@ int launch_matvec(const MatD& W, const float* x, float* y, uint32_t n_tok, hipSt
     return 0;
 }
 
+// Two passes over n >= 1 floats: at most kArgmaxBlocks partial maxima, then one
+// block over them. part: kArgmaxBlocks words of scratch.
+int launch_argmax(const float* x, uint32_t n, uint64_t* part, uint32_t* out, hipStream_t st) {
+    const uint32_t nb = std::min(kArgmaxBlocks, (n + 1023u) / 1024u);
+    k_argmax_part<<<nb, 256, 0, st>>>(x, n, part);
+    k_argmax_final<<<1, 256, 0, st>>>(x, part, nb, out);
+    CK(hipGetLastError());
+    return 0;
+}
+
 struct DevBuf {
     void* p = nullptr;
     ~DevBuf() {
@@ -1676,6 +1756,14 @@ int alloc_owned(qw6_hip_ctx_t* c, size_t bytes, void** p) {
     CK(hipMalloc(p, bytes ? bytes : 16));
     c->owned.push_back(*p);
     CK(hipMemset(*p, 0, bytes ? bytes : 16));
+    return 0;
+}
+
+int ensure_argmax_ws(qw6_hip_ctx_t* c) {
+    if (c->amax_part) return 0;
+    void* p;
+    if (alloc_owned(c, (size_t)kArgmaxBlocks * 8, &p)) return -1;
+    c->amax_part = (uint64_t*)p;
     return 0;
 }
 
@@ -2357,6 +2445,56 @@ int qw6_hip_profile_read(qw6_hip_ctx_t* c, float ms[3], uint32_t* calls) {
     }
     *calls = c->prof_calls;
     return 0;
+}
+
+int qw6_hip_argmax_host(const float* x, uint32_t n, uint32_t* out) {
+    if (!x || !out) return fail("null pointer");
+    if (n == 0) return fail("argmax of an empty vector");
+    DevBuf bx, bp, bo;
+    CK(hipMalloc(&bx.p, (size_t)n * 4));
+    CK(hipMalloc(&bp.p, (size_t)kArgmaxBlocks * 8));
+    CK(hipMalloc(&bo.p, 4));
+    CK(hipMemcpy(bx.p, x, (size_t)n * 4, hipMemcpyHostToDevice));
+    if (launch_argmax((const float*)bx.p, n, (uint64_t*)bp.p, (uint32_t*)bo.p, nullptr)) return -1;
+    CK(hipDeviceSynchronize());
+    CK(hipMemcpy(out, bo.p, 4, hipMemcpyDeviceToHost));
+    return 0;
+}
+
+int qw6_hip_argmax(qw6_hip_ctx_t* c, const float* x, uint32_t n, uint32_t* out, void* stream) {
+    if (!c || !x || !out) return fail("null pointer");
+    if (n == 0) return fail("argmax of an empty vector");
+    DevGuard g(c->device);
+    if (ensure_argmax_ws(c)) return -1;
+    return launch_argmax(x, n, c->amax_part, out, (hipStream_t)stream);
+}
+
+int qw6_hip_output_greedy(qw6_hip_ctx_t* c, const qw6_hip_matrix_t* w, const float* x,
+                          const float* norm_w, float eps, float* logits, uint32_t* token,
+                          void* stream) {
+    if (!c || !w || !w->data || !x || !logits || !token) return fail("null pointer");
+    int f;
+    if (check_matrix(w->quant, w->rows, w->cols, &f)) return -1;
+    if ((uintptr_t)w->data & 15u) return fail("weight data not 16-byte aligned");
+    DevGuard g(c->device);
+    const hipStream_t st = (hipStream_t)stream;
+    if (ensure_argmax_ws(c)) return -1;
+    const float* xin = x;
+    if (norm_w) {   // final RMSNorm (qw6.c:2490-2492)
+        if (!c->head_x || c->head_hidden < w->cols) {
+            void* p;
+            if (alloc_owned(c, (size_t)w->cols * 4, &p)) return -1;
+            c->head_x = (float*)p;
+            c->head_hidden = w->cols;
+        }
+        k_rmsnorm<<<1, kWG, 0, st>>>(x, norm_w, c->head_x, w->cols, eps);
+        CK(hipGetLastError());
+        xin = c->head_x;
+    }
+    const uint32_t rb = w->quant == 0 ? w->cols * 4 : (w->cols / 256) * fmt_block_bytes(f);
+    const MatD W = {(const uint8_t*)w->data, w->quant == 0 ? -1 : f, w->rows, w->cols, rb};
+    if (launch_matvec(W, xin, logits, 1, st)) return -1;   // qw6.c:2493
+    return launch_argmax(logits, w->rows, c->amax_part, token, st);
 }
 
 int qw6_hip_rmsnorm(qw6_hip_ctx_t* c, const float* x, const float* w, float* y, uint32_t n,

@@ -48,6 +48,7 @@ HASHES_PER_BLOCK = 40
 # stream kinds
 K_ROUTER, K_GATE, K_UP, K_DOWN = 1, 2, 3, 4
 K_SGATE, K_SUP, K_SDOWN, K_X, K_NORM, K_SROUTER = 5, 6, 7, 8, 9, 11
+K_OUTPUT, K_ONORM = 12, 13   # output head: [vocab x hidden] weights, final norm
 
 
 def stream_id(layer: int, kind: int, expert: int = 0) -> int:

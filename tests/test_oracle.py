@@ -343,3 +343,57 @@ def test_planted_mistakes_are_caught():
     w2[:, :, 5] &= 0xC0
     assert not np.array_equal(bits(O.matvec(S.Q_Q4_K_M, w2.reshape(-1), 512, 2048, x)),
                               bits(G["cfg0_y"]))
+
+
+# ---- greedy argmax (qw6_cpu_argmax, qw6.c:2858-2863) -------------------------------
+
+def test_argmax_special_cases_and_selftest_kat():
+    for x, want in cases.argmax_cases():
+        assert O.argmax(np.array(x, np.float32)) == want, x
+
+
+def test_argmax_brute_force_vs_numpy():
+    """NaN-free inputs: numpy's argmax also returns the first maximum."""
+    rng = np.random.default_rng(7)
+    for n in (1, 2, 3, 17, 1000, 4099):
+        for trial in range(20):
+            x = rng.integers(-5, 6, n).astype(np.float32)   # many ties
+            assert O.argmax(x) == int(np.argmax(x)), (n, trial)
+            y = rng.standard_normal(n).astype(np.float32)
+            assert O.argmax(y) == int(np.argmax(y))
+
+
+@pytest.mark.skipif(O.ref() is None, reason="reference tree not built here")
+def test_argmax_vs_reference_build():
+    """Bitwise the reference's own function on random vectors with planted
+    ties, NaNs, infinities and signed zeros."""
+    rng = np.random.default_rng(11)
+    R = O.ref()
+    for x, _ in cases.argmax_cases():
+        a = np.array(x, np.float32)
+        assert O.argmax(a) == R.qw6_cpu_argmax(a, a.size)
+    for n in (1, 5, 257, 248320):
+        for trial in range(8):
+            x = rng.standard_normal(n).astype(np.float32)
+            k = rng.integers(0, n, size=min(n, 6))
+            x[k[: len(k) // 2]] = x.max()                      # ties with the maximum
+            x[k[len(k) // 2:]] = [np.nan, np.inf, -np.inf, -0.0, 0.0, np.nan][: len(k) - len(k) // 2]
+            if trial == 0:
+                x[0] = np.nan
+            assert O.argmax(x) == R.qw6_cpu_argmax(x, n), (n, trial)
+
+
+def test_argmax_planted_mistake_is_caught():
+    """'>=' instead of '>' (last of the ties) or a reduction that lets a NaN
+    win would fail the special cases above."""
+    def last_tie(x):
+        best = 0
+        for i in range(1, len(x)):
+            if x[i] >= x[best]:
+                best = i
+        return best
+    def nan_wins(x):
+        return int(np.argmax(np.array(x, np.float32)))   # numpy takes the first NaN
+    cases_ = cases.argmax_cases()
+    assert any(last_tie(np.array(x, np.float32)) != want for x, want in cases_)
+    assert any(nan_wins(x) != want for x, want in cases_)
