@@ -1492,6 +1492,82 @@ __global__ __launch_bounds__(256) void k_argmax_final(const float* __restrict__ 
     }
 }
 
+// ---- output head: one streaming pass over a large matrix ------------------------
+// logits[r] = deq(W)[r] . (rmsnorm(x) * norm_w) for every row, plus each
+// wave's running argmax key (part[wave]) for k_argmax_final. The layout of
+// k_matvec (U = K/32 lanes per row, rps = 64/U rows per step), but each wave
+// loads its activations once (the norm fused: a lane's 32 values of the
+// first row group are the whole vector once) and streams its rows through
+// kHeadSlots direct-to-LDS slots, so that many row steps are in flight.
+// Step s of wave w covers row group w + s * (number of waves): neighbouring
+// waves read neighbouring rows. Every wave issues the same loads: steps
+// past the last row group restage group 0 and write nothing, so each wait
+// is a constant; the wave drains its loads before it ends (an LDS-direct
+// load must not land after the workgroup's LDS is released).
+constexpr int kHeadSlots = 4;        // row steps in flight per wave
+constexpr uint32_t kHeadWaves = 4096;   // waves of one launch, at most
+
+template <int F, int KU>
+__global__ __launch_bounds__(kWG) void k_head(const uint8_t* __restrict__ W, uint32_t groups,
+                                              uint32_t rows, uint32_t rb, uint32_t nsteps,
+                                              const float* __restrict__ x,
+                                              const float* __restrict__ norm_w, float eps,
+                                              float* __restrict__ logits,
+                                              uint64_t* __restrict__ part, uint32_t tmask) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    constexpr uint32_t U = KU, rps = 64 / KU, K = 32 * KU;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t unit = lane & (U - 1), blk = unit >> 3, q = lane / U;
+    const int j = (int)(unit & 7);
+    const uint32_t gw = blockIdx.x * 4 + wave, nwv = gridDim.x * 4;
+    const uint32_t soff = tab_bytes(tmask) + wave * kHeadSlots * kSlotBytes;
+    const uint32_t gbytes = rps * rb;   // one row group: 8 GGUF blocks
+    auto src = [&](uint32_t st) -> const uint8_t* {
+        const uint32_t g = gw + st * nwv;
+        return W + (size_t)(g < groups ? g : 0u) * gbytes;
+    };
+    stage_tables(smem, tmask);
+#pragma unroll
+    for (int st = 0; st < kHeadSlots; st++) stage_group(smem + soff + st * kSlotBytes, src(st), gbytes);
+    float xr[1][32], sx[1][4];
+    load_unit_x(F, x, blk, j, xr[0]);
+    if (norm_w) {   // final RMSNorm (qw6.c:2490-2492)
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 32; i++) ss = fmaf(xr[0][i], xr[0][i], ss);
+        ss = group_sum<64>(q == 0 ? ss : 0.f);
+        const float sc = 1.0f / sqrtf(ss / (float)K + eps);
+        float wr[32];
+        load_unit_x(F, norm_w, blk, j, wr);
+#pragma unroll
+        for (int i = 0; i < 32; i++) xr[0][i] = xr[0][i] * sc * wr[i];
+    }
+    unit_x_sums(F, xr[0], sx[0]);
+    if (tmask) {   // the lattice tables (this wave's oldest loads) of every wave
+        wait_vm(0);
+        lds_barrier();
+    }
+    const uint32_t* lds = (const uint32_t*)smem;
+    const uint32_t boff = q * rb + blk * fmt_block_bytes(F);
+    uint64_t best = 0;
+    for (uint32_t st = 0; st < nsteps; st++) {
+        wait_vm(2u * (kHeadSlots - 1));   // step st (the oldest in flight) has landed
+        const uint32_t so = soff + (st % kHeadSlots) * kSlotBytes;
+        float a[1] = {0.f};
+        unit_dot<1>(F, lds, so + boff, j, lds, xr, sx, a);
+        const float v = reduce_scatter_k<1, KU>(a);
+        const uint32_t row = (gw + st * nwv) * rps + q;
+        if (unit == 0 && row < rows) {
+            logits[row] = v;
+            best = max_u64(best, amax_key(v, row));
+        }
+        stage_group(smem + so, src(st + kHeadSlots), gbytes);   // after this slot's reads
+    }
+    wait_vm(0);
+    best = wave_max_u64(best);
+    if (lane == 0) part[gw] = best;
+}
+
 __global__ void k_gather(const float* eo, const float* ew, const float* sh, float sw,
                          float* o, uint32_t dim, uint32_t top_k) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1726,6 +1802,45 @@ int launch_argmax(const float* x, uint32_t n, uint64_t* part, uint32_t* out, hip
     return 0;
 }
 
+// The output head's streaming pass (k_head) and the argmax of its per-wave
+// keys. Needs a GGUF format, cols in {256, 512, 1024, 2048} and rows a
+// multiple of the rows per step; returns 1 when the shape does not fit.
+// part: kHeadWaves words.
+int launch_head(const MatD& W, const float* x, const float* norm_w, float eps, float* logits,
+                uint64_t* part, uint32_t* out, hipStream_t st) {
+    if (W.fmt < 0 || !fast_k(W.cols)) return 1;
+    const uint32_t U = W.cols / 32, rps = 64 / U;
+    if (W.rows % rps) return 1;
+    const uint32_t groups = W.rows / rps;
+    const uint32_t nwv = std::min(kHeadWaves, std::max(4u, (groups + 7) / 8 / 4 * 4));
+    const uint32_t nsteps = (groups + nwv - 1) / nwv;
+    const uint32_t tmask = fmt_table_mask(W.fmt);
+    const size_t lds = tab_bytes(tmask) + 4 * kHeadSlots * kSlotBytes;
+    auto go = [&](auto fc, auto kc) {
+        k_head<decltype(fc)::value, decltype(kc)::value><<<nwv / 4, kWG, lds, st>>>(
+            W.p, groups, W.rows, W.rb, nsteps, x, norm_w, eps, logits, part, tmask);
+    };
+    auto by_k = [&](auto fc) {
+        switch (U) {
+        case 8: go(fc, IC<8>{}); break;
+        case 16: go(fc, IC<16>{}); break;
+        case 32: go(fc, IC<32>{}); break;
+        default: go(fc, IC<64>{}); break;
+        }
+    };
+    switch (W.fmt) {
+    case F_Q4K: by_k(IC<F_Q4K>{}); break;
+    case F_Q5K: by_k(IC<F_Q5K>{}); break;
+    case F_Q6K: by_k(IC<F_Q6K>{}); break;
+    case F_IQ2XXS: by_k(IC<F_IQ2XXS>{}); break;
+    case F_IQ2S: by_k(IC<F_IQ2S>{}); break;
+    default: by_k(IC<F_IQ3S>{}); break;
+    }
+    k_argmax_final<<<1, 256, 0, st>>>(logits, part, nwv, out);
+    CK(hipGetLastError());
+    return 0;
+}
+
 struct DevBuf {
     void* p = nullptr;
     ~DevBuf() {
@@ -1762,7 +1877,7 @@ int alloc_owned(qw6_hip_ctx_t* c, size_t bytes, void** p) {
 int ensure_argmax_ws(qw6_hip_ctx_t* c) {
     if (c->amax_part) return 0;
     void* p;
-    if (alloc_owned(c, (size_t)kArgmaxBlocks * 8, &p)) return -1;
+    if (alloc_owned(c, (size_t)std::max(kArgmaxBlocks, kHeadWaves) * 8, &p)) return -1;
     c->amax_part = (uint64_t*)p;
     return 0;
 }
@@ -2479,6 +2594,10 @@ int qw6_hip_output_greedy(qw6_hip_ctx_t* c, const qw6_hip_matrix_t* w, const flo
     DevGuard g(c->device);
     const hipStream_t st = (hipStream_t)stream;
     if (ensure_argmax_ws(c)) return -1;
+    const uint32_t rb = w->quant == 0 ? w->cols * 4 : (w->cols / 256) * fmt_block_bytes(f);
+    const MatD W = {(const uint8_t*)w->data, w->quant == 0 ? -1 : f, w->rows, w->cols, rb};
+    const int hr = launch_head(W, x, norm_w, eps, logits, c->amax_part, token, st);
+    if (hr <= 0) return hr;   // else: a shape the streaming pass does not take
     const float* xin = x;
     if (norm_w) {   // final RMSNorm (qw6.c:2490-2492)
         if (!c->head_x || c->head_hidden < w->cols) {
@@ -2491,8 +2610,6 @@ int qw6_hip_output_greedy(qw6_hip_ctx_t* c, const qw6_hip_matrix_t* w, const flo
         CK(hipGetLastError());
         xin = c->head_x;
     }
-    const uint32_t rb = w->quant == 0 ? w->cols * 4 : (w->cols / 256) * fmt_block_bytes(f);
-    const MatD W = {(const uint8_t*)w->data, w->quant == 0 ? -1 : f, w->rows, w->cols, rb};
     if (launch_matvec(W, xin, logits, 1, st)) return -1;   // qw6.c:2493
     return launch_argmax(logits, w->rows, c->amax_part, token, st);
 }
