@@ -33,7 +33,9 @@ sample of the same workload on this host, single thread as qw6 runs it.
   mtp_T2        two tokens (MTP draft verification) with the router GEMV, and
                 small batches (3, 4, 8 tokens) through the automatic path;
   prefill_T512_iq2xxs_iq3s  the grouped kernels on an IQ layer (IQ2_XXS
-                gate/up, IQ3_S down, Q4_K / Q6_K shared expert).
+                gate/up, IQ3_S down, Q4_K / Q6_K shared expert);
+  output_head   the greedy next-token head: final RMSNorm, Q6_K [248320 x
+                2048] vocabulary projection and argmax, us/token and HBM GB/s.
 """
 from __future__ import annotations
 
@@ -59,7 +61,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--pool", type=int, default=16)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "q4k", "iq2m", "stack", "prefill"])
+                    choices=["all", "q4k", "iq2m", "stack", "prefill", "head"])
     ap.add_argument("--stack-steps", type=int, default=128)
     ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--no-small-batch", action="store_true",
@@ -266,6 +268,44 @@ def bench_decode(torch, Q, S, ctx, pool, X, out, idx, args, profile=True):
                            "GBps": round(d_b / kus[2] / 1e3, 1)},
         }
         res["profiled_calls"] = calls
+    return res
+
+
+VOCAB = 248320
+
+
+def bench_head(torch, Q, S, ctx, args):
+    """The greedy output head: final RMSNorm, Q6_K [248320 x 2048] vocabulary
+    projection (417 MB streamed per token) and argmax, per token."""
+    q = S.Q_Q6_K
+    rb = S.row_bytes(q, HIDDEN)
+    P = 2   # two resident heads, alternated, so no replay reads the same weights twice in a row
+    ws = []
+    for j in range(P):
+        w = torch.empty(VOCAB * rb, dtype=torch.uint8, device="cuda")
+        Q.synth_blocks(w, q, VOCAB * HIDDEN // 256, 5000 + j, S.stream_id(0, S.K_OUTPUT))
+        ws.append(w)
+    x = torch.empty(P, HIDDEN, dtype=torch.float32, device="cuda")
+    nw = torch.empty(HIDDEN, dtype=torch.float32, device="cuda")
+    for j in range(P):
+        Q.synth_normal(x[j], HIDDEN, 1.0, 5010 + j, S.stream_id(0, S.K_X))
+    Q.synth_normal(nw, HIDDEN, 0.1, 5020, S.stream_id(0, S.K_ONORM), mean=1.0)
+    lg = torch.empty(P, VOCAB, dtype=torch.float32, device="cuda")
+    tok = torch.zeros(P, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+
+    def fwd(sp):
+        for j in range(P):
+            ctx.output_greedy((ws[j].data_ptr(), q, VOCAB, HIDDEN), x[j], lg[j], tok[j:j + 1],
+                              norm_w=nw, stream=sp)
+    sec, _ = graph_time(torch, fwd, 20)
+    us = 1e6 * sec / P
+    nbytes = VOCAB * rb + 2 * HIDDEN * 4 + VOCAB * 4   # weights, x and norm weight, logits
+    res = {"us_per_token": round(us, 2), "bytes": nbytes, "hbm_GBps": round(nbytes / us / 1e3, 1),
+           "hbm_frac": round(nbytes / us / 1e3 / HBM_PEAK_GBPS, 4),
+           "workload": "output head: RMSNorm + Q6_K [248320 x 2048] projection + greedy argmax, "
+                       "one token, two resident heads alternated"}
+    ws.clear()
     return res
 
 
@@ -501,6 +541,10 @@ def main():
         st = bench_stack(torch, Q, S, ctx, args)
         secondary["stack"] = st
         log("stack: %s" % json.dumps(st))
+    if args.workload in ("all", "head"):
+        hd = bench_head(torch, Q, S, ctx, args)
+        secondary["output_head"] = hd
+        log("output head: %s" % json.dumps(hd))
 
     if res_main is None:
         print(json.dumps({"secondary": secondary}), flush=True)
