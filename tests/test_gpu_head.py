@@ -152,3 +152,26 @@ def test_output_greedy_full_vocab(torch_dev, ctx):
                               1, HIDDEN, xn)[0] for r in rows], np.float32)
     assert cases.rel_l2(glog[rows], want) <= TOL
     say("full-vocab token", gtok)
+
+
+@pytest.mark.parametrize("hidden,rows", [(256, 1024), (1024, 777), (1024, 2000), (512, 3001)])
+def test_output_greedy_other_shapes(torch_dev, ctx, hidden, rows):
+    """Rows of 256 / 512 / 1024 columns (8, 4, 2 rows per wave step), and row
+    counts that are not a multiple of a step (those take the plain matvec
+    and the two-pass argmax): logits and token against the oracle."""
+    torch = torch_dev
+    q = S.Q_Q6_K
+    w = S.quant_matrix(41, S.stream_id(1, S.K_OUTPUT), q, rows, hidden)
+    dw = torch.from_numpy(w).cuda()
+    x = S.f32_normal(42, S.stream_id(1, S.K_X), hidden, 1.0)
+    nw = S.f32_normal(43, S.stream_id(1, S.K_ONORM), hidden, 0.1, mean=1.0)
+    dx, dn = torch.from_numpy(x).cuda(), torch.from_numpy(nw).cuda()
+    logits = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ctx.output_greedy((dw.data_ptr(), q, rows, hidden), dx, logits, tok, norm_w=dn, eps=1e-6)
+    torch.cuda.synchronize()
+    glog = logits.cpu().numpy()
+    gtok = int(tok.cpu().numpy().view(np.uint32)[0])
+    olog = O.matvec(q, w, rows, hidden, O.rmsnorm(x, nw, 1e-6))
+    assert cases.rel_l2(glog, olog) <= TOL
+    assert gtok == O.argmax(glog)
