@@ -1241,6 +1241,7 @@ __device__ __forceinline__ void mx_gu_blocks(const MoeArgs& a, const MatD& Gm, c
 
 // Routed + shared gate/up/SiLU: block (matrix pair, 16-row tile), shared
 // expert first (blocks [0, n_sh_wg)); writes the down kernel's operands of mid.
+// Launched with at least kMaxTok waves: wave t routes token t.
 template <int T>
 __global__ __launch_bounds__(512, 4) void k_mx_gate_up(MoeArgs a) {
     TRACE_SCOPE(2);
@@ -2448,7 +2449,9 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
     const uint32_t sb_gu = std::max(sb_of(E->fmt_gu), has_sh ? sb_of(sg.fmt) : 0u);
     const uint32_t sb_dn = std::max(sb_of(E->fmt_dn), has_sh ? sb_of(sd.fmt) : 0u);
     const uint32_t nkb_gu = L->hidden / 256, nkb_dn = L->inter / 256;
-    const uint32_t mx_nw_b = nkb_gu < 8 ? nkb_gu : 8;
+    // k_mx_gate_up: one wave per 256-column block, at least kMaxTok waves
+    // (waves t < T route token t; the epilogue reads 128 threads' sums)
+    const uint32_t mx_nw_b = std::max<uint32_t>(kMaxTok, nkb_gu < 8 ? nkb_gu : 8);
     const uint32_t mx_tab_gu = mx_tab(mgu).bytes, mx_tab_dn = mx_tab(mdn).bytes;
     a.mx_gu_soff = mx_tab_gu;
     a.mx_sb = sb_dn;

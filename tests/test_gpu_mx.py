@@ -144,6 +144,26 @@ def test_mx_other_shape_vs_oracle(torch_dev, ctx, mix):
         L.free()
 
 
+@pytest.mark.parametrize("hidden,mix", [(512, "q4k"), (256, "iq2b"), (512, "iq2a")])
+def test_mx_narrow_hidden_vs_oracle(torch_dev, ctx, hidden, mix):
+    """hidden 256 / 512: one or two 256-column blocks per gate/up row, fewer
+    than the 4 tokens of a launch; the gate/up kernel still runs one routing
+    wave per token. T = 1..4, inter 256, 32 experts."""
+    from qw6_amd.workload import SynthLayer
+    say("mx narrow", hidden, mix)
+    L = SynthLayer(ctx, 69, 0, mix, hidden=hidden, inter=256, n_experts=32)
+    try:
+        router = L.router_host()
+        n = 0
+        for T in (1, 2, 3, 4):
+            xs = np.stack([cases.token_x(690 + T, 2, t, hidden=hidden) for t in range(T)])
+            out, idx = run(torch_dev, ctx, L, xs, 3)
+            n += check_tokens(L, xs, out, idx, router=router)
+        assert n >= 8
+    finally:
+        L.free()
+
+
 def test_mx_no_shared_given_logits_residual(torch_dev, ctx):
     """No shared expert, router logits given (Zipf), residual added: the router
     kernel then only writes the operands."""
