@@ -85,8 +85,18 @@ def ref():
                                     C.c_void_p, C.c_int, C.c_void_p, C.c_int,
                                     C.c_void_p, C.c_int, _f32p]
         R.ref_moe_layer_logits.argtypes = R.ref_moe_layer.argtypes
+        R.ref_moe_layer_sr.argtypes = R.ref_moe_layer.argtypes + [_f32p]
         R.qw6_cpu_argmax.restype = C.c_int
         R.qw6_cpu_argmax.argtypes = [_f32p, C.c_int]
+        u32, u64, i64 = C.POINTER(C.c_uint32), C.POINTER(C.c_uint64), C.POINTER(C.c_int64)
+        R.ref_gguf_header.argtypes = [C.c_char_p, u32, u32, u32, u32, u64, u64]
+        R.ref_gguf_validate.argtypes = [C.c_char_p]
+        R.ref_gguf_tensor.argtypes = [C.c_char_p, C.c_uint32, C.c_char_p, u32, i64,
+                                      C.POINTER(C.c_int32), u64, u64]
+        R.ref_gguf_pack.argtypes = [C.c_char_p, C.c_uint32, C.POINTER(C.c_int32), u32, u32,
+                                    u64, u64]
+        R.ref_gguf_kv.argtypes = [C.c_char_p, C.c_char_p, C.POINTER(C.c_int32), i64,
+                                  C.POINTER(C.c_double), C.c_char_p, C.c_size_t]
         _ref = R
     return _ref
 
@@ -280,8 +290,69 @@ def ref_moe_layer(layer: Layer, x: np.ndarray, logits: np.ndarray | None = None,
     else:
         fn, first = ref().ref_moe_layer_logits, np.ascontiguousarray(logits, np.float32)
     route = want_route or logits is not None
+    extra = []
+    if layer.shared_router is not None:
+        if logits is not None:
+            raise ValueError("the reference's given-logits composition has no shared gate")
+        fn = ref().ref_moe_layer_sr
+        extra = [np.ascontiguousarray(layer.shared_router, np.float32)]
     rc = fn(out, idx.ctypes.data if route else None, w.ctypes.data if route else None, first,
-            ptrs[0], qs[0], ptrs[1], qs[1], ptrs[2], qs[2], *sa, x)
+            ptrs[0], qs[0], ptrs[1], qs[1], ptrs[2], qs[2], *sa, x, *extra)
     if rc != 0:
         raise ValueError("reference moe layer failed")
     return out, idx, w
+
+
+# ---- qw6's GGUF reader (reference build) -------------------------------------
+
+def ref_gguf_header(path):
+    """qw6_gguf_parse's header facts, or None where it fails."""
+    v, nt, nkv, al = (C.c_uint32() for _ in range(4))
+    do, fs = C.c_uint64(), C.c_uint64()
+    if ref().ref_gguf_header(str(path).encode(), C.byref(v), C.byref(nt), C.byref(nkv),
+                             C.byref(al), C.byref(do), C.byref(fs)) != 0:
+        return None
+    return {"version": v.value, "n_tensors": nt.value, "n_kv": nkv.value,
+            "alignment": al.value, "data_offset": do.value, "file_size": fs.value}
+
+
+def ref_gguf_valid(path) -> bool:
+    """qw6_gguf_parse + gguf_validate_tensor_ranges both succeed."""
+    return ref().ref_gguf_validate(str(path).encode()) == 0
+
+
+def ref_gguf_tensor(path, i):
+    name = C.create_string_buffer(128)
+    nd, t = C.c_uint32(), C.c_int32()
+    dims = (C.c_int64 * 4)()
+    off, span = C.c_uint64(), C.c_uint64()
+    if ref().ref_gguf_tensor(str(path).encode(), i, name, C.byref(nd), dims, C.byref(t),
+                             C.byref(off), C.byref(span)) != 0:
+        return None
+    return {"name": name.value.decode(errors="replace"), "dims": list(dims[:nd.value]),
+            "type": t.value, "offset": off.value, "span": span.value}
+
+
+def ref_gguf_pack(path, i):
+    """bind_expert_pack on tensor i: quant, rows, cols, per-expert file
+    offsets and sizes (256 experts), or None where it fails."""
+    q = C.c_int32()
+    r, c = C.c_uint32(), C.c_uint32()
+    offs = (C.c_uint64 * 256)()
+    sizes = (C.c_uint64 * 256)()
+    if ref().ref_gguf_pack(str(path).encode(), i, C.byref(q), C.byref(r), C.byref(c), offs,
+                           sizes) != 0:
+        return None
+    return {"quant": q.value, "rows": r.value, "cols": c.value, "offsets": list(offs),
+            "sizes": list(sizes)}
+
+
+def ref_gguf_kv(path, key):
+    """(type, integer value, float value, string) of qw6_gguf_find_kv, or None."""
+    t = C.c_int32()
+    iv, fv = C.c_int64(), C.c_double()
+    sb = C.create_string_buffer(1 << 16)
+    if ref().ref_gguf_kv(str(path).encode(), key.encode(), C.byref(t), C.byref(iv), C.byref(fv),
+                         sb, 1 << 16) != 0:
+        return None
+    return t.value, iv.value, fv.value, sb.value.decode(errors="replace")

@@ -60,15 +60,17 @@ def main():
     xr = S.f32_normal(7, S.stream_id(0, S.K_X, 99), 2048, 1.0)
     g["rms_out"] = O.ref_rmsnorm(xr, cases.norm_w(7, 0))
     # single layers
-    for mix, seed, shared in (("q4k", 11, True), ("q4k", 12, True), ("q4k", 13, False),
-                              ("iq2m", 21, True), ("iq2m", 22, True)):
-        L = cases.HostLayer(seed, 0, mix, shared=shared)
+    for mix, seed, shared, sr in (("q4k", 11, True, False), ("q4k", 12, True, False),
+                                  ("q4k", 13, False, False), ("iq2m", 21, True, False),
+                                  ("iq2m", 22, True, False), ("q4k", 14, True, True),
+                                  ("iq2m", 23, True, True)):
+        L = cases.HostLayer(seed, 0, mix, shared=shared, shared_router=sr)
         x = cases.token_x(seed, 0)
         lg = cases.router_logits(L, x)
         idx, _ = O.moe_route(lg, 8)
         ol = L.oracle_layer(set(int(i) for i in idx))
         out, ridx, rw = O.ref_moe_layer(ol, x)
-        key = "layer_%s_s%d%s" % (mix, seed, "" if shared else "_noshared")
+        key = "layer_%s_s%d%s%s" % (mix, seed, "" if shared else "_noshared", "_sr" if sr else "")
         g[key + "_out"], g[key + "_idx"], g[key + "_w"] = out, ridx, rw
     # stack: 3 layers x 2 steps, h <- h + MoE_l(RMSNorm(h, w_l))  (qw6.c:2475-2484)
     seed = 41

@@ -281,12 +281,15 @@ def test_silu_gather_kat():
     assert np.abs(O.moe_gather(eo, wts, sh, 0.25) - want).max() < 2e-5
 
 
-@pytest.mark.parametrize("key", ["q4k_s11", "q4k_s12", "q4k_s13_noshared", "iq2m_s21", "iq2m_s22"])
+@pytest.mark.parametrize("key", ["q4k_s11", "q4k_s12", "q4k_s13_noshared", "iq2m_s21", "iq2m_s22",
+                                 "q4k_s14_sr", "iq2m_s23_sr"])
 def test_layer_golden(key):
+    """One layer, bit-exact against qw6_apply_layer_moe's outputs; the _sr
+    cases weight the shared expert by sigmoid(shared_router . x)."""
     mix, rest = key.split("_", 1)
     seed = int(rest.split("_")[0][1:])
     shared = "noshared" not in rest
-    L = cases.HostLayer(seed, 0, mix, shared=shared)
+    L = cases.HostLayer(seed, 0, mix, shared=shared, shared_router=rest.endswith("_sr"))
     out, idx, w = cases.oracle_layer_out(L, cases.token_x(seed, 0))
     gk = "layer_" + key
     assert np.array_equal(idx, G[gk + "_idx"])
