@@ -38,6 +38,7 @@
 
 #include "../../include/qw6_hip.h"
 #include "qw6_dev.h"
+#include "qw6_host.h"
 #include "qw6_moe.h"
 #include "qw6_tile.h"
 
@@ -1673,6 +1674,8 @@ struct qw6_hip_ctx_s {
     float* head_x;
     uint32_t head_hidden;
 };
+
+int qw6::ctx_device(const qw6_hip_ctx_t* c) { return c->device; }
 
 struct qw6_hip_experts_s {
     qw6_hip_ctx_t* ctx;

@@ -1,5 +1,6 @@
-"""The C ABI: the library loads, exports every function include/qw6_hip.h
-declares, and the host layer rejects bad arguments before any device work."""
+"""The C ABI: the library loads, exports every function include/*.h
+declares (qw6_hip.h, qw6_gguf.h), and the host layer rejects bad arguments
+before any device work."""
 import ctypes as C
 import re
 from pathlib import Path
@@ -9,11 +10,11 @@ import pytest
 
 import qw6_amd as Q
 
-HEADER = Path(__file__).resolve().parents[1] / "include" / "qw6_hip.h"
+HEADERS = sorted((Path(__file__).resolve().parents[1] / "include").glob("*.h"))
 
 
 def declared_functions():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = "".join(re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S) for h in HEADERS)
     return sorted(set(re.findall(r"\b(qw6_hip_\w+)\s*\(", text)))
 
 
