@@ -61,7 +61,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--pool", type=int, default=16)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "q4k", "iq2m", "stack", "prefill", "head"])
+                    choices=["all", "q4k", "iq2m", "stack", "prefill", "head", "floor"])
     ap.add_argument("--stack-steps", type=int, default=128)
     ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--no-small-batch", action="store_true",
@@ -269,6 +269,20 @@ def bench_decode(torch, Q, S, ctx, pool, X, out, idx, args, profile=True):
         }
         res["profiled_calls"] = calls
     return res
+
+
+def bench_floor(torch, Q, ctx):
+    """The cost of one dependent kernel in a replayed graph: 24 argmax calls
+    over 1024 floats (a one-block partial pass and a one-block final pass,
+    each one memory round trip) captured back to back, so 48 tiny kernels
+    each wait for the one before. A decode layer is three dependent kernels."""
+    x = torch.randn(1024, dtype=torch.float32, device="cuda")
+    out = torch.zeros(1, dtype=torch.int32, device="cuda")
+    n = 24
+    sec, _ = graph_time(torch, lambda s: [ctx.argmax(x, 1024, out, s) for _ in range(n)], 50)
+    per_kernel = 1e6 * sec / (2 * n)
+    return {"us_per_dependent_kernel": round(per_kernel, 3),
+            "three_kernel_chain_us": round(3 * per_kernel, 3)}
 
 
 VOCAB = 248320
@@ -545,6 +559,10 @@ def main():
         hd = bench_head(torch, Q, S, ctx, args)
         secondary["output_head"] = hd
         log("output head: %s" % json.dumps(hd))
+    if args.workload in ("all", "floor"):
+        fl = bench_floor(torch, Q, ctx)
+        secondary["kernel_floor"] = fl
+        log("dependent-kernel floor: %s" % json.dumps(fl))
 
     if res_main is None:
         print(json.dumps({"secondary": secondary}), flush=True)
