@@ -247,21 +247,27 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
             for (int j = 0; j < 4; j++) acc[r][j] = fmaf(-ts[r].dmin, v[j], acc[r][j]);
         }
     }
+    // sub-blocks 2p, 2p + 1: one row tile's codes at a time (8 VGPRs live
+    // instead of 8 RT), against the A operands of the two sub-blocks
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-        uint4 b[RT][2];
-#pragma unroll
-        for (int r = 0; r < RT; r++) tile_codes<F>(S.raw, R[r], q, p, b[r][0], b[r][1]);
+        uint4 ah[2], al[2];
 #pragma unroll
         for (int t = 0; t < 2; t++) {
-            const int sb = 2 * p + t;
-            const uint4 ah = S.a[0][sb][lane], al = S.a[1][sb][lane];
+            ah[t] = S.a[0][2 * p + t][lane];
+            al[t] = S.a[1][2 * p + t][lane];
+        }
 #pragma unroll
-            for (int r = 0; r < RT; r++) {
-                f32x4 c = mfma(ah, b[r][t], f32x4{0.f, 0.f, 0.f, 0.f});
-                c = mfma(al, b[r][t], c);
+        for (int r = 0; r < RT; r++) {
+            uint4 b[2];
+            tile_codes<F>(S.raw, R[r], q, p, b[0], b[1]);
 #pragma unroll
-                for (int j = 0; j < 4; j++) acc[r][j] = fmaf(ts[r].dsc[sb], c[j], acc[r][j]);
+            for (int t = 0; t < 2; t++) {
+                f32x4 c = mfma(ah[t], b[t], f32x4{0.f, 0.f, 0.f, 0.f});
+                c = mfma(al[t], b[t], c);
+                const float dsc = tile_dsc<F>(ts[r], 2 * p + t);
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[r][j] = fmaf(dsc, c[j], acc[r][j]);
             }
         }
     }
@@ -273,19 +279,32 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
 // matrix, whose size -- a multiple of 256 rows of 16-byte-aligned blocks or of
 // 420-byte Q6_K rows -- is a multiple of 16), its four A operand pieces and
 // its part of the 3-part sums.
-template <int F, uint32_t NR>
-__device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NR],
-                                           const uint32_t (&piece)[NR], const uint16_t* arow,
-                                           const uint16_t* srow, uint32_t sb0, uint32_t q,
-                                           uint32_t kb, u32x4 (&rawv)[NR], u32x4 (&av)[4],
-                                           u32x4& sxv) {
+// Formats whose 256-column blocks are 16-byte aligned (Q4_K, Q5_K) address a
+// piece as a 32-bit offset from its matrix, the matrix (gate or up) chosen by
+// bit i of sel; the others keep a row pointer and piece index per load
+// (their pieces depend on the block's alignment).
+template <int F>
+__host__ __device__ constexpr bool gemm_aligned() { return F == F_Q4K || F == F_Q5K; }
+
+template <int F, uint32_t NR, uint32_t NP>
+__device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NP],
+                                           const uint32_t (&piece)[NR], const uint8_t* m0,
+                                           const uint8_t* m1, uint32_t sel,
+                                           const uint16_t* arow, const uint16_t* srow,
+                                           uint32_t sb0, uint32_t q, uint32_t kb,
+                                           u32x4 (&rawv)[NR], u32x4 (&av)[4], u32x4& sxv) {
     constexpr uint32_t bb = fmt_block_bytes(F);
 #pragma unroll
     for (uint32_t i = 0; i < NR; i++) {
-        const uint8_t* p = rowp[i] + (size_t)kb * bb;
-        const uint32_t off = (uint32_t)((uintptr_t)p & 15u);
-        const uint32_t ch = 16 * piece[i] < off + bb ? piece[i] : 0u;
-        rawv[i] = *(const u32x4*)(p - off + 16 * ch);
+        if constexpr (gemm_aligned<F>()) {   // piece[i]: byte offset of the piece at block 0
+            const uint8_t* base = (sel >> i) & 1u ? m1 : m0;
+            rawv[i] = *(const u32x4*)(base + piece[i] + kb * bb);
+        } else {
+            const uint8_t* p = rowp[i] + (size_t)kb * bb;
+            const uint32_t off = (uint32_t)((uintptr_t)p & 15u);
+            const uint32_t ch = 16 * piece[i] < off + bb ? piece[i] : 0u;
+            rawv[i] = *(const u32x4*)(p - off + 16 * ch);
+        }
     }
 #pragma unroll
     for (uint32_t i = 0; i < 4; i++) av[i] = *(const u32x4*)(arow + kb * 256 + 32 * (sb0 + i) + 8 * q);
@@ -301,7 +320,13 @@ __device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NR],
 // sel: the tiles of the routed experts (0), of the shared expert (1), or both
 // (2); the shared expert's tiles follow the routed ones in the tile list.
 template <int MODE, int F>
-__global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs ws, uint32_t sel) {
+__host__ __device__ constexpr int gemm_min_blocks() {   // workgroups per CU
+    return F == F_Q4K ? 3 : 2;   // Q4_K: 52 KB of LDS each, three fit in 160 KB
+}
+
+template <int MODE, int F>
+__global__ __launch_bounds__(kPWG, (gemm_min_blocks<MODE, F>())) void k_pre_gemm(PrefillLayer L, PrefillWs ws,
+                                                                               uint32_t sel) {
     constexpr int RT = gemm_rt<MODE, F>();
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     GemmLds& S = *(GemmLds*)smem;
@@ -373,21 +398,31 @@ __global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs 
         arow = (hl ? ws.mid_l : ws.mid_h) + (size_t)(ent0 + sm) * L.inter;
         srow = ws.ms3 + (size_t)(ent0 + sm) * (L.inter / 256) * 24;
     }
-    const uint8_t* rowp[NR];   // this thread's raw pieces: row block start, piece
+    constexpr bool kAl = gemm_aligned<F>();
+    const uint8_t* rowp[kAl ? 1 : NR];   // this thread's raw pieces (see load_block)
     uint32_t piece[NR];
+    uint32_t psel = 0;
 #pragma unroll
     for (uint32_t i = 0; i < NR; i++) {
         const uint32_t c = i * kPWG + tid;    // chunk: row c / NCH, 16-B piece c % NCH
-        rowp[i] = row_ptr(c / NCH);
-        piece[i] = c % NCH;
+        if constexpr (kAl) {
+            const uint32_t rr = c / NCH;
+            const bool up = MODE == 0 && rr >= ROWS / 2;
+            piece[i] = (r0 + rr - (up ? ROWS / 2 : 0u)) * rb + 16 * (c % NCH);
+            psel |= (up ? 1u : 0u) << i;
+        } else {
+            rowp[i] = row_ptr(c / NCH);
+            piece[i] = c % NCH;
+        }
     }
+    if constexpr (kAl) rowp[0] = nullptr;
     u32x4 rawv[NR], av[4], sxv;
     uint8_t* tab = (uint8_t*)S.raw + (size_t)NR * kPWG * 16;   // IQ lattice tables
     if constexpr (is_iq(F)) stage_iq_tables<F>(tab, g_tabs_pre, kPWG);   // visible after the loop's first barrier
     f32x4 acc[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
-    load_block<F, NR>(rowp, piece, arow, srow, sb0, q, 0, rawv, av, sxv);
+    load_block<F, NR>(rowp, piece, m0, m1, psel, arow, srow, sb0, q, 0, rawv, av, sxv);
     for (uint32_t kb = 0; kb < nblk; kb++) {
         __syncthreads();   // every wave is done with block kb - 1's LDS data
 #pragma unroll
@@ -395,12 +430,13 @@ __global__ __launch_bounds__(kPWG, 2) void k_pre_gemm(PrefillLayer L, PrefillWs 
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) *(u32x4*)&S.a[hl][sb0 + i][lane] = av[i];
         const uint4 sxa = q < 3 ? u4(sxv.x, sxv.y, sxv.z, sxv.w) : u4(0, 0, 0, 0);
-        if (kb + 1 < nblk) load_block<F, NR>(rowp, piece, arow, srow, sb0, q, kb + 1, rawv, av, sxv);
+        if (kb + 1 < nblk) load_block<F, NR>(rowp, piece, m0, m1, psel, arow, srow, sb0, q, kb + 1, rawv, av, sxv);
         __syncthreads();   // block kb's bytes are in LDS
         uint32_t R[RT];
 #pragma unroll
         for (int r = 0; r < RT; r++)
-            R[r] = rrow[r] * NCH * 16 + (uint32_t)((uintptr_t)(row_ptr(rrow[r]) + (size_t)kb * bb) & 15u);
+            R[r] = rrow[r] * NCH * 16 +
+                   (kAl ? 0u : (uint32_t)((uintptr_t)(row_ptr(rrow[r]) + (size_t)kb * bb) & 15u));
         gemm_block<F, RT>(S, tab, R, lane, sxa, acc);
     }
 

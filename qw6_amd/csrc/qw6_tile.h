@@ -85,6 +85,7 @@ __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, const f32x
 struct TileScales {
     float dsc[8];
     float d, dmin;
+    uint32_t scw[2];   // the 8 sub-block scales as bytes (Q6_K: signed)
 };
 
 // The sub-block scales (and minimums) of row n as B operands over k =
@@ -118,12 +119,15 @@ __device__ __forceinline__ void tile_scales(const uint32_t* s, uint32_t R, TileS
             mn[j] = ub(mn_lo, j);
             mn[j + 4] = ub(mn_hi, j);
         }
+        ts.scw[0] = sc_lo;
+        ts.scw[1] = sc_hi;
     } else {   // Q6_K: sub-block 4h + k uses scale 8h + 2k (qw6.c:1550-1578)
         ts.d = h2f(lds16(s, R + 208));
         ts.dmin = 0.f;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const uint32_t w0 = lds32(s, R + 192 + 8 * h), w1 = lds32(s, R + 196 + 8 * h);
+            ts.scw[h] = __builtin_amdgcn_perm(w1, w0, 0x06040200u);   // bytes 0, 2 of w0, w1
             sc[4 * h + 0] = (float)(int8_t)(w0 & 0xffu);
             sc[4 * h + 1] = (float)(int8_t)((w0 >> 16) & 0xffu);
             sc[4 * h + 2] = (float)(int8_t)(w1 & 0xffu);
@@ -138,6 +142,15 @@ __device__ __forceinline__ void tile_scales(const uint32_t* s, uint32_t R, TileS
     bmin = F != F_Q6K ? u4(pk_bf16(mn[0], mn[1]), pk_bf16(mn[2], mn[3]), pk_bf16(mn[4], mn[5]),
                            pk_bf16(mn[6], mn[7]))
                       : u4(0, 0, 0, 0);
+}
+
+// d * scale of sub-block sb from the packed bytes (the same value as
+// ts.dsc[sb], computed where it is used instead of held in 8 registers).
+template <int F>
+__device__ __forceinline__ float tile_dsc(const TileScales& ts, int sb) {
+    const uint32_t w = ts.scw[sb >> 2], sh = 8u * (uint32_t)(sb & 3);
+    const float sc = F == F_Q6K ? (float)(int8_t)((w >> sh) & 0xffu) : (float)((w >> sh) & 0xffu);
+    return ts.d * sc;
 }
 
 // Codes of sub-blocks 2p and 2p + 1 of row n (this lane's 8 columns of each).
