@@ -61,7 +61,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--pool", type=int, default=16)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "q4k", "iq2m", "stack", "prefill", "head", "floor"])
+                    choices=["all", "q4k", "iq2m", "stack", "prefill", "head", "floor", "gguf"])
     ap.add_argument("--stack-steps", type=int, default=128)
     ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--no-small-batch", action="store_true",
@@ -269,6 +269,47 @@ def bench_decode(torch, Q, S, ctx, pool, X, out, idx, args, profile=True):
         }
         res["profiled_calls"] = calls
     return res
+
+
+def bench_gguf(torch, Q, S, ctx, pool, X, out, idx):
+    """A cfg1-shaped layer written as a GGUF file, made resident by the
+    library's loader (qw6_hip_gguf_moe_layer: parse, bind, stream through
+    pinned staging), then run: load GB/s (file in the page cache) and the
+    loaded layer's decode us/layer beside the synthetic layer's."""
+    import tempfile
+    import numpy as np
+    from qw6_amd import gguf as G
+    L = pool[0]
+    packs = []
+    for k in range(3):
+        q = L.quants[0][k]
+        packs.append((q, [L.expert_host(e)[k][0] for e in range(L.n_experts)]))
+    ts = G.moe_layer_tensors(0, L.hidden, L.inter, L.router_host(), packs, shared=L.shared_host())
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "layer.gguf")
+        G.write_gguf(path, [("general.architecture", G.T_STR, "qwen35moe")], ts)
+        size = os.path.getsize(path)
+        with G.GgufFile(path) as f:
+            t0 = time.perf_counter()
+            desc, E = f.moe_layer(ctx, 0)
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - t0
+    try:
+        o_file = torch.zeros_like(out[0])
+        i_file = torch.zeros_like(idx[0])
+        ctx.moe_forward(desc, X[0], o_file, n_tok=1, idx=i_file)
+        ctx.moe_forward(L.desc, X[0], out[0], n_tok=1, idx=idx[0])
+        torch.cuda.synchronize()
+        same = bool(torch.equal(o_file, out[0]) and torch.equal(i_file, idx[0]))
+        sec, _ = graph_time(torch, lambda s: [ctx.moe_forward(desc, X[0], o_file, n_tok=1, idx=i_file,
+                                                               stream=s) for _ in range(16)], 20)
+    finally:
+        E.free()
+    return {"file_MB": round(size / 1e6, 1), "load_s": round(dt, 4),
+            "load_GBps": round(size / dt / 1e9, 2), "decode_us_per_layer": round(1e6 * sec / 16, 3),
+            "bit_identical_to_synthetic_layer": same,
+            "workload": "one cfg1 layer (256 Q4_K/Q6_K experts + shared) written to a GGUF file "
+                        "and loaded; the same layer replayed 16 times per graph (MALL-resident)"}
 
 
 def bench_floor(torch, Q, ctx):
@@ -501,7 +542,7 @@ def main():
     secondary = {}
     res_main = None
     pool = []
-    if args.workload in ("all", "q4k", "iq2m", "prefill"):
+    if args.workload in ("all", "q4k", "iq2m", "prefill", "gguf"):
         log("building %d synthetic layers (%s)" % (P, mix))
         pool = [SynthLayer(ctx, 1000 + i, i, mix) for i in range(P)]
         X = torch.empty(P, HIDDEN, dtype=torch.float32, device="cuda")
@@ -521,6 +562,10 @@ def main():
             secondary["mtp_T2"] = t2
             log("T=2: %s" % json.dumps(t2))
 
+    if args.workload in ("all", "gguf") and pool:
+        gg = bench_gguf(torch, Q, S, ctx, pool, X, out, idx)
+        secondary["gguf_layer"] = gg
+        log("gguf layer: %s" % json.dumps(gg))
     cpu = None
     if res_main is not None and not args.no_cpu:
         cpu = cpu_baseline(pool[0], X.cpu().numpy(), args.cpu_seconds)
