@@ -219,6 +219,35 @@ def test_layer_vs_golden(torch_dev, ctx, layers, key):
     assert cases.rel_l2(out[0], G[gk + "_out"]) <= TOL
 
 
+@pytest.mark.parametrize("mix,seed", [("q4k", 14), ("iq2m", 23)])
+def test_shared_gate_layer_vs_golden(torch_dev, ctx, mix, seed):
+    """The shared expert weighted by sigmoid(shared_router . x) (qw6.c:
+    2267-2272): device layer, device-generated gate vector, against qw6's own
+    qw6_apply_layer_moe with the same shared router."""
+    torch = torch_dev
+    from qw6_amd.workload import SynthLayer
+    say("shared gate layer", mix, seed)
+    L = SynthLayer(ctx, seed, 0, mix)
+    try:
+        sr = torch.empty(L.hidden, dtype=torch.float32, device="cuda")
+        Q.synth_normal(sr, L.hidden, 0.02, seed, S.stream_id(0, S.K_SROUTER))
+        host = cases.HostLayer(seed, 0, mix, shared_router=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(sr.cpu().numpy(), host.shared_router)
+        d = Q.MoeLayer.from_buffer_copy(L.desc)
+        d.shared_router = sr.data_ptr()
+        x = torch.from_numpy(cases.token_x(seed, 0)[None].copy()).cuda()
+        out = torch.zeros_like(x)
+        idx = torch.zeros(1, L.top_k, dtype=torch.int32, device="cuda")
+        ctx.moe_forward(d, x, out, n_tok=1, idx=idx)
+        torch.cuda.synchronize()
+        gk = "layer_%s_s%d_sr" % (mix, seed)
+        assert np.array_equal(idx.cpu().numpy()[0], G[gk + "_idx"])
+        assert cases.rel_l2(out.cpu().numpy()[0], G[gk + "_out"]) <= TOL
+    finally:
+        L.free()
+
+
 @pytest.mark.parametrize("key", [("q4k", 11), ("iq2m", 21)])
 def test_layer_many_tokens_vs_oracle(torch_dev, ctx, layers, key):
     """Random tokens (T = 1, 2 as in MTP verification, 3) against the oracle;
