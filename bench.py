@@ -47,6 +47,10 @@ import os
 import sys
 import time
 
+# The oracle's OpenMP threads sleep between parallel regions instead of
+# spinning (the CPU-baseline leg alternates them with host work).
+os.environ.setdefault("OMP_WAIT_POLICY", "PASSIVE")
+
 HERE = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
@@ -213,9 +217,27 @@ def cpu_baseline(L, xs_host, budget_s):
         times.append(time.perf_counter() - t0)
         i += 1
     us = 1e6 * float(np.median(times))
+    # the same steps through the oracle port's row-parallel OpenMP build on
+    # the host's cores (per-row sums unchanged, so the outputs are bitwise
+    # the single-thread ones)
+    nt = max(1, min(8, len(os.sched_getaffinity(0)) // 2))   # leave cores to the rest
+    mt = []
+    for j in range(min(len(times), 50)):
+        x = xs_host[j % len(xs_host)]
+        lg = O.matvec(0, router, N_EXPERTS, HIDDEN, x, nthreads=nt)
+        idx, _ = O.moe_route(lg, TOP_K)
+        sel = set(int(e) for e in idx)
+        ex = [L.expert_host(e) if e in sel else None for e in range(N_EXPERTS)]
+        layer = O.Layer(HIDDEN, INTER, N_EXPERTS, TOP_K, router, ex, shared)
+        t0 = time.perf_counter()
+        O.moe_layer(layer, x, nthreads=nt)
+        mt.append(time.perf_counter() - t0)
     return {"value": round(us, 1), "unit": "us/layer", "cores": 1, "kind": kind,
             "sample": "%d single-token MoE layer steps (median), one pool layer, "
-                      "selected experts copied to host; single thread as qw6" % len(times)}
+                      "selected experts copied to host; single thread as qw6" % len(times),
+            "multicore": {"value": round(1e6 * float(np.median(mt)), 1), "cores": nt, "kind": "port",
+                          "sample": "%d of the same steps, the oracle's OpenMP row-parallel "
+                                    "build" % len(mt)}}
 
 
 # ---- workloads --------------------------------------------------------------------
