@@ -1,7 +1,8 @@
 """ctypes bindings for the oracle (test infrastructure only).
 
-The oracle is the CPU checker for the HIP library: tests, the smoke check and
-the CPU-baseline leg of bench.py call it to compute expected results. The
+The oracle is the CPU reference the HIP library is compared against: tests,
+the smoke check and the CPU-baseline leg of bench.py call it to compute
+expected results. The
 product never imports this package.
 
 ``lib()`` loads the repository's C restatement of qw6's CPU path

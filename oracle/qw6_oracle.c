@@ -1,7 +1,7 @@
 /* qw6_oracle.c -- CPU restatement of qw6's MoE FFN path (test infrastructure).
  *
- * The checker for the HIP library: only tests, the smoke check and the
- * CPU-baseline leg of the benchmark use it. See qw6_oracle.h.
+ * The expected results for the HIP library: only tests, the smoke check and
+ * the CPU-baseline leg of the benchmark use it. See qw6_oracle.h.
  *
  * Blocks are read through byte offsets of the GGUF layouts (little-endian,
  * 256 weights per super-block); the fp32 expressions keep the reference's

@@ -1,6 +1,6 @@
 /* qw6_oracle.h -- CPU restatement of qw6's routed-expert MoE FFN path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker: the parity tests,
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle: the parity tests,
  * the smoke check and the CPU-baseline leg of bench.py call it to compute the
  * expected result. Nothing in the product links it, and nothing here runs on
  * the GPU.

@@ -96,7 +96,7 @@ class SynthLayer:
             return 0
         return sum(S.row_bytes(m[1], m[3]) * m[2] for m in self.shared)
 
-    # ---- host copies (for the CPU checker and the CPU baseline) ---------------------
+    # ---- host copies (for the oracle and the CPU baseline) --------------------------
     def expert_host(self, e: int):
         out = []
         shapes = ((self.inter, self.hidden), (self.inter, self.hidden), (self.hidden, self.inter))
