@@ -212,6 +212,13 @@ int qw6_hip_synth_blocks(void *dst, int32_t quant, uint64_t nblocks,
 int qw6_hip_synth_normal(float *dst, uint64_t n, float mean, float std,
                          uint64_t seed, uint64_t stream_id, void *stream);
 
+/* Device self-test: known-answer inputs (unit-scale K-quant blocks with
+ * patterned codes, zero-index IQ blocks, a dense F32 matrix, SiLU*up, a tied
+ * routing case, the weighted gather) through the host operations above,
+ * checked against closed forms; one line per case on stderr. 0 when every
+ * case passes. Replaces qw6_vk_selftest (qw6_vk.h:9, qw6_vk.c:1514-2133). */
+int qw6_hip_selftest(void);
+
 /* Last error message of the calling thread ("" if none). */
 const char *qw6_hip_last_error(void);
 

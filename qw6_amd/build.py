@@ -15,7 +15,7 @@ from pathlib import Path
 PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 LIB = PKG / "libqw6_hip.so"
-SOURCES = ["qw6_hip.hip", "qw6_prefill.hip", "qw6_gguf.cpp"]
+SOURCES = ["qw6_hip.hip", "qw6_prefill.hip", "qw6_gguf.cpp", "qw6_selftest.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",

@@ -219,6 +219,11 @@ def test_layer_vs_golden(torch_dev, ctx, layers, key):
     assert cases.rel_l2(out[0], G[gk + "_out"]) <= TOL
 
 
+def test_selftest_passes(torch_dev):
+    """qw6_hip_selftest: every known-answer case within its tolerance."""
+    assert Q.lib().qw6_hip_selftest() == 0
+
+
 @pytest.mark.parametrize("mix,seed", [("q4k", 14), ("iq2m", 23)])
 def test_shared_gate_layer_vs_golden(torch_dev, ctx, mix, seed):
     """The shared expert weighted by sigmoid(shared_router . x) (qw6.c:
