@@ -171,16 +171,23 @@ def algorithmic_bytes(pool, sel, hidden=HIDDEN, inter=INTER):
     return r_b, gu_b, d_b, step_b
 
 
-def graph_time(torch, fn, reps):
-    """Seconds per replay of fn() captured as one HIP graph."""
+def capture_graph(torch, fn):
+    """fn(stream) captured as one HIP graph on a side stream (after one eager
+    call that makes first-use allocations); returns (graph, stream)."""
     g = torch.cuda.CUDAGraph()
     s2 = torch.cuda.Stream()
     with torch.cuda.stream(s2):
-        fn(s2.cuda_stream)                       # warm (first-use allocations)
+        fn(s2.cuda_stream)
         torch.cuda.synchronize()
         with torch.cuda.graph(g, stream=s2):
             fn(s2.cuda_stream)
     torch.cuda.synchronize()
+    return g, s2
+
+
+def graph_time(torch, fn, reps):
+    """Seconds per replay of fn() captured as one HIP graph."""
+    g, _ = capture_graph(torch, fn)
     for _ in range(2):
         g.replay()
     torch.cuda.synchronize()
@@ -189,6 +196,39 @@ def graph_time(torch, fn, reps):
         g.replay()
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) / reps, g
+
+
+def graph_replay_times(torch, fn, reps):
+    """Seconds of each of `reps` back-to-back replays of fn() captured as one
+    HIP graph, each bracketed by timing events on the replay stream."""
+    g, s2 = capture_graph(torch, fn)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(reps)]
+    with torch.cuda.stream(s2):
+        for _ in range(2):
+            g.replay()
+        torch.cuda.synchronize()
+        for e0, e1 in evs:
+            e0.record()
+            g.replay()
+            e1.record()
+    torch.cuda.synchronize()
+    return [1e-3 * e0.elapsed_time(e1) for e0, e1 in evs]
+
+
+def host_cpu():
+    """Host CPU model (the lscpu 'Model name' line) and logical CPU count."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"model": model, "nproc": os.cpu_count(),
+            "affinity": len(os.sched_getaffinity(0))}
 
 
 def cpu_baseline(L, xs_host, budget_s):
@@ -233,16 +273,19 @@ def cpu_baseline(L, xs_host, budget_s):
         O.moe_layer(layer, x, nthreads=nt)
         mt.append(time.perf_counter() - t0)
     return {"value": round(us, 1), "unit": "us/layer", "cores": 1, "kind": kind,
+            "host_cpu": host_cpu(),
             "sample": "%d single-token MoE layer steps (median), one pool layer, "
                       "selected experts copied to host; single thread as qw6" % len(times),
             "multicore": {"value": round(1e6 * float(np.median(mt)), 1), "cores": nt, "kind": "port",
                           "sample": "%d of the same steps, the oracle's OpenMP row-parallel "
-                                    "build" % len(mt)}}
+                                    "build on %d of the host's %d logical CPUs"
+                                    % (len(mt), nt, os.cpu_count())}}
 
 
 # ---- workloads --------------------------------------------------------------------
 
 def bench_decode(torch, Q, S, ctx, pool, X, out, idx, args, profile=True):
+    import numpy as np
     P = len(pool)
 
     def step(k, sp):
@@ -262,15 +305,25 @@ def bench_decode(torch, Q, S, ctx, pool, X, out, idx, args, profile=True):
     torch.cuda.synchronize()
     eager_us = 1e6 * (time.perf_counter() - t0) / K
     if args.no_graph:
-        us_layer, steps = eager_us, K
+        us_layer, steps, spread = eager_us, K, None
     else:
-        reps = max(1, K // P)
-        sec, _ = graph_time(torch, lambda s: [step(j, s) for j in range(P)], reps)
-        us_layer, steps = 1e6 * sec / P, reps * P
+        # the K timed steps (layer k % P for step k) captured as one graph;
+        # 20 replays of it, each timed on its own: the median, p10 and p90 of
+        # the per-layer time over the replays
+        reps = 20
+        per = np.array(graph_replay_times(torch, lambda s: [step(k, s) for k in range(K)], reps))
+        per_layer = 1e6 * per / K
+        us_layer, steps = float(np.median(per_layer)), K
+        spread = {"replays": reps, "layers_per_replay": K,
+                  "median": round(us_layer, 3),
+                  "p10": round(float(np.percentile(per_layer, 10)), 3),
+                  "p90": round(float(np.percentile(per_layer, 90)), 3),
+                  "min": round(float(per_layer.min()), 3)}
     res = {"us_per_layer": round(us_layer, 3), "eager_us_per_layer": round(eager_us, 3),
            "steps": steps, "bytes_per_step": int(step_b),
            "hbm_GBps": round(step_b / us_layer / 1e3, 1),
-           "hbm_frac": round(step_b / us_layer / 1e3 / HBM_PEAK_GBPS, 4)}
+           "hbm_frac": round(step_b / us_layer / 1e3 / HBM_PEAK_GBPS, 4),
+           "us_per_layer_spread": spread}
     if profile:
         # per-kernel durations from each kernel's own dispatch timestamps (HIP
         # events recorded by hipExtLaunchKernel on the launch stream)
@@ -387,31 +440,22 @@ def bench_head(torch, Q, S, ctx, args):
 
 
 def bench_stack(torch, Q, S, ctx, args):
-    """40 IQ2_M-mix layers, h <- h + MoE_l(RMSNorm(h, w_l)), single-token steps."""
-    from qw6_amd.workload import SynthLayer
+    """40 IQ2_M-mix layers, h <- h + MoE_l(RMSNorm(h, w_l)), single-token steps
+    (qw6_amd.workload.SynthStack: the norm fused into each layer's call, the
+    hidden state updated in place, the step captured as one HIP graph)."""
+    from qw6_amd.workload import SynthStack
     NL, NS = 40, args.stack_steps
     log("stack: building %d layers" % NL)
-    layers = [SynthLayer(ctx, 3000 + l, l, "iq2m") for l in range(NL)]
-    nw = torch.empty(NL, HIDDEN, dtype=torch.float32, device="cuda")
-    descs = []
-    for l, L in enumerate(layers):
-        Q.synth_normal(nw[l], HIDDEN, 0.1, 3000, S.stream_id(l, S.K_NORM), mean=1.0)
-        d = Q.MoeLayer.from_buffer_copy(L.desc)
-        d.norm_w, d.norm_eps = nw[l].data_ptr(), 1e-6
-        descs.append(d)
+    stk = SynthStack(ctx, 3000, NL, "iq2m")
     X = torch.empty(NS, HIDDEN, dtype=torch.float32, device="cuda")
     for s in range(NS):
         Q.synth_normal(X[s], HIDDEN, 1.0, 3001, S.stream_id(s, S.K_X))
     h = torch.empty(1, HIDDEN, dtype=torch.float32, device="cuda")
+    h.copy_(X[0])
     idx = torch.zeros(NL, TOP_K, dtype=torch.int32, device="cuda")
     torch.cuda.synchronize()
-
-    def one_step(sp):
-        for l in range(NL):
-            ctx.moe_forward(descs[l], h, h, n_tok=1, residual=h, idx=idx[l], stream=sp)
-
     # the step is captured once; each token's input is copied in before its replay
-    _, g = graph_time(torch, one_step, 1)
+    g = stk.capture(h, idx)
     for s in range(4):
         h.copy_(X[s])
         g.replay()
@@ -422,19 +466,18 @@ def bench_stack(torch, Q, S, ctx, args):
         g.replay()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    r_b, gu_b, d_b, step_b = algorithmic_bytes(layers, idx.cpu().numpy())
+    r_b, gu_b, d_b, step_b = algorithmic_bytes(stk.layers, idx.cpu().numpy())
     tok_bytes = step_b * NL
     res = {"layers": NL, "steps": NS, "tokens_per_s": round(NS / wall, 1),
            "us_per_token": round(1e6 * wall / NS, 2),
            "us_per_layer": round(1e6 * wall / NS / NL, 3),
            "bytes_per_token": int(tok_bytes),
            "hbm_GBps": round(tok_bytes * NS / wall / 1e9, 1),
-           "resident_GB": round(sum(sum(p.numel() for p in L.packs) for L in layers) / 1e9, 2),
+           "resident_GB": round(stk.resident_bytes() / 1e9, 2),
            "workload": "40 layers IQ2_XXS gate/up + IQ3_S/IQ2_S down, F32 router, shared "
                        "expert, RMSNorm (eps 1e-6) fused before each layer, residual in "
                        "place; 128 single-token steps with fresh inputs"}
-    for L in layers:
-        L.free()
+    stk.free()
     return res
 
 
@@ -636,15 +679,17 @@ def main():
         ctx.close()
         return
 
-    gk = res_main["kernels"]["k_moe_gate_up"]
+    kname = "k_moe_gate_up"
+    gk = res_main["kernels"][kname]
     achieved = gk["GBps"]
     traffic = None
     traffic_src = None
     if mix == "q4k" and os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as fh:
             tj = json.load(fh)
-        traffic = tj.get("traffic_bytes_per_launch")
-        traffic_src = os.path.relpath(TRAFFIC_FILE, HERE)
+        if tj.get("kernel") == kname:
+            traffic = tj.get("traffic_bytes_per_launch")
+            traffic_src = os.path.relpath(TRAFFIC_FILE, HERE)
     res = {
         "metric": "decode MoE-FFN us/layer + HBM GB/s vs 8 TB/s peak; T=512 prefill TFLOP/s",
         "value": res_main["us_per_layer"],
@@ -656,6 +701,7 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
+        "us_per_layer_spread": res_main["us_per_layer_spread"],
         "dtype": "f32",
         "data": "synthetic (seeded GGUF blocks generated on device)",
         "config": {"workload": "MoE FFN decode layer, batch 1: hidden 2048, 256 experts "
@@ -670,7 +716,7 @@ def main():
         "kernels": res_main["kernels"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                     "traffic": traffic, "kernel": "k_moe_gate_up",
+                     "traffic": traffic, "kernel": kname,
                      "algorithmic_bytes": gk["bytes"], "avg_us": gk["us"],
                      "traffic_source": traffic_src},
         "cpu_baseline": cpu,

@@ -162,6 +162,7 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t *ctx, const qw6_hip_moe_layer_t *layer,
  * Returns -1 for another value. */
 int qw6_hip_set_mode(qw6_hip_ctx_t *ctx, int mode);
 
+
 /* Per-kernel timing of qw6_hip_moe_forward on its launch stream (eager calls
  * only, not under graph capture). max_calls > 0 starts recording for up to
  * that many calls, 0 stops. Each of the three decode kernels (router,
@@ -188,8 +189,19 @@ int qw6_hip_rmsnorm(qw6_hip_ctx_t *ctx, const float *x, const float *w,
  * allocated on first use. */
 int qw6_hip_argmax(qw6_hip_ctx_t *ctx, const float *x, uint32_t n,
                    uint32_t *out, void *stream);
-/* The same, synchronous, host buffers in and out. */
-int qw6_hip_argmax_host(const float *x, uint32_t n, uint32_t *out);
+/* The same, synchronous, host buffers in and out: *out_idx the index and
+ * *out_val (if out_val is not NULL) the element x[*out_idx]. Replaces
+ * qw6_vk_argmax_host (qw6_vk.h:26-27, qw6_vk.c:811-833, 1258-1265). */
+int qw6_hip_argmax_host(const float *x, uint32_t n, uint32_t *out_idx,
+                        float *out_val);
+/* Greedy token of host logits[0..n): the index qw6_hip_argmax_host returns.
+ * Replaces qw6_vk_sampling_greedy_host (qw6_vk.h:28-29, qw6_vk.c:835-856,
+ * 1267-1274); n == 0 fails as there. Ties and NaNs follow qw6_cpu_argmax
+ * (qw6.c:2858-2863), the rule qw6's CPU greedy path applies; qw6's Vulkan
+ * sampling.comp starts from -FLT_MAX and merges per-lane winners by lane, so
+ * it can return a later index among exactly equal maxima. */
+int qw6_hip_sampling_greedy_host(const float *logits, uint32_t n,
+                                 uint32_t *token);
 
 /* Greedy token of the output head (qw6_forward_token's tail, qw6.c:2490-2493,
  * then qw6_cpu_argmax; the GPU path of qw6_vk_pipe_forward_greedy,

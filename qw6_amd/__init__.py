@@ -93,7 +93,8 @@ def lib():
         L.qw6_hip_rmsnorm.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                       C.c_uint32, C.c_uint32, C.c_float, C.c_void_p]
         L.qw6_hip_argmax.argtypes = [C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p]
-        L.qw6_hip_argmax_host.argtypes = [_f32p, C.c_uint32, _u32p]
+        L.qw6_hip_argmax_host.argtypes = [_f32p, C.c_uint32, _u32p, C.c_void_p]
+        L.qw6_hip_sampling_greedy_host.argtypes = [_f32p, C.c_uint32, _u32p]
         L.qw6_hip_output_greedy.argtypes = [C.c_void_p, C.POINTER(Matrix), C.c_void_p,
                                             C.c_void_p, C.c_float, C.c_void_p, C.c_void_p,
                                             C.c_void_p]
@@ -163,11 +164,21 @@ def rmsnorm_host(x: np.ndarray, w: np.ndarray, eps: float = 1e-6) -> np.ndarray:
     return y
 
 
-def argmax_host(x: np.ndarray) -> int:
-    """First index of the maximum, qw6_cpu_argmax semantics (qw6.c:2858-2863)."""
+def argmax_host(x: np.ndarray, with_value: bool = False):
+    """First index of the maximum, qw6_cpu_argmax semantics (qw6.c:2858-2863)
+    (qw6_vk_argmax_host); with_value: (index, x[index])."""
     x = np.ascontiguousarray(x, np.float32).reshape(-1)
     out = np.zeros(1, np.uint32)
-    _check(lib().qw6_hip_argmax_host(x, x.size, out))
+    val = np.zeros(1, np.float32)
+    _check(lib().qw6_hip_argmax_host(x, x.size, out, val.ctypes.data if with_value else None))
+    return (int(out[0]), val[0]) if with_value else int(out[0])
+
+
+def sampling_greedy_host(logits: np.ndarray) -> int:
+    """Greedy token of host logits (qw6_vk_sampling_greedy_host)."""
+    x = np.ascontiguousarray(logits, np.float32).reshape(-1)
+    out = np.zeros(1, np.uint32)
+    _check(lib().qw6_hip_sampling_greedy_host(x, x.size, out))
     return int(out[0])
 
 

@@ -23,15 +23,35 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-shared",
 
 
 def build(verbose: bool = False) -> Path:
-    srcs = [str(CSRC / s) for s in SOURCES if (CSRC / s).exists()]
+    """Compile every source to an object in parallel (one hipcc per source),
+    then link the shared library."""
+    srcs = [CSRC / s for s in SOURCES if (CSRC / s).exists()]
+    odir = PKG / "_build"
+    odir.mkdir(exist_ok=True)
+    procs = []
+    for s in srcs:
+        obj = odir / (s.name + ".o")
+        cmd = [HIPCC, *FLAGS, "-c", "-o", str(obj), str(s)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((s, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE,
+                                               stderr=subprocess.STDOUT, text=True)))
+    failed = False
+    for s, obj, p in procs:
+        out, _ = p.communicate()
+        if p.returncode != 0:
+            sys.stderr.write(out)
+            failed = True
+    if failed:
+        raise RuntimeError("hipcc failed building %s" % LIB)
     tmp = LIB.with_suffix(".so.tmp")
-    cmd = [HIPCC, *FLAGS, "-o", str(tmp), *srcs]
+    cmd = [HIPCC, *FLAGS, "-o", str(tmp), *[str(o) for _, o, _ in procs]]
     if verbose:
         print(" ".join(cmd), flush=True)
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         sys.stderr.write(r.stdout + r.stderr)
-        raise RuntimeError("hipcc failed building %s" % LIB)
+        raise RuntimeError("hipcc failed linking %s" % LIB)
     os.replace(tmp, LIB)
     return LIB
 

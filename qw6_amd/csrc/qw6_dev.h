@@ -584,8 +584,13 @@ __device__ __forceinline__ uint32_t scatter_step(uint32_t lane, uint32_t g) {
 
 // Order-preserving 32-bit key of a logit: unsigned key order equals float
 // order (-0 folded into +0, which compare equal). Ties between equal logits
-// are broken by index separately (lowest index wins).
-__device__ __forceinline__ uint32_t route_key(float v) {
+// are broken by index separately (lowest index wins). NaN logits take qw6's
+// meaning (each round of qw6_cpu_moe_route scans with a strict '>' from
+// best = index 0): a NaN at index 0 wins the first round whatever else is
+// there (key 0xffffffff, above every other key), a NaN elsewhere never wins
+// a comparison, so it is below every real key, -inf included (key 0).
+__device__ __forceinline__ uint32_t route_key(float v, bool first) {
+    if (v != v) return first ? 0xffffffffu : 0u;
     const uint32_t u = __float_as_uint(v + 0.0f);
     return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
@@ -617,10 +622,12 @@ __device__ __forceinline__ void route_keys(const float* __restrict__ logits, uin
     const uint32_t lane = threadIdx.x & 63u;
     if ((((uintptr_t)logits & 15u) == 0) && 4 * lane + 3 < n) {
         const float4 v = *(const float4*)(logits + 4 * lane);
-        k[0] = route_key(v.x); k[1] = route_key(v.y); k[2] = route_key(v.z); k[3] = route_key(v.w);
+        k[0] = route_key(v.x, lane == 0); k[1] = route_key(v.y, false);
+        k[2] = route_key(v.z, false); k[3] = route_key(v.w, false);
     } else {
 #pragma unroll
-        for (int i = 0; i < 4; i++) k[i] = 4 * lane + i < n ? route_key(logits[4 * lane + i]) : 0u;
+        for (int i = 0; i < 4; i++)
+            k[i] = 4 * lane + i < n ? route_key(logits[4 * lane + i], lane == 0 && i == 0) : 0u;
     }
 }
 
@@ -738,8 +745,11 @@ __device__ __forceinline__ void wave_route_keys(uint32_t (&k)[4], uint32_t top_k
     float v = -INFINITY;
     if (lane < top_k) {
         const uint2 me = scr[32 + lane];
-        v = key_value(me.y);
-        e = me.y > kKeyNegInf ? ~me.x : 0u;   // only -inf left: qw6 picks index 0
+        // only -inf (or NaN away from index 0) left: qw6 picks index 0, whose
+        // logit has been set to -inf by then
+        const bool live = me.y > kKeyNegInf;
+        v = live ? key_value(me.y) : -INFINITY;
+        e = live ? ~me.x : 0u;
     }
     const float mx = key_value(scr[32].y);   // rank 0 holds the maximum
     const float ex = lane < top_k ? expf(v - mx) : 0.f;

@@ -15,8 +15,10 @@
 //                  selected expert (plus the shared one); per-expert row sums
 //                  meet in LDS and are combined in selection order, with the
 //                  residual -- no atomics, deterministic.
-// Batches of 32 tokens or more take the grouped bf16-MFMA kernels of
-// qw6_prefill.hip.
+// In the automatic mode, calls of 5 tokens or more take the grouped bf16-MFMA
+// kernels of qw6_prefill.hip when every matrix kind has one format; other
+// calls run in per-token launches of up to 4 tokens, 4 (and 3 for mixed
+// formats) on the small-batch MFMA kernels k_mx_*, fewer on the fp32 ones.
 // Routing never leaves the device (qw6's Vulkan path reads idx/w back to the
 // host per layer, qw6_vk.c:3371-3374).
 //
@@ -1439,7 +1441,7 @@ __global__ void k_silu_mul(const float* g, const float* u, float* o, uint32_t n)
 constexpr uint32_t kArgmaxBlocks = 512;   // partial maxima of the first pass
 
 __device__ __forceinline__ uint64_t amax_key(float v, uint32_t i) {
-    const uint32_t k = v != v ? 0u : route_key(v);
+    const uint32_t k = v != v ? 0u : route_key(v, false);
     return ((uint64_t)k << 32) | (uint32_t)~i;
 }
 __device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
@@ -1627,8 +1629,11 @@ __global__ void k_synth_blocks(uint8_t* dst, int fmt, uint64_t nblocks, uint64_t
 __global__ void k_synth_normal(float* dst, uint64_t n, float mean, float sd, uint64_t key) {
     const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
-    const float z = sm_normal(key, 3 * i) * sd;
-    dst[i] = mean == 0.f ? z : mean + z;
+    {   // two roundings, as the host generator (no fused multiply-add)
+#pragma clang fp contract(off)
+        const float z = sm_normal(key, 3 * i) * sd;
+        dst[i] = mean == 0.f ? z : mean + z;
+    }
 }
 
 }  // namespace
@@ -1877,6 +1882,19 @@ int alloc_owned(qw6_hip_ctx_t* c, size_t bytes, void** p) {
     CK(hipMemset(*p, 0, bytes ? bytes : 16));
     return 0;
 }
+
+// Per-token decode workspace: the buffers ensure_ws and ensure_mx_ws allocate.
+struct DecodeWs {
+    float* logits;
+    float* sw;
+    float* xn;
+    SlotTable* slots;
+    float* mid;
+    uint4* mxa;
+    uint16_t* mxs;
+    uint4* mma;
+    uint16_t* mms;
+};
 
 int ensure_argmax_ws(qw6_hip_ctx_t* c) {
     if (c->amax_part) return 0;
@@ -2349,16 +2367,13 @@ int launch_moe(const MoeArgs& a, const MoeLaunch& m, hipStream_t st, hipEvent_t*
     return rc;
 }
 
-}  // namespace
-
-extern "C" {
-
-int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float* x,
-                        const float* logits, const float* residual, uint32_t n_tok,
-                        float* out, uint32_t* idx, float* w, void* stream) {
+int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float* x,
+                     const float* logits, const float* residual, uint32_t n_tok, float* out,
+                     uint32_t* idx, float* w, void* stream) {
     if (!c || !L || !L->experts || !x || !out) return fail("null pointer");
     if (n_tok == 0) return 0;
-    if (n_tok > c->max_tokens) return fail("n_tok %u > context max_tokens %u", n_tok, c->max_tokens);
+    if (n_tok > c->max_tokens)
+        return fail("n_tok %u > context max_tokens %u", n_tok, c->max_tokens);
     const qw6_hip_experts_t* E = L->experts;
     if (L->hidden != E->hidden || L->inter != E->inter)
         return fail("layer dims %ux%u do not match the expert table %ux%u", L->hidden, L->inter,
@@ -2419,11 +2434,12 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
         P.sg = sg; P.su = su; P.sd = sd;
         return prefill_forward(P, c->pre, st);
     }
-    if (ensure_ws(c, L->hidden, L->inter)) return -1;
     // per-token path: the fp32 kernels (k_moe_*) or the small-batch MFMA
     // kernels (k_mx_*: mode 3, or automatic for more than one token per launch)
     const bool mx_any = c->mode == 3 || c->mode == 0;
+    if (ensure_ws(c, L->hidden, L->inter)) return -1;
     if (mx_any && ensure_mx_ws(c, L->hidden, L->inter)) return -1;
+    const DecodeWs ws = {c->logits, c->sw, c->xn, c->slots, c->mid, c->mxa, c->mxs, c->mma, c->mms};
 
     MoeArgs a;
     memset(&a, 0, sizeof a);
@@ -2437,11 +2453,11 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
     a.experts = E->dev;
     for (int k = 0; k < 3; k++) a.pk[k] = E->pk[k];
     a.sg = sg; a.su = su; a.sd = sd;
-    a.logits = c->logits; a.sw = c->sw; a.xn = c->xn; a.mid = c->mid; a.slots = c->slots;
+    a.logits = ws.logits; a.sw = ws.sw; a.xn = ws.xn; a.mid = ws.mid; a.slots = ws.slots;
     a.tmask_gu = mgu;
     a.tmask_dn = mdn;
     a.xl_dn = E->xl_dn;
-    a.xs = c->mxs; a.ma = c->mma; a.ms = c->mms;
+    a.xs = ws.mxs; a.ma = ws.mma; a.ms = ws.mms;
     // k_mx_* launch shape: the staged block of a format (largest of those in use)
     auto sb_of = [](int f) {
         if (f >= 0) return mx_stage_bytes(f);
@@ -2484,7 +2500,7 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
         // formats are mixed (the fp32 kernels then dispatch per matrix)
         m.mx = c->mode == 3 ||
                (c->mode == 0 && (T >= kMxMinTokens || (T == kMxMinTokens - 1 && (m.fg < 0 || m.fd < 0))));
-        a.xa = m.mx ? c->mxa : nullptr;   // k_moe_router writes the operands
+        a.xa = m.mx ? ws.mxa : nullptr;   // k_moe_router writes the operands
         const uint32_t S = T == 2 ? 4u : 2u;                   // gu_steps<T>()
         const uint32_t rows_wg = 4 * S * rpsg;                 // gate/up rows per workgroup
         const uint32_t ntile_b = (L->inter + rows_wg - 1) / rows_wg;
@@ -2492,9 +2508,9 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
         m.lds_b = (size_t)tab_bytes(mgu) + 4 * S * a.gu_pb;
         m.grid_c = grid_c_valu;
         a.x = x + (size_t)t0 * L->hidden;
-        a.xin = L->norm_w ? c->xn : a.x;
+        a.xin = L->norm_w ? ws.xn : a.x;
         a.router = logits ? nullptr : L->router;
-        a.route_logits = logits ? logits + (size_t)t0 * E->n : c->logits;
+        a.route_logits = logits ? logits + (size_t)t0 * E->n : ws.logits;
         a.residual = residual ? residual + (size_t)t0 * L->hidden : nullptr;
         a.out = out + (size_t)t0 * L->hidden;
         a.idx_out = idx ? idx + (size_t)t0 * L->top_k : nullptr;
@@ -2538,6 +2554,16 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const fl
     return 0;
 }
 
+}  // namespace
+
+extern "C" {
+
+int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float* x,
+                        const float* logits, const float* residual, uint32_t n_tok,
+                        float* out, uint32_t* idx, float* w, void* stream) {
+    return moe_forward_impl(c, L, x, logits, residual, n_tok, out, idx, w, stream);
+}
+
 int qw6_hip_profile(qw6_hip_ctx_t* c, uint32_t max_calls) {
     if (!c) return fail("null ctx");
     DevGuard g(c->device);
@@ -2568,8 +2594,8 @@ int qw6_hip_profile_read(qw6_hip_ctx_t* c, float ms[3], uint32_t* calls) {
     return 0;
 }
 
-int qw6_hip_argmax_host(const float* x, uint32_t n, uint32_t* out) {
-    if (!x || !out) return fail("null pointer");
+int qw6_hip_argmax_host(const float* x, uint32_t n, uint32_t* out_idx, float* out_val) {
+    if (!x || !out_idx) return fail("null pointer");
     if (n == 0) return fail("argmax of an empty vector");
     DevBuf bx, bp, bo;
     CK(hipMalloc(&bx.p, (size_t)n * 4));
@@ -2578,8 +2604,17 @@ int qw6_hip_argmax_host(const float* x, uint32_t n, uint32_t* out) {
     CK(hipMemcpy(bx.p, x, (size_t)n * 4, hipMemcpyHostToDevice));
     if (launch_argmax((const float*)bx.p, n, (uint64_t*)bp.p, (uint32_t*)bo.p, nullptr)) return -1;
     CK(hipDeviceSynchronize());
-    CK(hipMemcpy(out, bo.p, 4, hipMemcpyDeviceToHost));
+    uint32_t i = 0;
+    CK(hipMemcpy(&i, bo.p, 4, hipMemcpyDeviceToHost));
+    if (i >= n) return fail("argmax index %u out of range", i);
+    *out_idx = i;
+    if (out_val) *out_val = x[i];   // the selected element itself, bit for bit
     return 0;
+}
+
+int qw6_hip_sampling_greedy_host(const float* logits, uint32_t n, uint32_t* token) {
+    if (!logits || !token) return fail("null pointer");
+    return qw6_hip_argmax_host(logits, n, token, nullptr);
 }
 
 int qw6_hip_argmax(qw6_hip_ctx_t* c, const float* x, uint32_t n, uint32_t* out, void* stream) {

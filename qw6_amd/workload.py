@@ -119,3 +119,65 @@ class SynthLayer:
         self.experts.free()
         self.packs = self.shared_bufs = []
         self.router = None
+
+
+class SynthStack:
+    """n_layers seeded MoE layers run as one decode step per token:
+    h <- h + MoE_l(RMSNorm(h, w_l)) for l = 0 .. n_layers - 1 (qw6.c:2475-2484
+    around qw6_apply_layer_moe, RMSNorm qw6.c:2503-2513), each layer one
+    qw6_hip_moe_forward call with its norm weight fused in (norm_w) and the
+    hidden state updated in place (x = residual = out).
+
+    Layer l is SynthLayer(seed + l * seed_step, l, mix); its norm weight is
+    N(1, 0.1) from (seed, stream (l, K_NORM)), generated on the device.
+    """
+
+    def __init__(self, ctx: Context, seed: int, n_layers: int, mix: str = "iq2m",
+                 seed_step: int = 1, hidden: int = 2048, eps: float = 1e-6):
+        import torch
+        from . import MoeLayer
+        self.ctx, self.seed, self.n_layers, self.hidden, self.eps = ctx, seed, n_layers, hidden, eps
+        dev = torch.device("cuda", ctx.device)
+        self.layers = [SynthLayer(ctx, seed + l * seed_step, l, mix, hidden=hidden)
+                       for l in range(n_layers)]
+        self.norm_w = torch.empty(n_layers, hidden, dtype=torch.float32, device=dev)
+        self.descs = []
+        for l, L in enumerate(self.layers):
+            synth_normal(self.norm_w[l], hidden, 0.1, seed, S.stream_id(l, S.K_NORM), mean=1.0)
+            d = MoeLayer.from_buffer_copy(L.desc)
+            d.norm_w, d.norm_eps = self.norm_w[l].data_ptr(), eps
+            self.descs.append(d)
+        torch.cuda.synchronize()
+
+    def step(self, h, idx, stream, hist=None):
+        """One token through every layer, in place on h [1][hidden]; idx[l]
+        receives layer l's selection. With hist, hist[l] receives h after
+        layer l (a device copy on torch's current stream, which must be
+        `stream`)."""
+        for l in range(self.n_layers):
+            self.ctx.moe_forward(self.descs[l], h, h, n_tok=1, residual=h, idx=idx[l],
+                                 stream=stream)
+            if hist is not None:
+                hist[l].copy_(h[0])
+
+    def capture(self, h, idx, hist=None):
+        """The step captured as one HIP graph on a side stream (after one
+        eager warm-up call); returns the graph."""
+        import torch
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            self.step(h, idx, s.cuda_stream, hist)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(g, stream=s):
+                self.step(h, idx, s.cuda_stream, hist)
+        torch.cuda.synchronize()
+        return g
+
+    def resident_bytes(self) -> int:
+        return sum(sum(p.numel() for p in L.packs) for L in self.layers)
+
+    def free(self):
+        for L in self.layers:
+            L.free()
+        self.layers = []

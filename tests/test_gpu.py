@@ -110,6 +110,28 @@ def test_host_route_exact(name):
     assert np.abs(w - G[name + "_w"]).max() <= 2e-5
 
 
+def test_host_route_nan_logits_vs_oracle():
+    """NaN router logits: the device routing gives qw6's indices (a NaN at
+    index 0 selected first, NaNs elsewhere never) and weights (all NaN when
+    the first pick is a NaN), against the oracle; plus 256-expert vectors with
+    NaNs scattered, at index 0 and not."""
+    from test_oracle import nan_route_cases
+    rng = np.random.default_rng(17)
+    vecs = [(np.array(lg, np.float32), k) for lg, k, _ in nan_route_cases()]
+    for trial in range(12):
+        lg = rng.standard_normal(256).astype(np.float32)
+        lg[rng.integers(0, 256, 1 + trial)] = np.nan
+        if trial % 3 == 0:
+            lg[0] = np.nan
+        vecs.append((lg, 8))
+    for lg, k in vecs:
+        idx, w = Q.moe_route_host(lg, k)
+        oi, ow = O.moe_route(lg, k)
+        assert np.array_equal(idx.astype(np.int32), oi), (lg, idx, oi)
+        assert np.array_equal(np.isnan(w), np.isnan(ow))
+        assert np.abs(np.nan_to_num(w) - np.nan_to_num(ow)).max() <= 2e-5
+
+
 def test_host_route_brute_force_ties():
     rng = np.random.default_rng(7)
     for _ in range(40):
@@ -152,6 +174,10 @@ def test_device_synth_matches_host_generator(torch_dev, ctx):
     Q.synth_normal(f, 5000, 0.02, 17, 99)
     torch.cuda.synchronize()
     assert np.array_equal(f.cpu().numpy(), S.f32_normal(17, 99, 5000, 0.02))
+    # with a mean (norm weights N(1, 0.1)): mean + sd * z, two roundings
+    Q.synth_normal(f, 5000, 0.1, 17, 98, mean=1.0)
+    torch.cuda.synchronize()
+    assert np.array_equal(f.cpu().numpy(), S.f32_normal(17, 98, 5000, 0.1, mean=1.0))
 
 
 @pytest.mark.parametrize("q", FORMATS)

@@ -77,8 +77,30 @@ def test_argmax_device_and_host_vs_oracle(torch_dev, ctx):
         want = O.argmax(x)
         assert dev_argmax(torch_dev, ctx, x) == want, (i, x.size)
         if x.size <= 65537:
-            assert Q.argmax_host(x) == want, (i, x.size)
+            got, val = Q.argmax_host(x, with_value=True)
+            assert got == want, (i, x.size)
+            assert np.array_equal(np.float32(val).view(np.uint32), x[want].view(np.uint32))
+            assert Q.sampling_greedy_host(x) == want, (i, x.size)
     say("argmax vectors checked:", len(vecs))
+
+
+def test_host_argmax_and_greedy_kats():
+    """qw6's Vulkan self-test vectors for the two host ops (qw6_vk.c:1810-1838):
+    argmax over 4097 values with 42 planted at 3079 (index and value), and
+    greedy sampling over 1029 logits with 11 planted at 877."""
+    an = 4097
+    i = np.arange(an, dtype=np.float32)
+    ax = (np.sin(i * np.float32(0.019)) - (np.arange(an) % 7).astype(np.float32) * np.float32(0.01)
+          ).astype(np.float32)
+    ax[3079] = 42.0
+    assert Q.argmax_host(ax, with_value=True) == (3079, np.float32(42.0))
+    gn = 1029
+    j = np.arange(gn, dtype=np.float32)
+    gx = (np.cos(j * np.float32(0.023)) - np.float32(0.001) * j).astype(np.float32)
+    gx[877] = 11.0
+    assert Q.sampling_greedy_host(gx) == 877
+    with pytest.raises(Q.Qw6HipError):
+        Q.sampling_greedy_host(np.zeros(0, np.float32))
 
 
 def test_argmax_unaligned_and_ties_across_blocks(torch_dev, ctx):

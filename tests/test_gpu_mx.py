@@ -257,19 +257,30 @@ def test_mx_graph_replay_matches_eager(torch_dev, ctx):
 
 
 def test_auto_mode_mixed_chunks_vs_oracle(torch_dev, ctx):
-    """Automatic path selection on 5 and 7 tokens: launches of 4 tokens (MFMA
-    kernels) followed by 1 or 3 (fp32 kernels, one format per matrix kind) in
-    one call."""
+    """Automatic path selection on a mixed-format layer (IQ2_XXS gate/up,
+    IQ3_S / IQ2_S down: the grouped kernels refuse it, so the call runs in
+    per-token launches of up to 4 tokens): 5 tokens = a launch of 4 on the
+    MFMA kernels then 1 on the fp32 kernels, 6 = 4 (MFMA) + 2 (fp32),
+    7 = 4 (MFMA) + 3 (MFMA, as for mixed formats). A uniform Q4_K layer under
+    the per-token mode (1) takes 4 + 1 on the fp32 kernels."""
     from qw6_amd.workload import SynthLayer
-    L = SynthLayer(ctx, 67, 0, "q4k")
+    L = SynthLayer(ctx, 67, 0, "iq2m")
     try:
         router = L.router_host()
         n = 0
-        for T in (5, 7):
+        for T in (5, 6, 7):
             xs = np.stack([cases.token_x(670 + T, 1, t) for t in range(T)])
             out, idx = run(torch_dev, ctx, L, xs, 0)
             n += check_tokens(L, xs, out, idx, router=router)
-        assert n >= 10
+        assert n >= 15
+    finally:
+        L.free()
+    L = SynthLayer(ctx, 69, 0, "q4k")
+    try:
+        router = L.router_host()
+        xs = np.stack([cases.token_x(695, 1, t) for t in range(5)])
+        out, idx = run(torch_dev, ctx, L, xs, 1)
+        assert check_tokens(L, xs, out, idx, router=router) >= 4
     finally:
         L.free()
 

@@ -241,6 +241,37 @@ def test_route_kat_small():
     assert list(idx) == [1, 2] and abs(w.sum() - 1) < 1e-6 and w[0] > w[1]
 
 
+def nan_route_cases():
+    """Router logits with NaNs, and qw6's answer worked by hand from its loop
+    (qw6.c:2808-2816: each round scans with a strict '>' from best = index 0,
+    then sets the winner to -inf): a NaN at index 0 wins the first round, a
+    NaN elsewhere never wins, and once only -inf / NaN remain index 0 (by then
+    -inf) is picked again."""
+    nan, inf = np.float32(np.nan), np.float32(np.inf)
+    return [
+        ([1.0, nan, 3.0, 2.0], 2, [2, 3]),
+        ([nan, 5.0, 1.0], 2, [0, 1]),
+        ([-np.float32(np.nan), 5.0, 1.0], 2, [0, 1]),   # a NaN with the sign bit set
+        ([1.0, nan, nan, 2.0], 4, [3, 0, 0, 0]),
+        ([nan, nan, nan], 3, [0, 0, 0]),
+        ([-inf, nan, 4.0, nan, -inf], 3, [2, 0, 0]),
+        ([3.0, nan, inf, 3.0], 3, [2, 0, 3]),
+    ]
+
+
+def test_route_nan_kats():
+    for lg, k, want in nan_route_cases():
+        lg = np.array(lg, np.float32)
+        idx, w = O.moe_route(lg, k)
+        assert list(idx) == want, (lg, idx, want)
+        if np.isnan(lg[0]):
+            assert np.isnan(w).all()   # qw6's max and softmax then propagate the NaN
+        if O.ref() is not None:
+            ri, rw = O.ref_moe_route(lg, k)
+            assert np.array_equal(ri, idx)
+            assert np.array_equal(bits(rw), bits(w))
+
+
 def test_route_brute_force_ties():
     """Top-k = stable argsort by (-value, index) on tiny inputs with duplicates."""
     rng = np.random.default_rng(3)
