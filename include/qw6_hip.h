@@ -150,6 +150,25 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t *ctx, const qw6_hip_moe_layer_t *layer,
                         const float *residual, uint32_t n_tok, float *out,
                         uint32_t *idx, float *w, void *stream);
 
+/* qw6_hip_moe_forward without any allocation, for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving
+ * loops). No counterpart in the reference. Same arguments, results and
+ * per-token kernels (launches of up to 4 tokens; never the grouped kernels,
+ * so mode 2 is refused); the kernels' workspace (router logits, selection
+ * table, expert intermediates, MFMA operands) is a 4 MiB static device array
+ * of the library instead of context allocations (every shape the per-token
+ * kernels take, hidden and inter up to 2048, needs at most 3.5 MB; a layer
+ * needing more would be refused with an error). Each device has one
+ * such array, shared by every context and call on that device: calls that
+ * overlap on one device race, so issue them on one stream (or otherwise
+ * order them). */
+int qw6_hip_moe_forward_noalloc(qw6_hip_ctx_t *ctx,
+                                const qw6_hip_moe_layer_t *layer,
+                                const float *x, const float *logits,
+                                const float *residual, uint32_t n_tok,
+                                float *out, uint32_t *idx, float *w,
+                                void *stream);
+
 /* Path selection for qw6_hip_moe_forward:
  * 0 = automatic (default): the fp32 per-token kernels for launches of 1-2
  *     tokens (and 3 when each matrix kind has one format), the small-batch

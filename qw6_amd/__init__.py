@@ -87,6 +87,7 @@ def lib():
         L.qw6_hip_moe_forward.argtypes = [C.c_void_p, C.POINTER(MoeLayer), C.c_void_p,
                                           C.c_void_p, C.c_void_p, C.c_uint32, C.c_void_p,
                                           C.c_void_p, C.c_void_p, C.c_void_p]
+        L.qw6_hip_moe_forward_noalloc.argtypes = L.qw6_hip_moe_forward.argtypes
         L.qw6_hip_profile.argtypes = [C.c_void_p, C.c_uint32]
         L.qw6_hip_profile_read.argtypes = [C.c_void_p, C.POINTER(C.c_float),
                                            C.POINTER(C.c_uint32)]
@@ -264,6 +265,15 @@ class Context:
         _check(lib().qw6_hip_moe_forward(self.handle, C.byref(layer), _addr(x), _addr(logits),
                                          _addr(residual), n_tok, _addr(out), _addr(idx),
                                          _addr(w), _stream(stream)))
+
+    def moe_forward_noalloc(self, layer: MoeLayer, x, out, n_tok: int = 1, logits=None,
+                            residual=None, idx=None, w=None, stream=None):
+        """moe_forward on the library's static per-device workspace: no
+        allocation, per-token kernels only (qw6_hip_moe_forward_noalloc)."""
+        _check(lib().qw6_hip_moe_forward_noalloc(self.handle, C.byref(layer), _addr(x),
+                                                 _addr(logits), _addr(residual), n_tok,
+                                                 _addr(out), _addr(idx), _addr(w),
+                                                 _stream(stream)))
 
     def profile(self, max_calls: int):
         _check(lib().qw6_hip_profile(self.handle, max_calls))

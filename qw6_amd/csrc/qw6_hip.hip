@@ -35,6 +35,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 #include <vector>
 
@@ -1678,6 +1679,8 @@ struct qw6_hip_ctx_s {
     uint64_t* amax_part;
     float* head_x;
     uint32_t head_hidden;
+    // this device's copy of the static decode workspace (qw6_hip_moe_forward_noalloc)
+    uint8_t* scratch;
 };
 
 int qw6::ctx_device(const qw6_hip_ctx_t* c) { return c->device; }
@@ -1883,7 +1886,36 @@ int alloc_owned(qw6_hip_ctx_t* c, size_t bytes, void** p) {
     return 0;
 }
 
-// Per-token decode workspace: the buffers ensure_ws and ensure_mx_ws allocate.
+// ---- the static decode workspace -------------------------------------------------
+// qw6_hip_moe_forward_noalloc runs the per-token kernels on a workspace that
+// is a file-scope device array instead of context allocations. Every device
+// the library runs on holds its own copy of the array (at its own address)
+// until the process ends. Host code never uses the array's name as an
+// address: each device's address comes from hipGetSymbolAddress, taken once
+// per device with that device current (at qw6_hip_ctx_init).
+constexpr size_t kScratchBytes = (size_t)4 << 20;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+uint8_t* g_scratch_addr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The address of `scratch` on `device` (which must be current).
+int scratch_address(int device, uint8_t** out) {
+    if (device < 0 || device >= kMaxDevices) return fail("device %d beyond the static workspace table", device);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_addr[device]) {
+        void* p = nullptr;
+        CK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail("no device address for the static workspace");
+        g_scratch_addr[device] = (uint8_t*)p;
+    }
+    *out = g_scratch_addr[device];
+    return 0;
+}
+
+// Per-token decode workspace carved from one region (256-byte aligned
+// pieces): the same buffers ensure_ws and ensure_mx_ws allocate one by one.
 struct DecodeWs {
     float* logits;
     float* sw;
@@ -1895,6 +1927,27 @@ struct DecodeWs {
     uint4* mma;
     uint16_t* mms;
 };
+
+size_t carve_decode_ws(uint8_t* base, uint32_t hidden, uint32_t inter, DecodeWs* w) {
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        uint8_t* p = base ? base + o : nullptr;
+        o += (bytes + 255) & ~(size_t)255;
+        return p;
+    };
+    DecodeWs d;
+    d.logits = (float*)take((size_t)kMaxTok * 256 * 4);
+    d.sw = (float*)take(kMaxTok * 4);
+    d.xn = (float*)take((size_t)kMaxTok * hidden * 4);
+    d.slots = (SlotTable*)take(sizeof(SlotTable));
+    d.mid = (float*)take((size_t)(kMaxSlots + 1) * kMaxTok * inter * 4);
+    d.mxa = (uint4*)take((size_t)(hidden / 32) * 64 * 16);
+    d.mxs = (uint16_t*)take((size_t)(hidden / 256) * 192 * 2);
+    d.mma = (uint4*)take((size_t)(kMaxSlots + 1) * (inter / 32) * 64 * 16);
+    d.mms = (uint16_t*)take((size_t)(kMaxSlots + 1) * (inter / 256) * 192 * 2);
+    if (w) *w = d;
+    return o;
+}
 
 int ensure_argmax_ws(qw6_hip_ctx_t* c) {
     if (c->amax_part) return 0;
@@ -2046,10 +2099,13 @@ int qw6_hip_ctx_init(qw6_hip_ctx_t** out, int device, uint32_t max_tokens) {
     if (device < 0 || device >= n) return fail("device %d not present (%d devices)", device, n);
     if (max_tokens == 0) return fail("max_tokens == 0");
     DevGuard g(device);
+    uint8_t* sp = nullptr;
+    if (scratch_address(device, &sp)) return -1;
     qw6_hip_ctx_t* c = new qw6_hip_ctx_t();
     c->device = device;
     c->max_tokens = max_tokens;
     c->mode = 0;
+    c->scratch = sp;
     *out = c;
     return 0;
 }
@@ -2367,12 +2423,15 @@ int launch_moe(const MoeArgs& a, const MoeLaunch& m, hipStream_t st, hipEvent_t*
     return rc;
 }
 
+// qw6_hip_moe_forward and, with noalloc, qw6_hip_moe_forward_noalloc: the
+// latter never takes the grouped kernels and runs the per-token ones on the
+// static workspace instead of the context's.
 int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float* x,
                      const float* logits, const float* residual, uint32_t n_tok, float* out,
-                     uint32_t* idx, float* w, void* stream) {
+                     uint32_t* idx, float* w, void* stream, bool noalloc) {
     if (!c || !L || !L->experts || !x || !out) return fail("null pointer");
     if (n_tok == 0) return 0;
-    if (n_tok > c->max_tokens)
+    if (!noalloc && n_tok > c->max_tokens)
         return fail("n_tok %u > context max_tokens %u", n_tok, c->max_tokens);
     const qw6_hip_experts_t* E = L->experts;
     if (L->hidden != E->hidden || L->inter != E->inter)
@@ -2417,9 +2476,11 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
     const bool grouped_ok = prefill_supports(fgu) && prefill_supports(fdn) &&
                             (!has_sh || (prefill_supports(sg.fmt) && prefill_supports(sd.fmt))) &&
                             L->hidden % 256 == 0 && L->inter % 256 == 0;
+    if (noalloc && c->mode == 2)
+        return fail("the grouped MFMA path needs context workspace: not available without allocation");
     if (c->mode == 2 && !grouped_ok)
         return fail("grouped MFMA path needs one format per matrix kind across the routed experts");
-    if (grouped_ok && (c->mode == 2 || (c->mode == 0 && n_tok >= kGroupedMinTokens))) {
+    if (!noalloc && grouped_ok && (c->mode == 2 || (c->mode == 0 && n_tok >= kGroupedMinTokens))) {
         if (ensure_prefill_ws(c, L->hidden, L->inter, E->n, L->top_k)) return -1;
         PrefillLayer P;
         memset(&P, 0, sizeof P);
@@ -2437,9 +2498,18 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
     // per-token path: the fp32 kernels (k_moe_*) or the small-batch MFMA
     // kernels (k_mx_*: mode 3, or automatic for more than one token per launch)
     const bool mx_any = c->mode == 3 || c->mode == 0;
-    if (ensure_ws(c, L->hidden, L->inter)) return -1;
-    if (mx_any && ensure_mx_ws(c, L->hidden, L->inter)) return -1;
-    const DecodeWs ws = {c->logits, c->sw, c->xn, c->slots, c->mid, c->mxa, c->mxs, c->mma, c->mms};
+    DecodeWs ws;
+    if (noalloc) {
+        const size_t need = carve_decode_ws(nullptr, L->hidden, L->inter, nullptr);
+        if (need > kScratchBytes)
+            return fail("layer %ux%u needs %zu bytes of decode workspace; the static workspace "
+                        "holds %zu", L->hidden, L->inter, need, kScratchBytes);
+        carve_decode_ws(c->scratch, L->hidden, L->inter, &ws);
+    } else {
+        if (ensure_ws(c, L->hidden, L->inter)) return -1;
+        if (mx_any && ensure_mx_ws(c, L->hidden, L->inter)) return -1;
+        ws = {c->logits, c->sw, c->xn, c->slots, c->mid, c->mxa, c->mxs, c->mma, c->mms};
+    }
 
     MoeArgs a;
     memset(&a, 0, sizeof a);
@@ -2561,7 +2631,14 @@ extern "C" {
 int qw6_hip_moe_forward(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float* x,
                         const float* logits, const float* residual, uint32_t n_tok,
                         float* out, uint32_t* idx, float* w, void* stream) {
-    return moe_forward_impl(c, L, x, logits, residual, n_tok, out, idx, w, stream);
+    return moe_forward_impl(c, L, x, logits, residual, n_tok, out, idx, w, stream, false);
+}
+
+int qw6_hip_moe_forward_noalloc(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L,
+                                const float* x, const float* logits, const float* residual,
+                                uint32_t n_tok, float* out, uint32_t* idx, float* w,
+                                void* stream) {
+    return moe_forward_impl(c, L, x, logits, residual, n_tok, out, idx, w, stream, true);
 }
 
 int qw6_hip_profile(qw6_hip_ctx_t* c, uint32_t max_calls) {
