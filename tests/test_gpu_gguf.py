@@ -233,4 +233,4 @@ def test_gguf_layer_errors(torch_dev, ctx, tmp_path):
     bad_router = [("blk.0.ffn_gate_inp.weight", G.G_F16, [H, N], np.zeros(N * H, np.uint16))] + full[1:]
     attempt(bad_router, "F32")
     wide = [("blk.0.ffn_gate_inp.weight", G.G_F32, [H, 2 * N], np.zeros(2 * N * H, np.float32))]
-    attempt(wide + full[1:], "expected 3 dims, last=8, expected 16")
+    attempt(wide + full[1:], r"is not \[cols, rows, 16\]: 3 dims, the last 8")

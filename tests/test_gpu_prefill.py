@@ -1,10 +1,13 @@
 """The batched (grouped bf16-MFMA) MoE path against the oracle, through the
-C ABI. Bars: expert indices exact for given router logits; outputs rel-L2
-<= 2e-3 per token (the bf16-MFMA bar; the construction -- exact integer codes,
-hi/lo activations, fp32 scales -- lands near 1e-5, which the tighter assert
-on the mean pins). The full T = 512 batch is checked against the per-token
-fp32 kernels of the same library (a size-independent consistency check) and
-on a sample of tokens against the oracle.
+C ABI. Bars: expert indices exact for given router logits. Outputs: calls of
+64 tokens or more, rel-L2 <= 2e-3 per token (the bf16-MFMA bar) with a mean
+<= 1e-4; calls of fewer tokens (where the automatic path also takes these
+kernels) are held near the fp32 bar: rel-L2 <= 2e-5 per token and <= 1e-5 in
+the mean (the construction -- exact integer codes, hi/lo activations, fp32
+scales -- measures 4e-6 to 1.05e-5 per token). The full T = 512 batch is
+checked against the per-token fp32 kernels of the same library (a
+size-independent consistency check) and on a sample of tokens against the
+oracle.
 """
 from __future__ import annotations
 
@@ -22,6 +25,8 @@ pytestmark = pytest.mark.gpu
 
 TOL_BF16 = 2e-3
 TOL_MEAN = 1e-4
+TOL_SMALL = 2e-5        # fewer than 64 tokens: per token
+TOL_SMALL_MEAN = 1e-5   # and in the mean
 
 
 def say(*a):
@@ -121,8 +126,8 @@ def test_grouped_other_formats_vs_oracle(torch_dev, ctx, mix):
             assert np.array_equal(idx[t], oi), t
             rels.append(cases.rel_l2(out[t], oo))
         say("rel-L2 max %.2e mean %.2e" % (max(rels), np.mean(rels)))
-        assert max(rels) <= TOL_BF16
-        assert np.mean(rels) <= TOL_MEAN
+        assert max(rels) <= TOL_SMALL
+        assert np.mean(rels) <= TOL_SMALL_MEAN
     finally:
         L.free()
 
@@ -146,8 +151,8 @@ def test_grouped_other_shape_vs_oracle(torch_dev, ctx):
             assert np.array_equal(idx[t], oi), t
             rels.append(cases.rel_l2(out[t], oo))
         say("rel-L2 max %.2e mean %.2e" % (max(rels), np.mean(rels)))
-        assert max(rels) <= TOL_BF16
-        assert np.mean(rels) <= TOL_MEAN
+        assert max(rels) <= TOL_SMALL
+        assert np.mean(rels) <= TOL_SMALL_MEAN
     finally:
         L.free()
 
@@ -187,7 +192,8 @@ def test_grouped_router_and_norm_vs_oracle(torch_dev, ctx):
             assert np.array_equal(idx[t], oi), t
             rels.append(cases.rel_l2(out[t], oo))
         assert ties <= 1
-        assert max(rels) <= TOL_BF16 and np.mean(rels) <= TOL_MEAN, (max(rels), np.mean(rels))
+        say("rel-L2 max %.2e mean %.2e" % (max(rels), np.mean(rels)))
+        assert max(rels) <= TOL_SMALL and np.mean(rels) <= TOL_SMALL_MEAN, (max(rels), np.mean(rels))
     finally:
         L.free()
 
@@ -226,7 +232,7 @@ def test_grouped_small_batch_vs_golden(torch_dev, ctx):
         out, idx, _ = run(torch_dev, ctx, L, xs, logits=lg, residual=res)
         for t in range(4):
             assert np.array_equal(idx[t], TG.G["prefill_t%d_idx" % t])
-            assert cases.rel_l2(out[t] - res[t], TG.G["prefill_t%d_out" % t]) <= TOL_BF16
+            assert cases.rel_l2(out[t] - res[t], TG.G["prefill_t%d_out" % t]) <= TOL_SMALL
     finally:
         L.free()
 
