@@ -80,6 +80,16 @@ def parse():
                          "MIB MiB read and written per launch)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="turn two rocprofv3 --pmc csv outputs (FETCH_SIZE, WRITE_SIZE) into the traffic summary")
+    ap.add_argument("--summarize-trace", nargs="+", metavar="PATH",
+                    help="TRACE_DIR BENCH_JSON [PLAIN_JSON]: split a rocprofv3 --kernel-trace "
+                         "csv of a decode workload run into the run's phases (BENCH_JSON: the "
+                         "line that run printed) and print per-kernel duration statistics for "
+                         "each phase as markdown, beside the line of the same command run "
+                         "without the profiler (PLAIN_JSON)")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="PMC_DIR",
+                    help="print the mean per dispatch of every counter in these rocprofv3 --pmc "
+                         "csv outputs for each k_moe_/k_pre_ kernel as markdown (FETCH_SIZE and "
+                         "WRITE_SIZE scaled by the --calib-copy copy kernel, when present)")
     ap.add_argument("--command", default="", help="command line recorded in the summary")
     return ap.parse_args()
 
@@ -147,6 +157,111 @@ def summarize_pmc(fetch_dir, write_dir, calib_mib, command):
         "command": command,
     }
     print(json.dumps(out, indent=1))
+
+
+def _short_kernel(name):
+    n = name.replace("void ", "").replace("(anonymous namespace)::", "")
+    return n.split("(")[0]
+
+
+def summarize_counters(dirs, calib_mib, command):
+    """Mean value per dispatch of each counter, per kernel of the path."""
+    rows = []
+    for d in dirs:
+        rows.extend(_pmc_rows(d))
+    counters = sorted(set(r["Counter_Name"] for r in rows))
+    table, calib = {}, {}
+    for c in counters:
+        for k, (v, n) in _per_kernel(rows, c).items():
+            if "MulFunctor" in k:
+                calib[c] = v
+                continue
+            if "k_moe_" not in k and "k_pre_" not in k:
+                continue
+            table.setdefault(_short_kernel(k), {})[c] = (v, n)
+    nbytes = calib_mib * 1024 * 1024
+    print("Command (repository root R):\n\n```\n%s\n```\n" % command)
+    print("Mean per dispatch; the dispatches each mean is over in parentheses.\n")
+    ks = sorted(table)
+    print("| Counter | " + " | ".join("`%s`" % k for k in ks) + " |")
+    print("|---|" + "---|" * len(ks))
+    for c in counters:
+        if c not in set().union(*[set(table[k]) for k in ks]):
+            continue
+        cells = []
+        for k in ks:
+            v = table[k].get(c)
+            cells.append("" if v is None else "%.0f (%d)" % v)
+        print("| %s | " % c + " | ".join(cells) + " |")
+    for c, what in (("FETCH_SIZE", "read"), ("WRITE_SIZE", "written")):
+        if c in calib and calib[c] > 0:
+            fac = nbytes / (calib[c] * 1024.0)
+            print("\n%s (KiB): the copy kernel that reads and writes %d MiB counts %.1f KiB "
+                  "-> factor %.4f; HBM bytes %s per launch:" % (c, calib_mib, calib[c], fac, what))
+            for k in sorted(table):
+                if c in table[k]:
+                    print("- `%s`: %.0f B" % (k, table[k][c][0] * 1024.0 * fac))
+
+
+def summarize_trace(trace_dir, bench_json, command, plain_json=None):
+    """Per-kernel duration statistics of a decode run's kernel trace, split
+    into the run's phases by dispatch order (bench_decode's dispatch_plan:
+    every layer step dispatches each of the three kernels once, in order)."""
+    import numpy as np
+    with open(bench_json) as fh:
+        line = [l for l in fh if l.startswith("{")][-1]
+    bj = json.loads(line)
+    plan = bj["dispatch_plan"]
+    files = glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise SystemExit("no kernel_trace.csv under %s" % trace_dir)
+    per = {}
+    for f in files:
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                name = r["Kernel_Name"]
+                if "k_moe_" not in name:
+                    continue
+                per.setdefault(name, []).append(
+                    (int(r["Start_Timestamp"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    total = sum(n for _, n in plan)
+    if len(per) != 3:
+        raise SystemExit("expected the three decode kernels, found %s" % sorted(per))
+    order = sorted(per, key=lambda k: min(t for t, _ in per[k]))
+    print("# Kernel durations of `%s` by phase (rocprofv3 kernel trace, %d dispatches per kernel)\n"
+          % (bj["config"]["workload"], total))
+    print("Command (repository root R):\n\n```\n%s\n```\n" % command)
+    print("| Kernel | Phase | Dispatches | Avg ns | Median ns | p10 ns | p90 ns |")
+    print("|---|---|---|---|---|---|---|")
+    for name in order:
+        d = sorted(per[name])
+        if len(d) != total:
+            raise SystemExit("%s: %d dispatches, the plan says %d" % (name, len(d), total))
+        durs = np.array([x for _, x in d], dtype=np.float64)
+        i = 0
+        for phase, n in plan:
+            seg = durs[i:i + n]
+            i += n
+            short = _short_kernel(name)
+            print("| `%s` | %s | %d | %.0f | %.0f | %.0f | %.0f |" % (
+                short, phase, n, seg.mean(), np.median(seg), np.percentile(seg, 10),
+                np.percentile(seg, 90)))
+    runs = [("the profiled run", bj)]
+    if plain_json:
+        with open(plain_json) as fh:
+            runs.insert(0, ("the same command without the profiler",
+                            json.loads([l for l in fh if l.startswith("{")][-1])))
+    for what, j in runs:
+        k = j["kernels"]
+        print("\nBench line of %s (HIP events around each kernel of the `profile` phase):" % what)
+        for kn in ("k_moe_router", "k_moe_gate_up", "k_moe_down"):
+            print("- `%s`: %.3f us, %d algorithmic bytes, %.1f GB/s" % (
+                kn, k[kn]["us"], k[kn]["bytes"], k[kn]["GBps"]))
+        sp = j.get("us_per_layer_spread") or {}
+        print("- layer (graph replays): median %s us, p10 %s, p90 %s over %s replays of %s layers"
+              % (sp.get("median"), sp.get("p10"), sp.get("p90"), sp.get("replays"),
+                 sp.get("layers_per_replay")))
+        print("- roofline: %s" % json.dumps(j["roofline"]))
 
 
 # ---- shared helpers ---------------------------------------------------------------
@@ -343,6 +458,14 @@ def bench_decode(torch, Q, S, ctx, pool, X, out, idx, args, profile=True):
                            "GBps": round(d_b / kus[2] / 1e3, 1)},
         }
         res["profiled_calls"] = calls
+    # the order in which this function dispatched layer steps (each step one
+    # launch of each of the three kernels), for splitting a kernel trace
+    plan = [("warmup", args.warmup), ("eager", K)]
+    if not args.no_graph:
+        plan += [("capture-call", K), ("replay-warmup", 2 * K), ("timed-replays", 20 * K)]
+    if profile:
+        plan.append(("profile", nprof))
+    res["dispatch_plan"] = plan
     return res
 
 
@@ -580,6 +703,15 @@ def main():
         summarize_pmc(args.summarize_pmc[0], args.summarize_pmc[1], args.calib_copy or 512,
                       args.command)
         return
+    if args.summarize_counters:
+        summarize_counters(args.summarize_counters, args.calib_copy or 512, args.command)
+        return
+    if args.summarize_trace:
+        st = args.summarize_trace
+        if len(st) not in (2, 3):
+            raise SystemExit("--summarize-trace takes TRACE_DIR BENCH_JSON [PLAIN_JSON]")
+        summarize_trace(st[0], st[1], args.command, st[2] if len(st) == 3 else None)
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU only: the MoE FFN path is benchmarked on a single "
               "MI355X; --gpus %d is not run (sharding is a design note, not a benchmark)."
@@ -714,6 +846,7 @@ def main():
         "bytes_per_step": res_main["bytes_per_step"],
         "eager_us_per_layer": res_main["eager_us_per_layer"],
         "kernels": res_main["kernels"],
+        "dispatch_plan": res_main["dispatch_plan"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
                      "traffic": traffic, "kernel": kname,
