@@ -793,6 +793,16 @@ def main():
         log("prefill iq: %s" % json.dumps(pf3))
         for L in pool3:
             L.free()
+        # batched layer of mixed per-expert formats (the decode IQ2_M mix):
+        # one grouped launch per down format
+        pool4 = [SynthLayer(ctx, 2600 + i, i, "iq2m") for i in range(2)]
+        pf4, _ = bench_prefill(torch, Q, S, ctx, pool4, args, with_t2=False,
+                               formats="IQ2_XXS gate/up, IQ3_S (even experts) / IQ2_S (odd) "
+                                       "down, Q4_K/Q6_K shared")
+        secondary["prefill_T%d_iq2m_mixed" % args.prefill_tokens] = pf4
+        log("prefill iq2m mixed: %s" % json.dumps(pf4))
+        for L in pool4:
+            L.free()
     if args.workload in ("all", "stack"):
         st = bench_stack(torch, Q, S, ctx, args)
         secondary["stack"] = st

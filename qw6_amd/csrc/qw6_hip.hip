@@ -16,7 +16,7 @@
 //                  meet in LDS and are combined in selection order, with the
 //                  residual -- no atomics, deterministic.
 // In the automatic mode, calls of 5 tokens or more take the grouped bf16-MFMA
-// kernels of qw6_prefill.hip when every matrix kind has one format; other
+// kernels of qw6_prefill.hip (one launch per expert format present); other
 // calls run in per-token launches of up to 4 tokens, 4 (and 3 for mixed
 // formats) on the small-batch MFMA kernels k_mx_*, fewer on the fp32 ones.
 // Routing never leaves the device (qw6's Vulkan path reads idx/w back to the
@@ -1694,6 +1694,7 @@ struct qw6_hip_experts_s {
     uint32_t rb_gu_max;   // widest gate/up row in bytes
     uint32_t rb_dn_max;   // widest down row in bytes
     int fmt_gu, fmt_dn;   // the single gate/up (down) format, -1 if mixed
+    uint32_t fmask_gu, fmask_dn;   // the formats present: bit f (bit 31: one the grouped path lacks)
     int xl_dn;            // a down format whose activation layout every expert's
                           // down format shares (the IQ formats share one), or -1
     int gu_same;          // every expert's gate and up share a format
@@ -2199,7 +2200,10 @@ int qw6_hip_experts_create(qw6_hip_ctx_t* c, const qw6_hip_matrix_t* gate,
     E->fmt_dn = tab[0].fmt[2];
     E->xl_dn = tab[0].fmt[2];
     E->gu_same = 1;
+    E->fmask_gu = E->fmask_dn = 0;
     for (uint32_t e = 0; e < n_experts; e++) {
+        E->fmask_gu |= prefill_supports(tab[e].fmt[0]) ? 1u << tab[e].fmt[0] : 1u << 31;
+        E->fmask_dn |= prefill_supports(tab[e].fmt[2]) ? 1u << tab[e].fmt[2] : 1u << 31;
         if (tab[e].fmt[0] != E->fmt_gu || tab[e].fmt[1] != E->fmt_gu) E->fmt_gu = -1;
         if (tab[e].fmt[2] != E->fmt_dn) E->fmt_dn = -1;
         if (E->xl_dn >= 0 && x_layout(tab[e].fmt[2]) != x_layout(E->xl_dn)) E->xl_dn = -1;
@@ -2296,6 +2300,10 @@ int ensure_prefill_ws(qw6_hip_ctx_t* c, uint32_t hidden, uint32_t inter, uint32_
     w.tiles = (uint4*)p;
     if (alloc_owned(c, 16, &p)) return -1;
     w.n_tiles = (uint32_t*)p;
+    if (alloc_owned(c, (size_t)2 * prefill_tiles_max(T, K8, 256) * 4, &p)) return -1;
+    w.forder = (uint32_t*)p;
+    if (alloc_owned(c, 2 * 8 * 2 * 4, &p)) return -1;
+    w.fseg = (uint32_t*)p;
     if (alloc_owned(c, (size_t)T * 256 * 4, &p)) return -1;
     w.logits = (float*)p;
     if (alloc_owned(c, (size_t)T * hidden * 4, &p)) return -1;
@@ -2469,17 +2477,16 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
         return fail("gate and up of each expert must share a quant type");
     DevGuard g(c->device);
     hipStream_t st = (hipStream_t)stream;
-    // batched tokens: grouped MFMA contraction when every matrix kind has one
-    // supported format (qw6_hip_set_mode: 0 automatic, 1 per-token, 2 grouped)
-    // (the shared expert's formats may differ from the routed experts')
-    const int fgu = E->fmt_gu, fdn = E->fmt_dn;
-    const bool grouped_ok = prefill_supports(fgu) && prefill_supports(fdn) &&
+    // batched tokens: grouped MFMA contraction when every expert matrix has a
+    // format the grouped kernels decode; one launch per format present
+    // (qw6_hip_set_mode: 0 automatic, 1 per-token, 2 grouped)
+    const bool grouped_ok = !((E->fmask_gu | E->fmask_dn) >> 31) &&
                             (!has_sh || (prefill_supports(sg.fmt) && prefill_supports(sd.fmt))) &&
                             L->hidden % 256 == 0 && L->inter % 256 == 0;
     if (noalloc && c->mode == 2)
         return fail("the grouped MFMA path needs context workspace: not available without allocation");
     if (c->mode == 2 && !grouped_ok)
-        return fail("grouped MFMA path needs one format per matrix kind across the routed experts");
+        return fail("grouped MFMA path: an expert matrix has a format the grouped kernels do not decode");
     if (!noalloc && grouped_ok && (c->mode == 2 || (c->mode == 0 && n_tok >= kGroupedMinTokens))) {
         if (ensure_prefill_ws(c, L->hidden, L->inter, E->n, L->top_k)) return -1;
         PrefillLayer P;
@@ -2491,7 +2498,7 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
         P.residual = residual; P.out = out; P.idx_out = idx; P.w_out = w;
         P.experts = E->dev;
         for (int k = 0; k < 3; k++) P.pk[k] = E->pk[k];
-        P.fmt_gu = fgu; P.fmt_dn = fdn;
+        P.fmask_gu = E->fmask_gu; P.fmask_dn = E->fmask_dn;
         P.sg = sg; P.su = su; P.sd = sd;
         return prefill_forward(P, c->pre, st);
     }

@@ -43,7 +43,9 @@ struct PrefillWs {
     float* ent_w;        // [E] gate weight of each entry
     uint32_t* ent_pos;   // [T][top_k] entry of (token, k)
     uint4* tiles;        // [n_tiles_max] {matrix id, first entry, count, 0}
-    uint32_t* n_tiles;   // [1]
+    uint32_t* n_tiles;   // [2] routed tiles, shared tiles
+    uint32_t* forder;    // [2][n_tiles_max] tile indices grouped by format (gate/up, down)
+    uint32_t* fseg;      // [2][8][2] {first, count} of each format's group in forder
     float* logits;       // [T][n_experts]
     float* xn;           // [T][hidden] (RMSNorm of the input)
     uint16_t* xh;        // [T][hidden] bf16 of the input
@@ -69,13 +71,20 @@ struct PrefillLayer {
     float* w_out;
     const ExpertEnt* experts;
     PackRef pk[3];
-    int fmt_gu, fmt_dn;           // one format per matrix kind
+    uint32_t fmask_gu, fmask_dn;  // formats of the routed experts' gate/up (down): bit f
     MatD sg, su, sd;              // shared expert (sg.p == nullptr: none)
 };
 
 // Entries of a batch of T tokens: T * top_k routed, then T shared.
 inline uint32_t prefill_entries(uint32_t T, uint32_t top_k) { return T * top_k + T; }
-uint32_t prefill_tiles_max(uint32_t T, uint32_t top_k, uint32_t n_experts);
+// Entries per tile of the grouped kernels (one MFMA row group).
+constexpr uint32_t kPrefillTileEntries = 16;
+// Tiles of a batch at most: the routed entries in tiles of one expert each
+// (at most one partial tile per expert), then the shared expert's.
+__host__ __device__ inline uint32_t prefill_tiles_max(uint32_t T, uint32_t top_k, uint32_t n_experts) {
+    const uint32_t m = kPrefillTileEntries;
+    return (T * top_k + m - 1) / m + n_experts + (T + m - 1) / m;
+}
 // Formats the grouped kernels decode (others take the per-token kernels).
 bool prefill_supports(int fmt);
 // Launch the batched MoE FFN on `st`; 0 or -1 (message via qw6_fail).

@@ -8,9 +8,12 @@
 //   k_pre_route   one wave per token: softmax top-k (wave_route), the
 //                 shared-expert weight, the shared entries.
 //   k_pre_sort    one workgroup: counting sort of the (token, k) pairs by
-//                 expert into "entries", and a tile list of <= 16 entries of
-//                 one expert (the shared expert last, with every token).
-//   k_pre_gemm<0> gate and up for 128 intermediate rows of one tile (64
+//                 expert into "entries", a tile list of <= 16 entries of
+//                 one expert (the shared expert last, with every token), and
+//                 the tiles grouped by the format of their gate/up and of
+//                 their down matrix (experts may differ in format).
+//   k_pre_gemm<0, F> (one launch per format F present)
+//                 gate and up for 128 intermediate rows of one tile (64
 //                 for Q6_K and IQ3_S): mid[entry] = silu(x.gate) * (x.up).
 //   k_pre_gemm<1> down for 256 hidden rows of one tile (128 for Q6_K and
 //                 IQ3_S), times the entry's gate weight -> ybuf[entry].
@@ -44,7 +47,7 @@ namespace {
 
 __device__ const IqTables g_tabs_pre = make_tables();
 
-constexpr uint32_t kPM = 16;      // entries per tile (one MFMA row group)
+constexpr uint32_t kPM = kPrefillTileEntries;   // entries per tile (one MFMA row group)
 constexpr uint32_t kPWG = 256;    // threads per workgroup (4 waves)
 
 // Eight floats -> bf16 hi and lo parts (hi = bf16(x), lo = bf16(x - hi)), packed
@@ -170,6 +173,62 @@ __global__ __launch_bounds__(1024) void k_pre_sort(PrefillLayer L, PrefillWs ws)
     if (tid == 0) {
         ws.n_tiles[0] = nrt;
         ws.n_tiles[1] = nsh;
+    }
+    // The tiles grouped by the format of their matrix, per matrix kind (wave
+    // k: 0 gate/up, 1 down), each group in tile order (the tiles of one
+    // expert stay together): one grouped launch per format present.
+    // Experts (and last the shared one) go 64 to a round, lane l expert
+    // 64 r + l; a wave scan per format places its tiles.
+    const uint32_t wave = tid >> 6, lane = tid & 63u;
+    if (wave < 2) {
+        const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
+        const int k = wave == 0 ? 0 : 2;
+        uint32_t* order = ws.forder + (size_t)wave * cap;
+        uint32_t base[F_NFMT];
+#pragma unroll
+        for (int f = 0; f < F_NFMT; f++) base[f] = 0;
+        // two passes: counts (the group sizes and starts), then placement
+        for (int pass = 0; pass < 2; pass++) {
+            uint32_t start[F_NFMT];
+            if (pass == 1) {
+                uint32_t run = 0;
+#pragma unroll
+                for (int f = 0; f < F_NFMT; f++) { start[f] = run; run += base[f]; }
+                if (lane < F_NFMT) {
+                    ws.fseg[(wave * 8 + lane) * 2 + 0] = start[lane];
+                    ws.fseg[(wave * 8 + lane) * 2 + 1] = base[lane];
+                }
+#pragma unroll
+                for (int f = 0; f < F_NFMT; f++) base[f] = start[f];
+            }
+            for (uint32_t e0 = 0; e0 <= E; e0 += 64) {
+                const uint32_t e = e0 + lane;
+                uint32_t nt = 0, t0 = 0;
+                int f = 0;
+                if (e < E) {
+                    nt = (cnt[e] + kPM - 1) / kPM;
+                    t0 = tof[e];
+                    f = L.pk[k].regular ? L.pk[k].fmt : L.experts[e].fmt[k];
+                } else if (e == E) {
+                    nt = nsh;
+                    t0 = nrt;
+                    f = k == 0 ? L.sg.fmt : L.sd.fmt;
+                }
+#pragma unroll
+                for (int g = 0; g < F_NFMT; g++) {
+                    const uint32_t mine = f == g ? nt : 0u;
+                    uint32_t incl = mine;   // inclusive scan over the lanes
+#pragma unroll
+                    for (int d = 1; d < 64; d <<= 1) {
+                        const uint32_t o = __shfl_up(incl, d);
+                        if (lane >= (uint32_t)d) incl += o;
+                    }
+                    if (pass == 1 && mine)
+                        for (uint32_t i = 0; i < mine; i++) order[base[g] + incl - mine + i] = t0 + i;
+                    base[g] += __shfl(incl, 63);
+                }
+            }
+        }
     }
 }
 
@@ -317,16 +376,14 @@ __device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NP],
 // Software pipeline over the 256-column blocks: the raw weight bytes and the
 // A operands of block kb + 1 are loaded into registers while block kb is
 // multiplied, then written to LDS between two barriers.
-// sel: the tiles of the routed experts (0), of the shared expert (1), or both
-// (2); the shared expert's tiles follow the routed ones in the tile list.
+// The launch for format F takes the tiles of F's group (ws.forder, ws.fseg).
 template <int MODE, int F>
 __host__ __device__ constexpr int gemm_min_blocks() {   // workgroups per CU
     return F == F_Q4K ? 3 : 2;   // Q4_K: 52 KB of LDS each, three fit in 160 KB
 }
 
 template <int MODE, int F>
-__global__ __launch_bounds__(kPWG, (gemm_min_blocks<MODE, F>())) void k_pre_gemm(PrefillLayer L, PrefillWs ws,
-                                                                               uint32_t sel) {
+__global__ __launch_bounds__(kPWG, (gemm_min_blocks<MODE, F>())) void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
     constexpr int RT = gemm_rt<MODE, F>();
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     GemmLds& S = *(GemmLds*)smem;
@@ -335,15 +392,16 @@ __global__ __launch_bounds__(kPWG, (gemm_min_blocks<MODE, F>())) void k_pre_gemm
     // block) items -- the row blocks of one tile (same A rows) and the tiles of
     // one expert (same weights) then share that XCD's L2.
     const uint32_t ny = MODE == 0 ? L.inter / (32 * RT) : L.hidden / (64 * RT);
-    const uint32_t t_first = sel == 1 ? ws.n_tiles[0] : 0u;
-    const uint32_t n_t = sel == 0 ? ws.n_tiles[0] : sel == 1 ? ws.n_tiles[1] : ws.n_tiles[0] + ws.n_tiles[1];
+    const uint32_t g_first = ws.fseg[(MODE * 8 + F) * 2 + 0];
+    const uint32_t n_t = ws.fseg[(MODE * 8 + F) * 2 + 1];
     const uint32_t total = n_t * ny;
     const uint32_t per_xcd = (total + 7) / 8;
     const uint32_t slot = blockIdx.x / 8;
     const uint32_t item = (blockIdx.x % 8) * per_xcd + slot;
     if (slot >= per_xcd || item >= total) return;
     const uint32_t ti = item / ny, yb = item % ny;
-    const uint4 tile = ws.tiles[t_first + ti];
+    const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
+    const uint4 tile = ws.tiles[ws.forder[(size_t)MODE * cap + g_first + ti]];
     const uint32_t mid_e = tile.x, ent0 = tile.y, cnt = tile.z;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
     const uint32_t n = lane & 15u, q = lane >> 4;
@@ -581,56 +639,45 @@ __global__ __launch_bounds__(64) void k_pre_router(const float* __restrict__ rou
 }
 
 template <int MODE, int F>
-void launch_gemm_f(const PrefillLayer& L, const PrefillWs& ws, uint32_t cap, uint32_t sel,
-                   hipStream_t st) {
+void launch_gemm_f(const PrefillLayer& L, const PrefillWs& ws, uint32_t cap, hipStream_t st) {
     constexpr int RT = gemm_rt<MODE, F>();
     const size_t lds = offsetof(GemmLds, raw) + (size_t)64 * RT * raw_chunks(F) * 16 + iq_tab_bytes(F);
     const uint32_t ny = MODE == 0 ? L.inter / (32 * RT) : L.hidden / (64 * RT);
-    // cap tiles at most; the kernel maps workgroups to the actual items
+    // cap tiles at most; the kernel maps workgroups to its format's items
     const uint32_t nwg = (cap * ny + 7) / 8 * 8;
-    k_pre_gemm<MODE, F><<<nwg, kPWG, lds, st>>>(L, ws, sel);
+    k_pre_gemm<MODE, F><<<nwg, kPWG, lds, st>>>(L, ws);
 }
 
+// One launch per format in `mask` (the routed experts' formats of this
+// matrix kind and the shared expert's), each over its format's tiles.
 template <int MODE>
-int launch_gemm_sel(int f, const PrefillLayer& L, const PrefillWs& ws, uint32_t cap, uint32_t sel,
-                    hipStream_t st) {
-    switch (f) {
-    case F_Q4K: launch_gemm_f<MODE, F_Q4K>(L, ws, cap, sel, st); break;
-    case F_Q5K: launch_gemm_f<MODE, F_Q5K>(L, ws, cap, sel, st); break;
-    case F_Q6K: launch_gemm_f<MODE, F_Q6K>(L, ws, cap, sel, st); break;
-    case F_IQ2XXS: launch_gemm_f<MODE, F_IQ2XXS>(L, ws, cap, sel, st); break;
-    case F_IQ2S: launch_gemm_f<MODE, F_IQ2S>(L, ws, cap, sel, st); break;
-    case F_IQ3S: launch_gemm_f<MODE, F_IQ3S>(L, ws, cap, sel, st); break;
-    default: return qw6_fail("batched path: unsupported weight format %d", f);
+int launch_gemm(uint32_t mask, const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) {
+    const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
+    for (int f = 0; f < F_NFMT; f++) {
+        if (!((mask >> f) & 1u)) continue;
+        switch (f) {
+        case F_Q4K: launch_gemm_f<MODE, F_Q4K>(L, ws, cap, st); break;
+        case F_Q5K: launch_gemm_f<MODE, F_Q5K>(L, ws, cap, st); break;
+        case F_Q6K: launch_gemm_f<MODE, F_Q6K>(L, ws, cap, st); break;
+        case F_IQ2XXS: launch_gemm_f<MODE, F_IQ2XXS>(L, ws, cap, st); break;
+        case F_IQ2S: launch_gemm_f<MODE, F_IQ2S>(L, ws, cap, st); break;
+        default: launch_gemm_f<MODE, F_IQ3S>(L, ws, cap, st); break;
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return qw6_fail("batched kernel launch: %s", hipGetErrorString(e));
     }
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return qw6_fail("batched kernel launch: %s", hipGetErrorString(e));
     return 0;
 }
 
-// The routed experts' tiles with their format f; the shared expert's with
-// its own format fs (one launch when the formats agree).
-template <int MODE>
-int launch_gemm(int f, int fs, const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) {
-    const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
-    const uint32_t cap_sh = (L.T + kPM - 1) / kPM;
-    if (!L.sg.p || fs == f) return launch_gemm_sel<MODE>(f, L, ws, cap, 2, st);
-    if (launch_gemm_sel<MODE>(f, L, ws, cap, 0, st)) return -1;
-    return launch_gemm_sel<MODE>(fs, L, ws, cap_sh, 1, st);
-}
-
 }  // namespace
-
-uint32_t prefill_tiles_max(uint32_t T, uint32_t top_k, uint32_t n_experts) {
-    return (T * top_k + kPM - 1) / kPM + n_experts + (T + kPM - 1) / kPM;
-}
 
 bool prefill_supports(int f) { return f >= F_Q4K && f <= F_IQ3S; }
 
 int prefill_forward(const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) {
     if (L.hidden % 256 || L.inter % 256)
         return qw6_fail("batched path needs hidden, inter multiples of 256");
-    if (!prefill_supports(L.fmt_gu) || !prefill_supports(L.fmt_dn) ||
+    const uint32_t all = (1u << F_NFMT) - 1u;
+    if (!L.fmask_gu || !L.fmask_dn || (L.fmask_gu & ~all) || (L.fmask_dn & ~all) ||
         (L.sg.p && (!prefill_supports(L.sg.fmt) || !prefill_supports(L.sd.fmt) ||
                     L.su.fmt != L.sg.fmt)))
         return qw6_fail("batched path: unsupported expert format");
@@ -659,8 +706,10 @@ int prefill_forward(const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) 
     k_pre_sort<<<1, 1024, 0, st>>>(Lx, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return qw6_fail("batched routing launch: %s", hipGetErrorString(e));
-    if (launch_gemm<0>(L.fmt_gu, L.sg.fmt, Lx, ws, st)) return -1;
-    if (launch_gemm<1>(L.fmt_dn, L.sd.fmt, Lx, ws, st)) return -1;
+    const uint32_t m_gu = L.fmask_gu | (L.sg.p ? 1u << L.sg.fmt : 0u);
+    const uint32_t m_dn = L.fmask_dn | (L.sg.p ? 1u << L.sd.fmt : 0u);
+    if (launch_gemm<0>(m_gu, Lx, ws, st)) return -1;
+    if (launch_gemm<1>(m_dn, Lx, ws, st)) return -1;
     k_pre_combine<<<dim3(L.T, (L.hidden / 4 + 255) / 256), 256, 0, st>>>(Lx, ws);
     e = hipGetLastError();
     if (e != hipSuccess) return qw6_fail("batched combine launch: %s", hipGetErrorString(e));

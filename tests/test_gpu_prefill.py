@@ -219,6 +219,51 @@ def test_grouped_full_batch_vs_per_token_kernels_and_oracle(torch_dev, ctx, laye
         assert cases.rel_l2(d_out[t], oo) <= 1e-5
 
 
+def test_grouped_mixed_formats_vs_oracle(torch_dev, ctx):
+    """Experts of different formats in one layer (qw6.h:160-162): IQ2_XXS
+    gate/up, IQ3_S downs for even and IQ2_S downs for odd experts, shared
+    expert Q4_K / Q6_K -- the down contraction runs as one grouped launch per
+    format (IQ3_S, IQ2_S, Q6_K). T = 64 against the oracle; T = 512 against
+    the fp32 per-token kernels for every token and the oracle on a sample."""
+    from qw6_amd.workload import SynthLayer
+    L = SynthLayer(ctx, 66, 0, "iq2m")
+    try:
+        T = 64
+        lg = S.zipf_logits(66, T)
+        xs = np.stack([cases.token_x(66, 1, t) for t in range(T)])
+        res = np.stack([cases.token_x(66, 2, t) for t in range(T)])
+        say("mixed formats grouped T=%d" % T)
+        out, idx, w = run(torch_dev, ctx, L, xs, logits=lg, residual=res)
+        want = oracle_tokens(L, xs, lg, range(T))
+        rels = []
+        for t in range(T):
+            oo, oi, ow = want[t]
+            assert np.array_equal(idx[t], oi), t
+            assert np.abs(w[t] - ow).max() <= 2e-5
+            rels.append(cases.rel_l2(out[t] - res[t], oo))
+        say("rel-L2 max %.2e mean %.2e" % (max(rels), np.mean(rels)))
+        assert max(rels) <= TOL_BF16 and np.mean(rels) <= TOL_MEAN
+        T = 512
+        lg = S.zipf_logits(67, T)
+        xs = np.stack([cases.token_x(67, 3, t) for t in range(T)])
+        say("mixed formats grouped T=%d" % T)
+        g_out, g_idx, _ = run(torch_dev, ctx, L, xs, logits=lg, mode=2)
+        d_out, d_idx, _ = run(torch_dev, ctx, L, xs, logits=lg, mode=1)
+        assert np.array_equal(g_idx, d_idx)
+        rels = [cases.rel_l2(g_out[t], d_out[t]) for t in range(T)]
+        say("T=512 mixed grouped vs per-token: max %.2e mean %.2e" % (max(rels), np.mean(rels)))
+        assert max(rels) <= TOL_BF16 and np.mean(rels) <= TOL_MEAN
+        sample = [0, 5, 131, 300, 511]
+        want = oracle_tokens(L, xs, lg, sample)
+        for t in sample:
+            oo, oi, _ = want[t]
+            assert np.array_equal(g_idx[t], oi)
+            assert cases.rel_l2(g_out[t], oo) <= TOL_BF16
+            assert cases.rel_l2(d_out[t], oo) <= 1e-5
+    finally:
+        L.free()
+
+
 def test_grouped_small_batch_vs_golden(torch_dev, ctx):
     """The 4-token golden fixture (qw6's own layer on Zipf logits, with a
     residual) through the grouped kernels."""
