@@ -923,6 +923,83 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
     }
 }
 
+// One token, every gate/up pair of the layer in each workgroup: workgroup b
+// takes rows [b R, (b + 1) R) (R = 2 rps, two row steps) of every selected
+// expert and of the shared one. Wave w < top_k works on the expert of rank w
+// (slot w), which it selects itself from the logits (no barrier); in
+// workgroup 0, wave 0 runs the full routing instead and publishes the
+// selection and the slot table. Wave top_k (when present) streams the shared
+// expert from the start. Every workgroup moves the same bytes and there is
+// one per row tile: at hidden 2048 / inter 512, 256 workgroups of 9 waves,
+// one per CU (the 4-wave layout of k_moe_gate_up puts 576 workgroups on the
+// 256 CUs, three on a quarter of them).
+template <int FG, int KU>
+__global__ __launch_bounds__(64 * 9) void k_moe_gate_up1(MoeArgs a) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    __shared__ uint32_t s_idx[8];
+    __shared__ float s_w[8];
+    __shared__ uint2 s_route[8 * kRouteScr];   // one per routed wave
+    constexpr int S = gu_steps<1>();
+    constexpr uint32_t rps = 64 / KU;
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const bool shared_w = wave >= a.top_k;
+    const uint32_t toff = tab_bytes(a.tmask_gu);
+    const uint32_t slot_off = toff + wave * S * a.gu_pb;
+    // the logits load is a routed wave's first memory operation; every wave
+    // then stages its share of the lattice tables
+    uint32_t keys[4];
+    if (!shared_w) route_keys(a.route_logits, a.n_experts, keys);
+    stage_tables_from(smem, a.tmask_gu, 0);
+    const bool bar = a.tmask_gu != 0;   // wave_gate_up waits for them, then meets the others
+    MatD G, Up;
+    float* midp;
+    if (shared_w) {
+        G = a.sg;
+        Up = a.su;
+        midp = a.mid + (size_t)a.max_u * a.inter;
+    } else {
+        uint32_t e;
+        if (blockIdx.x == 0 && wave == 0) {
+            // publish the routing and the slot table for k_moe_down (one
+            // token: the slots are the selection itself)
+            wave_route_keys(keys, a.top_k, s_route, s_idx, s_w);
+            __builtin_amdgcn_wave_barrier();
+            if (lane < a.top_k) {
+                if (a.idx_out) a.idx_out[lane] = s_idx[lane];
+                if (a.w_out) a.w_out[lane] = s_w[lane];
+                SlotTable* st = a.slots;
+                const MatD D = expert_mat(a, s_idx[lane], 2);
+                st->p[lane] = D.p; st->fmt[lane] = D.fmt; st->rb[lane] = D.rb;
+                st->wt[lane][0] = s_w[lane];
+#pragma unroll
+                for (uint32_t t = 1; t < kMaxTok; t++) st->wt[lane][t] = 0.f;
+            }
+            if (lane == 0) a.slots->n = a.top_k;
+            e = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_idx[0]);
+        } else {
+            e = wave_route_select(keys, a.top_k, wave, s_route + wave * kRouteScr);
+        }
+        G = expert_mat_wave(a, e, 0);
+        Up = expert_mat_wave(a, e, 1);
+        midp = a.mid + (size_t)wave * a.inter;
+    }
+    const uint32_t row0 = blockIdx.x * S * rps;
+    const uint32_t* lds = (const uint32_t*)smem;
+    uint8_t* wslots = smem + slot_off;
+    if (FG >= 0) {
+        wave_gate_up<1, FG, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds);
+        return;
+    }
+    switch (G.fmt) {   // mixed formats: one switch per wave, each body specialised
+    case F_Q4K: wave_gate_up<1, F_Q4K, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_Q5K: wave_gate_up<1, F_Q5K, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_Q6K: wave_gate_up<1, F_Q6K, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_IQ2XXS: wave_gate_up<1, F_IQ2XXS, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    case F_IQ2S: wave_gate_up<1, F_IQ2S, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    default: wave_gate_up<1, F_IQ3S, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
+    }
+}
+
 // Down projection + combine for rows [r0, r0 + R), R = S * rps. Matrix m of
 // the block: m = 0 the shared expert (when present; no routing needed, so
 // its wave starts streaming at once), then the slots in first-use order.
@@ -2347,7 +2424,10 @@ int launch_k(void (*kern)(Args...), uint32_t grid, uint32_t block, size_t lds, h
 struct MoeLaunch {
     bool router;             // k_moe_router runs
     bool mx;                 // the small-batch MFMA kernels (k_mx_*)
+    bool gu1;                // one token: k_moe_gate_up1 (every matrix pair per workgroup)
     uint32_t grid_r;
+    uint32_t grid_b1, nw_b1;
+    size_t lds_b1;
     int fg, fd;              // format of the gate/up (down) kernels, -1: mixed
     size_t lds_b, lds_c;
     uint32_t grid_b, grid_c, nw_b, nw_c;
@@ -2419,10 +2499,17 @@ int launch_moe(const MoeArgs& a, const MoeLaunch& m, hipStream_t st, hipEvent_t*
         }
         return rc;
     }
-    launch_expert_kernel<64>(m.fg, a.T, a.hidden / 32, [&](auto tc, auto fc, auto kc) {
-        rc = launch_k(k_moe_gate_up<decltype(tc)::value, decltype(fc)::value, decltype(kc)::value>,
-                      m.grid_b, kWG, m.lds_b, st, ev ? ev + 2 : nullptr, a);
-    });
+    if (m.gu1) {
+        launch_expert_kernel<64>(m.fg, 1, a.hidden / 32, [&](auto, auto fc, auto kc) {
+            rc = launch_k(k_moe_gate_up1<decltype(fc)::value, decltype(kc)::value>, m.grid_b1,
+                          64 * m.nw_b1, m.lds_b1, st, ev ? ev + 2 : nullptr, a);
+        });
+    } else {
+        launch_expert_kernel<64>(m.fg, a.T, a.hidden / 32, [&](auto tc, auto fc, auto kc) {
+            rc = launch_k(k_moe_gate_up<decltype(tc)::value, decltype(fc)::value, decltype(kc)::value>,
+                          m.grid_b, kWG, m.lds_b, st, ev ? ev + 2 : nullptr, a);
+        });
+    }
     if (rc) return rc;
     launch_expert_kernel<16>(m.fd, a.T, a.inter / 32, [&](auto tc, auto fc, auto kc) {
         rc = launch_k(k_moe_down<decltype(tc)::value, decltype(fc)::value, decltype(kc)::value>,
@@ -2593,6 +2680,13 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
         a.idx_out = idx ? idx + (size_t)t0 * L->top_k : nullptr;
         a.w_out = w ? w + (size_t)t0 * L->top_k : nullptr;
         m.grid_b = a.n_sh_wg + a.max_u * ntile_b;
+        // one token: every matrix pair in each workgroup, one workgroup per
+        // two row steps (k_moe_gate_up1)
+        m.gu1 = T == 1;
+        m.nw_b1 = L->top_k + (has_sh ? 1u : 0u);
+        m.grid_b1 = (L->inter + S * rpsg - 1) / (S * rpsg);
+        m.lds_b1 = (size_t)tab_bytes(mgu) + (size_t)m.nw_b1 * S * a.gu_pb;
+        if (m.gu1 && m.lds_b1 > kMxLdsBudget) m.gu1 = false;
         const uint32_t ntot = a.max_u + (has_sh ? 1u : 0u);
         const uint32_t nw_max = T == 1 ? down_waves<1>() : T == 2 ? down_waves<2>() : down_waves<3>();
         m.nw_c = ntot < nw_max ? ntot : nw_max;
