@@ -139,12 +139,12 @@ def summarize_pmc(fetch_dir, write_dir, calib_mib, command):
     ck_w = pick(w, "MulFunctor")
     fac_f = nbytes / (f[ck_f][0] * 1024.0)
     fac_w = nbytes / (w[ck_w][0] * 1024.0)
-    gu_f = pick(f, "k_moe_gate_up")
-    gu_w = pick(w, "k_moe_gate_up")
+    gu_f = pick(f, "k_moe_gate_up1")
+    gu_w = pick(w, "k_moe_gate_up1")
     fetch = f[gu_f][0] * 1024.0 * fac_f
     write = w[gu_w][0] * 1024.0 * fac_w
     out = {
-        "kernel": "k_moe_gate_up",
+        "kernel": "k_moe_gate_up1",
         "workload": "decode layer, batch 1, Q4_K gate/up + Q6_K down, F32 router, shared expert",
         "fetch_bytes_per_launch": round(fetch),
         "write_bytes_per_launch": round(write),
@@ -254,7 +254,7 @@ def summarize_trace(trace_dir, bench_json, command, plain_json=None):
     for what, j in runs:
         k = j["kernels"]
         print("\nBench line of %s (HIP events around each kernel of the `profile` phase):" % what)
-        for kn in ("k_moe_router", "k_moe_gate_up", "k_moe_down"):
+        for kn in ("k_moe_router", "k_moe_gate_up1", "k_moe_down"):
             print("- `%s`: %.3f us, %d algorithmic bytes, %.1f GB/s" % (
                 kn, k[kn]["us"], k[kn]["bytes"], k[kn]["GBps"]))
         sp = j.get("us_per_layer_spread") or {}
@@ -452,7 +452,7 @@ def bench_decode(torch, Q, S, ctx, pool, X, out, idx, args, profile=True):
         res["kernels"] = {
             "k_moe_router": {"us": round(kus[0], 3), "bytes": int(r_b),
                              "GBps": round(r_b / kus[0] / 1e3, 1)},
-            "k_moe_gate_up": {"us": round(kus[1], 3), "bytes": int(gu_b),
+            "k_moe_gate_up1": {"us": round(kus[1], 3), "bytes": int(gu_b),
                               "GBps": round(gu_b / kus[1] / 1e3, 1)},
             "k_moe_down": {"us": round(kus[2], 3), "bytes": int(d_b),
                            "GBps": round(d_b / kus[2] / 1e3, 1)},
@@ -821,7 +821,7 @@ def main():
         ctx.close()
         return
 
-    kname = "k_moe_gate_up"
+    kname = "k_moe_gate_up1"   # the gate/up kernel of one-token launches
     gk = res_main["kernels"][kname]
     achieved = gk["GBps"]
     traffic = None
