@@ -58,6 +58,14 @@ HIDDEN, INTER, N_EXPERTS, TOP_K = 2048, 512, 256, 8
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "moe_gate_up_q4k_decode_traffic.json")
 
 
+# --prefill-mix layer kinds and the formats they hold
+PREFILL_FORMATS = {
+    "q4k": "Q4_K gate/up, Q6_K down",
+    "iq2a": "IQ2_XXS gate/up, IQ3_S down, Q4_K/Q6_K shared",
+    "iq2m": "IQ2_XXS gate/up, IQ3_S (even experts) / IQ2_S (odd) down, Q4_K/Q6_K shared",
+}
+
+
 def parse():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -68,6 +76,10 @@ def parse():
                     choices=["all", "q4k", "iq2m", "stack", "prefill", "head", "floor", "gguf"])
     ap.add_argument("--stack-steps", type=int, default=128)
     ap.add_argument("--prefill-tokens", type=int, default=512)
+    ap.add_argument("--prefill-mix", default="q4k", choices=sorted(PREFILL_FORMATS),
+                    help="with --workload prefill: the layer formats (q4k: Q4_K gate/up, Q6_K "
+                         "down; iq2a: IQ2_XXS gate/up, IQ3_S down; iq2m: IQ2_XXS gate/up, "
+                         "IQ3_S / IQ2_S downs by expert)")
     ap.add_argument("--no-small-batch", action="store_true",
                     help="with --workload prefill: time the prefill_T512 case only (no T=2 and "
                          "small-batch cases), for a kernel profile of that workload alone")
@@ -605,7 +617,7 @@ def bench_stack(torch, Q, S, ctx, args):
 
 
 def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
-                  formats="Q4_K gate/up, Q6_K down"):
+                  formats=PREFILL_FORMATS["q4k"]):
     """T tokens with Zipf-skewed logits through the grouped MFMA kernels, plus
     (with_t2) the T=2 MTP case through the per-token kernels with the router
     GEMV."""
@@ -735,11 +747,14 @@ def main():
     want_prefill = args.workload in ("all", "prefill")
     ctx = Q.Context(0, max_tokens=args.prefill_tokens if want_prefill else 4)
     P = args.pool
-    mix = "iq2m" if args.workload == "iq2m" else "q4k"
+    mix = ("iq2m" if args.workload == "iq2m" else
+           args.prefill_mix if args.workload == "prefill" else "q4k")
     secondary = {}
     res_main = None
     pool = []
     if args.workload in ("all", "q4k", "iq2m", "prefill", "gguf"):
+        if args.workload == "prefill":
+            P = 2   # the prefill figure alternates two layers
         log("building %d synthetic layers (%s)" % (P, mix))
         pool = [SynthLayer(ctx, 1000 + i, i, mix) for i in range(P)]
         X = torch.empty(P, HIDDEN, dtype=torch.float32, device="cuda")
@@ -752,8 +767,10 @@ def main():
             res_main = bench_decode(torch, Q, S, ctx, pool, X, out, idx, args)
             log("decode %s: %s" % (mix, json.dumps(res_main)))
     if want_prefill:
-        pf, t2 = bench_prefill(torch, Q, S, ctx, pool, args, with_t2=not args.no_small_batch)
-        secondary["prefill_T%d" % args.prefill_tokens] = pf
+        pf, t2 = bench_prefill(torch, Q, S, ctx, pool, args,
+                               with_t2=not args.no_small_batch and mix == "q4k",
+                               formats=PREFILL_FORMATS[mix])
+        secondary["prefill_T%d%s" % (args.prefill_tokens, "" if mix == "q4k" else "_" + mix)] = pf
         log("prefill: %s" % json.dumps(pf))
         if t2 is not None:
             secondary["mtp_T2"] = t2
@@ -788,7 +805,7 @@ def main():
         # batched IQ layer: one IQ format per matrix kind, as in a GGUF expert pack
         pool3 = [SynthLayer(ctx, 2500 + i, i, "iq2a") for i in range(2)]
         pf3, _ = bench_prefill(torch, Q, S, ctx, pool3, args, with_t2=False,
-                               formats="IQ2_XXS gate/up, IQ3_S down, Q4_K/Q6_K shared")
+                               formats=PREFILL_FORMATS["iq2a"])
         secondary["prefill_T%d_iq2xxs_iq3s" % args.prefill_tokens] = pf3
         log("prefill iq: %s" % json.dumps(pf3))
         for L in pool3:
@@ -797,8 +814,7 @@ def main():
         # one grouped launch per down format
         pool4 = [SynthLayer(ctx, 2600 + i, i, "iq2m") for i in range(2)]
         pf4, _ = bench_prefill(torch, Q, S, ctx, pool4, args, with_t2=False,
-                               formats="IQ2_XXS gate/up, IQ3_S (even experts) / IQ2_S (odd) "
-                                       "down, Q4_K/Q6_K shared")
+                               formats=PREFILL_FORMATS["iq2m"])
         secondary["prefill_T%d_iq2m_mixed" % args.prefill_tokens] = pf4
         log("prefill iq2m mixed: %s" % json.dumps(pf4))
         for L in pool4:

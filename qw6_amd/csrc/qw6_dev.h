@@ -536,6 +536,21 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave, without LDS traffic:
+// Hillis-Steele steps 1, 2, 4, 8 inside each 16-lane row (DPP row_shr:n;
+// lanes with no source n places back in their row add 0), then each row adds
+// the totals of the rows before it (lanes 15, 31, 47 read as scalars).
+__device__ __forceinline__ uint32_t wave_scan_incl(uint32_t v, uint32_t lane) {
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x111, 0xf, 0xf, false);   // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x112, 0xf, 0xf, false);   // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x114, 0xf, 0xf, false);   // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0u, v, 0x118, 0xf, 0xf, false);   // row_shr:8
+    const uint32_t t0 = __builtin_amdgcn_readlane(v, 15), t1 = __builtin_amdgcn_readlane(v, 31),
+                   t2 = __builtin_amdgcn_readlane(v, 47);
+    const uint32_t row = lane >> 4;
+    return v + (row >= 1 ? t0 : 0u) + (row >= 2 ? t1 : 0u) + (row >= 3 ? t2 : 0u);
+}
+
 // Reduce-scatter: each lane holds S partial sums v[0..S) (one per row step)
 // of a group of G lanes (S <= G). Returns the full group sum of step
 // s = (lane & (G-1)) >> log2(G/S); all lanes of each G/S sub-group get it.

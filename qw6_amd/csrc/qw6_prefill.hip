@@ -127,11 +127,41 @@ __global__ __launch_bounds__(64) void k_pre_route(PrefillLayer L, PrefillWs ws,
 // and the combine sums in (token, k) order).
 __global__ __launch_bounds__(1024) void k_pre_sort(PrefillLayer L, PrefillWs ws) {
     __shared__ uint32_t cnt[257], off[257], cur[257], tof[257];
-    const uint32_t tid = threadIdx.x;
+    __shared__ uint8_t efmt[2][257];   // gate/up and down format per expert, the shared one last
+    const uint32_t tid = threadIdx.x, nthr = blockDim.x;
     const uint32_t ne = L.T * L.top_k, E = L.n_experts;
-    for (uint32_t e = tid; e <= E; e += blockDim.x) cnt[e] = 0;
+    // Every global load a thread needs goes out before its first wait: its
+    // PT (token, k) pairs' experts and gate weights, and (expert tid) the
+    // formats of expert tid's matrices. Layers beyond PT pairs per thread
+    // reload per chunk.
+    constexpr uint32_t PT = 4;
+    const uint32_t chunk = PT * nthr;
+    uint32_t ev[PT];
+    float wv[PT];
+#pragma unroll
+    for (uint32_t u = 0; u < PT; u++) {
+        const uint32_t i = u * nthr + tid;
+        ev[u] = i < ne ? ws.pidx[i] : 0u;
+        wv[u] = i < ne ? ws.pw[i] : 0.f;
+    }
+    if (tid <= E) {
+        cnt[tid] = 0;
+        efmt[0][tid] = tid == E ? L.sg.fmt : L.pk[0].regular ? L.pk[0].fmt : L.experts[tid].fmt[0];
+        efmt[1][tid] = tid == E ? L.sd.fmt : L.pk[2].regular ? L.pk[2].fmt : L.experts[tid].fmt[2];
+    }
     __syncthreads();
-    for (uint32_t i = tid; i < ne; i += blockDim.x) atomicAdd(&cnt[ws.pidx[i]], 1u);
+    for (uint32_t c0 = 0; c0 < ne; c0 += chunk) {
+        if (c0) {
+#pragma unroll
+            for (uint32_t u = 0; u < PT; u++) {
+                const uint32_t i = c0 + u * nthr + tid;
+                ev[u] = i < ne ? ws.pidx[i] : 0u;
+            }
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < PT; u++)
+            if (c0 + u * nthr + tid < ne) atomicAdd(&cnt[ev[u]], 1u);
+    }
     __syncthreads();
     if (tid < 64) {   // exclusive scans of the counts and of the tiles per expert
         uint32_t run = 0, trun = 0;
@@ -139,27 +169,35 @@ __global__ __launch_bounds__(1024) void k_pre_sort(PrefillLayer L, PrefillWs ws)
             const uint32_t e = e0 + tid;
             const uint32_t c = e < E ? cnt[e] : 0u;
             const uint32_t nt = (c + kPM - 1) / kPM;
-            uint32_t sc = c, st = nt;
-#pragma unroll
-            for (int d = 1; d < 64; d <<= 1) {   // inclusive wave scan
-                const uint32_t oc = __shfl_up(sc, d), ot = __shfl_up(st, d);
-                if (tid >= (uint32_t)d) { sc += oc; st += ot; }
-            }
+            const uint32_t sc = wave_scan_incl(c, tid), st = wave_scan_incl(nt, tid);
             if (e < E) { off[e] = run + sc - c; tof[e] = trun + st - nt; }
-            run += __shfl(sc, 63);
-            trun += __shfl(st, 63);
+            run += __builtin_amdgcn_readlane(sc, 63);
+            trun += __builtin_amdgcn_readlane(st, 63);
         }
         if (tid == 0) { off[E] = run; tof[E] = trun; }
     }
     __syncthreads();
-    for (uint32_t e = tid; e < E; e += blockDim.x) cur[e] = off[e];
+    for (uint32_t e = tid; e < E; e += nthr) cur[e] = off[e];
     __syncthreads();
-    for (uint32_t i = tid; i < ne; i += blockDim.x) {
-        const uint32_t e = ws.pidx[i];
-        const uint32_t pos = atomicAdd(&cur[e], 1u);
-        ws.ent_tok[pos] = i / L.top_k;
-        ws.ent_w[pos] = ws.pw[i];
-        ws.ent_pos[i] = pos;
+    for (uint32_t c0 = 0; c0 < ne; c0 += chunk) {
+        if (ne > chunk) {   // the registers hold the last chunk: reload
+#pragma unroll
+            for (uint32_t u = 0; u < PT; u++) {
+                const uint32_t i = c0 + u * nthr + tid;
+                ev[u] = i < ne ? ws.pidx[i] : 0u;
+                wv[u] = i < ne ? ws.pw[i] : 0.f;
+            }
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < PT; u++) {
+            const uint32_t i = c0 + u * nthr + tid;
+            if (i >= ne) continue;
+            const uint32_t pos = atomicAdd(&cur[ev[u]], 1u);
+            if (pos >= ne) continue;   // cannot happen: the counts bound every expert's range
+            ws.ent_tok[pos] = i / L.top_k;
+            ws.ent_w[pos] = wv[u];
+            ws.ent_pos[i] = pos;
+        }
     }
     for (uint32_t e = tid; e < E; e += blockDim.x) {
         const uint32_t c = cnt[e];
@@ -178,11 +216,13 @@ __global__ __launch_bounds__(1024) void k_pre_sort(PrefillLayer L, PrefillWs ws)
     // k: 0 gate/up, 1 down), each group in tile order (the tiles of one
     // expert stay together): one grouped launch per format present.
     // Experts (and last the shared one) go 64 to a round, lane l expert
-    // 64 r + l; a wave scan per format places its tiles.
+    // 64 r + l; a wave scan per format present in the layer places its tiles.
     const uint32_t wave = tid >> 6, lane = tid & 63u;
     if (wave < 2) {
         const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
         const int k = wave == 0 ? 0 : 2;
+        const uint32_t present = (k == 0 ? L.fmask_gu : L.fmask_dn) |
+                                 (L.sg.p ? 1u << (k == 0 ? L.sg.fmt : L.sd.fmt) : 0u);
         uint32_t* order = ws.forder + (size_t)wave * cap;
         uint32_t base[F_NFMT];
 #pragma unroll
@@ -208,24 +248,23 @@ __global__ __launch_bounds__(1024) void k_pre_sort(PrefillLayer L, PrefillWs ws)
                 if (e < E) {
                     nt = (cnt[e] + kPM - 1) / kPM;
                     t0 = tof[e];
-                    f = L.pk[k].regular ? L.pk[k].fmt : L.experts[e].fmt[k];
+                    f = efmt[wave][e];
                 } else if (e == E) {
                     nt = nsh;
                     t0 = nrt;
-                    f = k == 0 ? L.sg.fmt : L.sd.fmt;
+                    f = efmt[wave][E];
                 }
 #pragma unroll
                 for (int g = 0; g < F_NFMT; g++) {
+                    if (!((present >> g) & 1u)) continue;
                     const uint32_t mine = f == g ? nt : 0u;
-                    uint32_t incl = mine;   // inclusive scan over the lanes
-#pragma unroll
-                    for (int d = 1; d < 64; d <<= 1) {
-                        const uint32_t o = __shfl_up(incl, d);
-                        if (lane >= (uint32_t)d) incl += o;
-                    }
+                    const uint32_t incl = wave_scan_incl(mine, lane);
                     if (pass == 1 && mine)
-                        for (uint32_t i = 0; i < mine; i++) order[base[g] + incl - mine + i] = t0 + i;
-                    base[g] += __shfl(incl, 63);
+                        for (uint32_t i = 0; i < mine; i++) {
+                            const uint32_t o = base[g] + incl - mine + i;
+                            if (o < cap) order[o] = t0 + i;
+                        }
+                    base[g] += __builtin_amdgcn_readlane(incl, 63);
                 }
             }
         }
@@ -401,7 +440,9 @@ __global__ __launch_bounds__(kPWG, (gemm_min_blocks<MODE, F>())) void k_pre_gemm
     if (slot >= per_xcd || item >= total) return;
     const uint32_t ti = item / ny, yb = item % ny;
     const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
-    const uint4 tile = ws.tiles[ws.forder[(size_t)MODE * cap + g_first + ti]];
+    const uint32_t oi = ws.forder[(size_t)MODE * cap + g_first + ti];
+    if (oi >= ws.n_tiles[0] + ws.n_tiles[1]) return;   // not a tile of this call
+    const uint4 tile = ws.tiles[oi];
     const uint32_t mid_e = tile.x, ent0 = tile.y, cnt = tile.z;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
     const uint32_t n = lane & 15u, q = lane >> 4;

@@ -313,6 +313,56 @@ def test_grouped_graph_replay(torch_dev, ctx, layer):
         ctx.set_mode(0)
 
 
+def test_grouped_format_groups_graph_replay(torch_dev, ctx):
+    """A layer whose shared expert has formats no routed expert has and whose
+    downs mix IQ3_S and IQ2_S (several format groups per matrix kind): eager
+    calls agree bitwise with each other and with every replay of the captured
+    graph, and the output matches the oracle on a sample of tokens."""
+    from qw6_amd.workload import SynthLayer
+    torch = torch_dev
+    L = SynthLayer(ctx, 68, 0, "iq2m")
+    try:
+        T = 96
+        lg_h = S.zipf_logits(69, T)
+        xs = np.stack([cases.token_x(68, 6, t) for t in range(T)])
+        lg = torch.from_numpy(lg_h).cuda()
+        x = torch.from_numpy(xs).cuda()
+        eager = torch.zeros(T, L.hidden, dtype=torch.float32, device="cuda")
+        again = torch.zeros_like(eager)
+        ctx.set_mode(2)
+        try:
+            ctx.moe_forward(L.desc, x, eager, n_tok=T, logits=lg)
+            ctx.moe_forward(L.desc, x, again, n_tok=T, logits=lg)
+            torch.cuda.synchronize()
+            assert torch.equal(again, eager)
+            out = torch.zeros_like(eager)
+            s = torch.cuda.Stream()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.stream(s):
+                ctx.moe_forward(L.desc, x, out, n_tok=T, logits=lg, stream=s.cuda_stream)
+                torch.cuda.synchronize()
+                with torch.cuda.graph(g, stream=s):
+                    ctx.moe_forward(L.desc, x, out, n_tok=T, logits=lg, stream=s.cuda_stream)
+            for _ in range(3):
+                out.zero_()
+                g.replay()
+                torch.cuda.synchronize()
+                assert torch.equal(out, eager)
+                ctx.moe_forward(L.desc, x, again, n_tok=T, logits=lg)
+                torch.cuda.synchronize()
+                assert torch.equal(again, eager)
+        finally:
+            ctx.set_mode(0)
+        got = eager.cpu().numpy()
+        ref = oracle_tokens(L, xs, lg_h, [0, 47, 95])
+        for t, (oo, _, _) in ref.items():
+            rel = cases.rel_l2(got[t], oo)
+            say("format groups, token %d: rel-L2 %.2e" % (t, rel))
+            assert rel <= TOL_BF16
+    finally:
+        L.free()
+
+
 def test_grouped_in_place_residual_update(torch_dev, ctx, layer):
     """x, residual and out the same buffer on the grouped path (router and
     RMSNorm on the device) equals the call with separate buffers."""
