@@ -12,11 +12,13 @@
 //                 one expert (the shared expert last, with every token), and
 //                 the tiles grouped by the format of their gate/up and of
 //                 their down matrix (experts may differ in format).
-//   k_pre_gemm<0, F> (one launch per format F present)
+//   k_pre_gemm<0, F, FS> (one launch per format group, or per two groups
+//                 of one occupancy class: the shared expert's own format
+//                 beside the routed experts', or two routed formats)
 //                 gate and up for 128 intermediate rows of one tile (64
 //                 for Q6_K and IQ3_S): mid[entry] = silu(x.gate) * (x.up).
-//   k_pre_gemm<1> down for 256 hidden rows of one tile (128 for Q6_K and
-//                 IQ3_S), times the entry's gate weight -> ybuf[entry].
+//   k_pre_gemm<1, F, FS> down for 256 hidden rows of one tile (128 for
+//                 Q6_K and IQ3_S), times the entry's gate weight -> ybuf[entry].
 //   k_pre_combine out[t] = sum_k ybuf[entry(t, k)] + ybuf[shared entry(t)]
 //                 (+ residual), a fixed order: deterministic, no atomics.
 //
@@ -411,38 +413,37 @@ __device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NP],
 
 // MODE 0: gate/up; wave w holds RT/2 gate tiles and the RT/2 up tiles of the
 // same 8 RT intermediate rows (block rows: 32 RT). MODE 1: down; wave w holds
-// RT tiles of 16 hidden rows (block rows: 64 RT). Block (tile, row group).
+// RT tiles of 16 hidden rows (block rows: 64 RT). Work item (tile, row block).
 // Software pipeline over the 256-column blocks: the raw weight bytes and the
 // A operands of block kb + 1 are loaded into registers while block kb is
 // multiplied, then written to LDS between two barriers.
-// The launch for format F takes the tiles of F's group (ws.forder, ws.fseg).
+// Occupancy class of a format's contraction: three workgroups per CU (at
+// most 168 VGPRs; 53 KB of LDS or less each) except Q5_K and IQ2_S, whose
+// bodies need up to 198 VGPRs (two). Format groups share a launch only
+// within a class; a shared launch is built for its class, a single format's
+// launch for three (Q4_K) or with room for two (the others, whose
+// allocations fit three workgroups per CU all the same).
+__host__ __device__ constexpr int gemm_class(int f) { return (f == F_Q5K || f == F_IQ2S) ? 2 : 3; }
+template <int F, int FS>
+__host__ __device__ constexpr int gemm_min_blocks() {
+    return F == FS ? (F == F_Q4K ? 3 : 2) : (gemm_class(F) < gemm_class(FS) ? gemm_class(F) : gemm_class(FS));
+}
 template <int MODE, int F>
-__host__ __device__ constexpr int gemm_min_blocks() {   // workgroups per CU
-    return F == F_Q4K ? 3 : 2;   // Q4_K: 52 KB of LDS each, three fit in 160 KB
+__host__ __device__ inline uint32_t gemm_ny(uint32_t hidden, uint32_t inter) {   // row blocks
+    constexpr int RT = gemm_rt<MODE, F>();
+    return MODE == 0 ? inter / (32 * RT) : hidden / (64 * RT);
+}
+template <int MODE, int F>
+__host__ __device__ constexpr size_t gemm_lds() {
+    return offsetof(GemmLds, raw) + (size_t)64 * gemm_rt<MODE, F>() * raw_chunks(F) * 16 + iq_tab_bytes(F);
 }
 
+// Row block yb of tile `tile` (format F).
 template <int MODE, int F>
-__global__ __launch_bounds__(kPWG, (gemm_min_blocks<MODE, F>())) void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
+__device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs& ws, uint4 tile,
+                                          uint32_t yb, uint8_t* smem) {
     constexpr int RT = gemm_rt<MODE, F>();
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     GemmLds& S = *(GemmLds*)smem;
-    // XCD-aware work order: workgroup p runs on XCD p % 8 (round-robin
-    // dispatch), so XCD x takes the x-th contiguous range of the (tile, row
-    // block) items -- the row blocks of one tile (same A rows) and the tiles of
-    // one expert (same weights) then share that XCD's L2.
-    const uint32_t ny = MODE == 0 ? L.inter / (32 * RT) : L.hidden / (64 * RT);
-    const uint32_t g_first = ws.fseg[(MODE * 8 + F) * 2 + 0];
-    const uint32_t n_t = ws.fseg[(MODE * 8 + F) * 2 + 1];
-    const uint32_t total = n_t * ny;
-    const uint32_t per_xcd = (total + 7) / 8;
-    const uint32_t slot = blockIdx.x / 8;
-    const uint32_t item = (blockIdx.x % 8) * per_xcd + slot;
-    if (slot >= per_xcd || item >= total) return;
-    const uint32_t ti = item / ny, yb = item % ny;
-    const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
-    const uint32_t oi = ws.forder[(size_t)MODE * cap + g_first + ti];
-    if (oi >= ws.n_tiles[0] + ws.n_tiles[1]) return;   // not a tile of this call
-    const uint4 tile = ws.tiles[oi];
     const uint32_t mid_e = tile.x, ent0 = tile.y, cnt = tile.z;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
     const uint32_t n = lane & 15u, q = lane >> 4;
@@ -601,6 +602,46 @@ __global__ __launch_bounds__(kPWG, (gemm_min_blocks<MODE, F>())) void k_pre_gemm
     }
 }
 
+// One launch over the work items of one or two format groups (ws.forder,
+// ws.fseg): group F's items and (FS != F) group FS's. Each workgroup takes
+// one item and decodes it with its group's format; a layer whose shared
+// expert has a format no routed expert has, or whose experts mix formats,
+// needs no launch that fills only part of the GPU.
+// XCD-aware work order: workgroup p runs on XCD p % 8 (round-robin
+// dispatch), so XCD x takes the x-th contiguous range of each group's items
+// (its slots first cover its range of F, then its range of FS) -- the row
+// blocks of one tile (same A rows) and the tiles of one expert (same
+// weights) then share that XCD's L2, and every XCD gets the same share of
+// each format.
+template <int MODE, int F, int FS>
+__global__ __launch_bounds__(kPWG, (gemm_min_blocks<F, FS>()))
+void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const uint32_t ny_a = gemm_ny<MODE, F>(L.hidden, L.inter);
+    const uint32_t ny_b = gemm_ny<MODE, FS>(L.hidden, L.inter);
+    const uint32_t first_a = ws.fseg[(MODE * 8 + F) * 2 + 0], n_a = ws.fseg[(MODE * 8 + F) * 2 + 1];
+    const uint32_t first_b = FS != F ? ws.fseg[(MODE * 8 + FS) * 2 + 0] : 0u;
+    const uint32_t n_b = FS != F ? ws.fseg[(MODE * 8 + FS) * 2 + 1] : 0u;
+    const uint32_t items_a = n_a * ny_a, items_b = n_b * ny_b;
+    const uint32_t pa = (items_a + 7) / 8, pb = (items_b + 7) / 8;   // per XCD
+    const uint32_t slot = blockIdx.x / 8, xcd = blockIdx.x % 8;
+    const bool in_b = slot >= pa;
+    if (slot >= pa + pb) return;
+    const uint32_t it = in_b ? xcd * pb + (slot - pa) : xcd * pa + slot;
+    if (it >= (in_b ? items_b : items_a)) return;
+    const uint32_t ny = in_b ? ny_b : ny_a;
+    const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
+    const uint32_t oi = ws.forder[(size_t)MODE * cap + (in_b ? first_b : first_a) + it / ny];
+    if (oi >= ws.n_tiles[0] + ws.n_tiles[1]) return;   // not a tile of this call
+    const uint4 tile = ws.tiles[oi];
+    if constexpr (FS == F) {
+        gemm_item<MODE, F>(L, ws, tile, it % ny, smem);
+    } else {
+        if (in_b) gemm_item<MODE, FS>(L, ws, tile, it % ny, smem);
+        else gemm_item<MODE, F>(L, ws, tile, it % ny, smem);
+    }
+}
+
 // out[t] = sum_k ybuf[entry(t, k)] + ybuf[shared entry(t)] (+ residual); the
 // gate weights were applied by the down kernel. Selection order, shared last,
 // as qw6.c:2263, 2284.
@@ -679,31 +720,70 @@ __global__ __launch_bounds__(64) void k_pre_router(const float* __restrict__ rou
     }
 }
 
+template <int MODE, int F, int FS>
+void launch_gemm_ff(const PrefillLayer& L, const PrefillWs& ws, uint32_t cap, hipStream_t st) {
+    const size_t lds = gemm_lds<MODE, F>() > gemm_lds<MODE, FS>() ? gemm_lds<MODE, F>() : gemm_lds<MODE, FS>();
+    const uint32_t ny_a = gemm_ny<MODE, F>(L.hidden, L.inter), ny_b = gemm_ny<MODE, FS>(L.hidden, L.inter);
+    // at most cap tiles in all; the kernel maps workgroups to its groups'
+    // items, per XCD a rounded-up share of each group
+    const uint32_t nwg = (cap * (ny_a > ny_b ? ny_a : ny_b) + 7) / 8 * 8 + (FS != F ? 8u : 0u);
+    k_pre_gemm<MODE, F, FS><<<nwg, kPWG, lds, st>>>(L, ws);
+}
+// Groups of one occupancy class only (no other pair is instantiated).
+template <int MODE, int F, int FS>
+int launch_pair(const PrefillLayer& L, const PrefillWs& ws, uint32_t cap, hipStream_t st) {
+    if constexpr (gemm_class(F) == gemm_class(FS)) {
+        launch_gemm_ff<MODE, F, FS>(L, ws, cap, st);
+        return 0;
+    } else {
+        return qw6_fail("batched path: formats %d and %d paired across occupancy classes", F, FS);
+    }
+}
 template <int MODE, int F>
-void launch_gemm_f(const PrefillLayer& L, const PrefillWs& ws, uint32_t cap, hipStream_t st) {
-    constexpr int RT = gemm_rt<MODE, F>();
-    const size_t lds = offsetof(GemmLds, raw) + (size_t)64 * RT * raw_chunks(F) * 16 + iq_tab_bytes(F);
-    const uint32_t ny = MODE == 0 ? L.inter / (32 * RT) : L.hidden / (64 * RT);
-    // cap tiles at most; the kernel maps workgroups to its format's items
-    const uint32_t nwg = (cap * ny + 7) / 8 * 8;
-    k_pre_gemm<MODE, F><<<nwg, kPWG, lds, st>>>(L, ws);
+int launch_gemm_f(int fs, const PrefillLayer& L, const PrefillWs& ws, uint32_t cap, hipStream_t st) {
+    switch (fs) {
+    case F_Q4K: return launch_pair<MODE, F, F_Q4K>(L, ws, cap, st);
+    case F_Q5K: return launch_pair<MODE, F, F_Q5K>(L, ws, cap, st);
+    case F_Q6K: return launch_pair<MODE, F, F_Q6K>(L, ws, cap, st);
+    case F_IQ2XXS: return launch_pair<MODE, F, F_IQ2XXS>(L, ws, cap, st);
+    case F_IQ2S: return launch_pair<MODE, F, F_IQ2S>(L, ws, cap, st);
+    default: return launch_pair<MODE, F, F_IQ3S>(L, ws, cap, st);
+    }
 }
 
-// One launch per format in `mask` (the routed experts' formats of this
-// matrix kind and the shared expert's), each over its format's tiles.
+// The format groups of one matrix kind (routed formats `routed`, the shared
+// expert's `fsh`, or -1), up to two to a launch: in the order the shared
+// expert's group (when no routed expert has its format), then the routed
+// groups by format, each group not yet launched takes the next one of its
+// occupancy class as its partner.
 template <int MODE>
-int launch_gemm(uint32_t mask, const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) {
+int launch_gemm(uint32_t routed, int fsh, const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) {
     const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
-    for (int f = 0; f < F_NFMT; f++) {
-        if (!((mask >> f) & 1u)) continue;
-        switch (f) {
-        case F_Q4K: launch_gemm_f<MODE, F_Q4K>(L, ws, cap, st); break;
-        case F_Q5K: launch_gemm_f<MODE, F_Q5K>(L, ws, cap, st); break;
-        case F_Q6K: launch_gemm_f<MODE, F_Q6K>(L, ws, cap, st); break;
-        case F_IQ2XXS: launch_gemm_f<MODE, F_IQ2XXS>(L, ws, cap, st); break;
-        case F_IQ2S: launch_gemm_f<MODE, F_IQ2S>(L, ws, cap, st); break;
-        default: launch_gemm_f<MODE, F_IQ3S>(L, ws, cap, st); break;
+    int order[F_NFMT + 1], n = 0;
+    bool done[F_NFMT + 1] = {};
+    if (fsh >= 0 && !((routed >> fsh) & 1u)) order[n++] = fsh;
+    for (int f = 0; f < F_NFMT; f++)
+        if ((routed >> f) & 1u) order[n++] = f;
+    for (int i = 0; i < n; i++) {
+        if (done[i]) continue;
+        const int fa = order[i];
+        int fb = fa;
+        for (int j = i + 1; j < n; j++)
+            if (!done[j] && gemm_class(order[j]) == gemm_class(fa)) {
+                fb = order[j];
+                done[j] = true;
+                break;
+            }
+        int rc;
+        switch (fa) {
+        case F_Q4K: rc = launch_gemm_f<MODE, F_Q4K>(fb, L, ws, cap, st); break;
+        case F_Q5K: rc = launch_gemm_f<MODE, F_Q5K>(fb, L, ws, cap, st); break;
+        case F_Q6K: rc = launch_gemm_f<MODE, F_Q6K>(fb, L, ws, cap, st); break;
+        case F_IQ2XXS: rc = launch_gemm_f<MODE, F_IQ2XXS>(fb, L, ws, cap, st); break;
+        case F_IQ2S: rc = launch_gemm_f<MODE, F_IQ2S>(fb, L, ws, cap, st); break;
+        default: rc = launch_gemm_f<MODE, F_IQ3S>(fb, L, ws, cap, st); break;
         }
+        if (rc) return -1;
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return qw6_fail("batched kernel launch: %s", hipGetErrorString(e));
     }
@@ -747,10 +827,8 @@ int prefill_forward(const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) 
     k_pre_sort<<<1, 1024, 0, st>>>(Lx, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return qw6_fail("batched routing launch: %s", hipGetErrorString(e));
-    const uint32_t m_gu = L.fmask_gu | (L.sg.p ? 1u << L.sg.fmt : 0u);
-    const uint32_t m_dn = L.fmask_dn | (L.sg.p ? 1u << L.sd.fmt : 0u);
-    if (launch_gemm<0>(m_gu, Lx, ws, st)) return -1;
-    if (launch_gemm<1>(m_dn, Lx, ws, st)) return -1;
+    if (launch_gemm<0>(L.fmask_gu, L.sg.p ? L.sg.fmt : -1, Lx, ws, st)) return -1;
+    if (launch_gemm<1>(L.fmask_dn, L.sg.p ? L.sd.fmt : -1, Lx, ws, st)) return -1;
     k_pre_combine<<<dim3(L.T, (L.hidden / 4 + 255) / 256), 256, 0, st>>>(Lx, ws);
     e = hipGetLastError();
     if (e != hipSuccess) return qw6_fail("batched combine launch: %s", hipGetErrorString(e));
