@@ -226,6 +226,22 @@ __global__ __launch_bounds__(1024) void k_pre_sort(PrefillLayer L, PrefillWs ws)
         const uint32_t present = (k == 0 ? L.fmask_gu : L.fmask_dn) |
                                  (L.sg.p ? 1u << (k == 0 ? L.sg.fmt : L.sd.fmt) : 0u);
         uint32_t* order = ws.forder + (size_t)wave * cap;
+        const uint32_t routed = k == 0 ? L.fmask_gu : L.fmask_dn;
+        if (__builtin_popcount(routed) == 1) {
+            // one routed format: the tile list is grouped already (routed
+            // tiles, then the shared expert's)
+            const int fr = __builtin_ctz(routed);
+            const int fs = nsh ? (int)efmt[wave][E] : -1;
+            for (uint32_t i = lane; i < nrt + nsh; i += 64) order[i] = i;
+            if (lane < F_NFMT) {
+                uint32_t first = 0, count = 0;
+                if ((int)lane == fr) count = nrt + (fs == fr ? nsh : 0u);
+                else if ((int)lane == fs) { first = nrt; count = nsh; }
+                ws.fseg[(wave * 8 + lane) * 2 + 0] = first;
+                ws.fseg[(wave * 8 + lane) * 2 + 1] = count;
+            }
+            return;
+        }
         uint32_t base[F_NFMT];
 #pragma unroll
         for (int f = 0; f < F_NFMT; f++) base[f] = 0;
