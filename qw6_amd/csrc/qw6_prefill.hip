@@ -130,6 +130,8 @@ __global__ __launch_bounds__(64) void k_pre_route(PrefillLayer L, PrefillWs ws,
 __global__ __launch_bounds__(1024) void k_pre_sort(PrefillLayer L, PrefillWs ws) {
     __shared__ uint32_t cnt[257], off[257], cur[257], tof[257];
     __shared__ uint8_t efmt[2][257];   // gate/up and down format per expert, the shared one last
+    __shared__ uint32_t rel[2][257];   // per kind: an expert's first tile within its format group
+    __shared__ uint32_t gst[2][F_NFMT];   // per kind: the groups' first places
     const uint32_t tid = threadIdx.x, nthr = blockDim.x;
     const uint32_t ne = L.T * L.top_k, E = L.n_experts;
     // Every global load a thread needs goes out before its first wait: its
@@ -216,20 +218,19 @@ __global__ __launch_bounds__(1024) void k_pre_sort(PrefillLayer L, PrefillWs ws)
     }
     // The tiles grouped by the format of their matrix, per matrix kind (wave
     // k: 0 gate/up, 1 down), each group in tile order (the tiles of one
-    // expert stay together): one grouped launch per format present.
-    // Experts (and last the shared one) go 64 to a round, lane l expert
-    // 64 r + l; a wave scan per format present in the layer places its tiles.
+    // expert stay together): one grouped launch per format (group pair).
+    // With one routed format the list is grouped already (routed tiles, then
+    // the shared expert's). Otherwise wave k finds each expert's place in its
+    // group (experts, the shared one last, 64 to a round, a wave scan per
+    // format present), then one thread per (kind, expert) writes its tiles.
     const uint32_t wave = tid >> 6, lane = tid & 63u;
+    const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
+    const bool mixed0 = __builtin_popcount(L.fmask_gu) > 1, mixed1 = __builtin_popcount(L.fmask_dn) > 1;
     if (wave < 2) {
-        const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
         const int k = wave == 0 ? 0 : 2;
-        const uint32_t present = (k == 0 ? L.fmask_gu : L.fmask_dn) |
-                                 (L.sg.p ? 1u << (k == 0 ? L.sg.fmt : L.sd.fmt) : 0u);
         uint32_t* order = ws.forder + (size_t)wave * cap;
         const uint32_t routed = k == 0 ? L.fmask_gu : L.fmask_dn;
-        if (__builtin_popcount(routed) == 1) {
-            // one routed format: the tile list is grouped already (routed
-            // tiles, then the shared expert's)
+        if (!(wave == 0 ? mixed0 : mixed1)) {
             const int fr = __builtin_ctz(routed);
             const int fs = nsh ? (int)efmt[wave][E] : -1;
             for (uint32_t i = lane; i < nrt + nsh; i += 64) order[i] = i;
@@ -240,52 +241,46 @@ __global__ __launch_bounds__(1024) void k_pre_sort(PrefillLayer L, PrefillWs ws)
                 ws.fseg[(wave * 8 + lane) * 2 + 0] = first;
                 ws.fseg[(wave * 8 + lane) * 2 + 1] = count;
             }
-            return;
-        }
-        uint32_t base[F_NFMT];
+        } else {
+            const uint32_t present = routed | (nsh ? 1u << efmt[wave][E] : 0u);
+            uint32_t base[F_NFMT];
 #pragma unroll
-        for (int f = 0; f < F_NFMT; f++) base[f] = 0;
-        // two passes: counts (the group sizes and starts), then placement
-        for (int pass = 0; pass < 2; pass++) {
-            uint32_t start[F_NFMT];
-            if (pass == 1) {
-                uint32_t run = 0;
-#pragma unroll
-                for (int f = 0; f < F_NFMT; f++) { start[f] = run; run += base[f]; }
-                if (lane < F_NFMT) {
-                    ws.fseg[(wave * 8 + lane) * 2 + 0] = start[lane];
-                    ws.fseg[(wave * 8 + lane) * 2 + 1] = base[lane];
-                }
-#pragma unroll
-                for (int f = 0; f < F_NFMT; f++) base[f] = start[f];
-            }
+            for (int f = 0; f < F_NFMT; f++) base[f] = 0;
             for (uint32_t e0 = 0; e0 <= E; e0 += 64) {
                 const uint32_t e = e0 + lane;
-                uint32_t nt = 0, t0 = 0;
-                int f = 0;
-                if (e < E) {
-                    nt = (cnt[e] + kPM - 1) / kPM;
-                    t0 = tof[e];
-                    f = efmt[wave][e];
-                } else if (e == E) {
-                    nt = nsh;
-                    t0 = nrt;
-                    f = efmt[wave][E];
-                }
+                const uint32_t nt = e < E ? (cnt[e] + kPM - 1) / kPM : e == E ? nsh : 0u;
+                const int f = e <= E ? (int)efmt[wave][e] : -1;
 #pragma unroll
                 for (int g = 0; g < F_NFMT; g++) {
                     if (!((present >> g) & 1u)) continue;
                     const uint32_t mine = f == g ? nt : 0u;
                     const uint32_t incl = wave_scan_incl(mine, lane);
-                    if (pass == 1 && mine)
-                        for (uint32_t i = 0; i < mine; i++) {
-                            const uint32_t o = base[g] + incl - mine + i;
-                            if (o < cap) order[o] = t0 + i;
-                        }
+                    if (f == g) rel[wave][e] = base[g] + incl - mine;   // place in the group
                     base[g] += __builtin_amdgcn_readlane(incl, 63);
                 }
             }
+            uint32_t run = 0;
+#pragma unroll
+            for (int f = 0; f < F_NFMT; f++) {
+                if (lane == (uint32_t)f) {
+                    gst[wave][f] = run;
+                    ws.fseg[(wave * 8 + lane) * 2 + 0] = run;
+                    ws.fseg[(wave * 8 + lane) * 2 + 1] = base[f];
+                }
+                run += base[f];
+            }
         }
+    }
+    if (!mixed0 && !mixed1) return;   // the same for every thread
+    __syncthreads();
+    const uint32_t kk = tid >> 9, e = tid & 511u;
+    if ((kk == 0 ? mixed0 : mixed1) && e <= E) {
+        const uint32_t nt = e < E ? (cnt[e] + kPM - 1) / kPM : nsh;
+        const uint32_t t0 = e < E ? tof[e] : nrt;
+        const uint32_t o = gst[kk][efmt[kk][e]] + rel[kk][e];
+        uint32_t* order = ws.forder + (size_t)kk * cap;
+        for (uint32_t j = 0; j < nt; j++)
+            if (o + j < cap) order[o + j] = t0 + j;
     }
 }
 
