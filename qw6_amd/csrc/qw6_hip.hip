@@ -1650,6 +1650,228 @@ __global__ __launch_bounds__(kWG) void k_head(const uint8_t* __restrict__ W, uin
     if (lane == 0) part[gw] = best;
 }
 
+// ---- output head, Q6_K rows of 2048 columns: bf16 MFMA -------------------------
+// A 16-row tile and one 256-column block (a "unit") at a time, per wave.
+// For each 32-column run r of the block (qw6's even-scale rule gives a run one
+// scale), one v_mfma_f32_16x16x32_bf16 with
+//   B[k][n] = 128 + q (bf16, exact) of row n, column 32 r + k of the block,
+//   A[c][k] = part c / 8 (hi, lo) of the normalised activation of column
+//             32 (c % 8) + k of the block,
+// so that D_r[c][n] for c % 8 == r is row n's product with run r, part c / 8
+// (the other entries are not used). A is the same for every tile: eight 4-VGPR
+// operands per lane, built once. A ninth MFMA with B = -160 (the code bias 128
+// plus Q6_K's 32) gives -160 x each A row's sum, and seeds every D_r with it.
+// The run's d * scale multiplies its entry afterwards; the four lane groups
+// (hi / lo, runs 0-3 / 4-7) add up a row at the end (qw6_vk.c:3447-3478 is the
+// reference's head; the arithmetic is qw6.c:1550-1578 and 2490-2492).
+// Units stream through kHqSlots direct-to-LDS slots per wave: 16 rows x 15
+// chunks of 16 B (the block spans 14; the 15th, a repeat of the row's first,
+// spaces the rows over the LDS banks).
+constexpr uint32_t kHqChunks = 15;
+constexpr uint32_t kHqSlot = 4096;          // bytes per slot (240 chunks, padded)
+constexpr uint32_t kHqSlots = 4;            // units in flight per wave
+constexpr uint32_t kHqWG = 4;               // waves per workgroup
+constexpr uint32_t kHqLoads = 4;            // 16-B loads per lane per unit
+constexpr uint32_t kHqWaves = 2048;         // waves of one launch, at most
+constexpr uint32_t kHqRowBytes = 8 * 210;   // a Q6_K row of 2048 columns
+
+// Stage block b of tile `tile` (16 rows from W + 16 tile rows) into slot.
+// The block starts 2b bytes into its first 16-B chunk (W 16-byte aligned).
+__device__ __forceinline__ void hq_stage(uint8_t* slot, const uint8_t* W, uint32_t tile, uint32_t b) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint8_t* c0 = W + (size_t)tile * 16u * kHqRowBytes + 208u * b;   // 16-aligned: 210 b - 2 b
+#pragma unroll
+    for (uint32_t k = 0; k < kHqLoads; k++) {
+        const uint32_t i = 64u * k + lane;   // chunk i: row i / 15, chunk i % 15
+        const uint32_t row = i < 16u * kHqChunks ? i / kHqChunks : 0u;
+        const uint32_t ch = i % kHqChunks < 14u ? i % kHqChunks : 0u;
+        __builtin_amdgcn_global_load_lds((glb_void_t*)(c0 + (size_t)row * kHqRowBytes + 16u * ch),
+                                         (lds_void_t*)(slot + 1024u * k), 16, 0, 0);
+    }
+}
+
+// Two dwords from 8 bytes at LDS byte offset o, o % 4 == 2 * (B & 1).
+template <uint32_t B>
+__device__ __forceinline__ uint2 hq_read8(const uint32_t* s, uint32_t o) {
+    if constexpr ((B & 1u) == 0) {
+        return make_uint2(s[o >> 2], s[(o >> 2) + 1]);
+    } else {
+        const uint32_t i = o >> 2, w0 = s[i], w1 = s[i + 1], w2 = s[i + 2];
+        return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, 2), __builtin_amdgcn_alignbyte(w2, w1, 2));
+    }
+}
+
+// The bytes of block B of a unit this lane needs (row n at LDS byte offset
+// o_row): ql of runs 4h + 0 / 2 (a) and 4h + 1 / 3 (c), qh (h), for halves h;
+// scales 8 hs + 0, 2, 4, 6 (hs = g & 1, the runs of its D entries); d.
+struct HqRaw {
+    uint2 a[2], c[2], h[2], sc;
+    uint32_t dw;
+};
+template <uint32_t B>
+__device__ __forceinline__ HqRaw hq_load(const uint32_t* s, uint32_t o_row, uint32_t g) {
+    const uint32_t o = o_row + 2u * B;   // the block's first byte
+    HqRaw r;
+#pragma unroll
+    for (uint32_t h = 0; h < 2; h++) {
+        r.a[h] = hq_read8<B>(s, o + 64u * h + 8u * g);
+        r.c[h] = hq_read8<B>(s, o + 64u * h + 32u + 8u * g);
+        r.h[h] = hq_read8<B>(s, o + 128u + 32u * h + 8u * g);
+    }
+    r.sc = hq_read8<B>(s, o + 192u + 8u * (g & 1u));
+    r.dw = s[(o + 208u) >> 2];
+    return r;
+}
+
+// Block B's products from its bytes: adds this lane's share of row n's dot
+// product with the block to acc.
+template <uint32_t B>
+__device__ __forceinline__ void hq_math(const HqRaw& r, uint32_t g, const uint4& a, float& acc) {
+    const uint4 bias = u4(0xC320C320u, 0xC320C320u, 0xC320C320u, 0xC320C320u);   // bf16 -160
+    const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+    const f32x4 db = mfma(a, bias, z4);
+    f32x4 D[8];
+#pragma unroll
+    for (uint32_t h = 0; h < 2; h++) {
+        // runs 4h .. 4h + 3: low / high nibbles of a (runs 0, 2) and c (1, 3),
+        // two bits of qh per run (qw6.c:1550-1578)
+        const uint32_t av[2] = {r.a[h].x, r.a[h].y}, cv[2] = {r.c[h].x, r.c[h].y};
+        const uint32_t hv[2] = {r.h[h].x, r.h[h].y};
+        uint32_t w[4][2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            w[0][i] = (av[i] & 0x0f0f0f0fu) | ((hv[i] & 0x03030303u) << 4);
+            w[1][i] = (cv[i] & 0x0f0f0f0fu) | ((hv[i] & 0x0c0c0c0cu) << 2);
+            w[2][i] = ((av[i] >> 4) & 0x0f0f0f0fu) | (hv[i] & 0x30303030u);
+            w[3][i] = ((cv[i] >> 4) & 0x0f0f0f0fu) | ((hv[i] >> 2) & 0x30303030u);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; k++) D[4 * h + k] = mfma(a, codes8(w[k][0], w[k][1]), db);
+    }
+    // lane (n, g) holds D[4g + v][n]: part g / 2 of run 4 (g & 1) + v
+    const uint32_t hs = g & 1u;
+    const float d = h2f((r.dw >> (16u * (B & 1u))) & 0xffffu);   // byte 208 + 2B of a 4-aligned row
+    float t = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+        const float val = hs ? D[4 + v][v] : D[v][v];
+        const uint32_t wv = v < 2 ? r.sc.x : r.sc.y;
+        const float sc = (float)(int8_t)((wv >> (16 * (v & 1))) & 0xffu);
+        t = fmaf(sc, val, t);
+    }
+    acc = fmaf(d, t, acc);
+}
+
+// LDS reads of this wave done (before a slot they read is restaged).
+__device__ __forceinline__ void wait_lgkm0() {
+    __builtin_amdgcn_s_waitcnt(0xc07fu);   // lgkmcnt(0); vmcnt, expcnt not waited
+    asm volatile("" ::: "memory");
+}
+
+// Unit u = 8 st + B (block B of this step's tile) with its bytes in r:
+// restage its slot with unit u + S, read unit u + 1's bytes (landed once at
+// most S - 1 units remain in flight) into rn, then multiply block B.
+template <uint32_t S, uint32_t B>
+__device__ __forceinline__ void hq_step(const uint32_t* s, uint8_t* slots, uint32_t so, uint32_t g,
+                                        const uint4 (&A)[8], float& acc, HqRaw& r, const uint8_t* W,
+                                        uint32_t tile_next, uint32_t tile_now, uint32_t tiles) {
+    wait_lgkm0();
+    const uint32_t t = B + S < 8 ? tile_now : tile_next;
+    hq_stage(slots + (B % S) * kHqSlot, W, t < tiles ? t : 0u, (B + S) % 8);
+    wait_vm((S - 1) * kHqLoads);
+    const HqRaw rn = hq_load<(B + 1) % 8>(s, so + ((B + 1) % S) * kHqSlot, g);
+    hq_math<B>(r, g, A[B], acc);
+    r = rn;
+}
+
+// S: units in flight per wave (4 or 8), NW: waves per workgroup; built for
+// two waves per SIMD (at most 256 registers).
+template <uint32_t S, uint32_t NW>
+__global__ __launch_bounds__(64 * NW, 2) void k_head_q6k(const uint8_t* __restrict__ W, uint32_t tiles,
+                                                      uint32_t nsteps, const float* __restrict__ x,
+                                                      const float* __restrict__ norm_w, float eps,
+                                                      float* __restrict__ logits,
+                                                      uint64_t* __restrict__ part) {
+    static_assert(S == 4 || S == 8, "a slot per block or per half of the blocks");
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    const uint32_t n = lane & 15u, g = lane >> 4, c = lane & 15u;
+    const uint32_t gw = blockIdx.x * NW + wave, nwv = gridDim.x * NW;
+    uint8_t* slots = smem + wave * S * kHqSlot;
+    const uint32_t so = (uint32_t)(slots - smem) + 240u * n;   // row n in slot 0
+    auto tile_of = [&](uint32_t st) { return gw + st * nwv; };
+    // the first S units of step 0 in flight first
+#pragma unroll
+    for (uint32_t b = 0; b < S; b++) {
+        const uint32_t t = tile_of(0);
+        hq_stage(slots + b * kHqSlot, W, t < tiles ? t : 0u, b);
+    }
+    // A operands: lane (c, g) holds part c / 8 of columns 256 b + 32 (c % 8) + 8 g .. + 8
+    float xv[8][8];
+    float ss = 0.f;
+#pragma unroll
+    for (uint32_t b = 0; b < 8; b++) {
+        const float* xp = x + 256u * b + 32u * (c & 7u) + 8u * g;
+        const float4 u0 = *(const float4*)xp, u1 = *(const float4*)(xp + 4);
+        xv[b][0] = u0.x; xv[b][1] = u0.y; xv[b][2] = u0.z; xv[b][3] = u0.w;
+        xv[b][4] = u1.x; xv[b][5] = u1.y; xv[b][6] = u1.z; xv[b][7] = u1.w;
+#pragma unroll
+        for (int j = 0; j < 8; j++) ss = fmaf(xv[b][j], xv[b][j], ss);
+    }
+    if (norm_w) {   // final RMSNorm (qw6.c:2490-2492); every column appears in two lanes
+        ss = group_sum<64>(ss) * 0.5f;
+        const float sc = 1.0f / sqrtf(ss / 2048.0f + eps);
+#pragma unroll
+        for (uint32_t b = 0; b < 8; b++) {
+            const float* wp = norm_w + 256u * b + 32u * (c & 7u) + 8u * g;
+            const float4 u0 = *(const float4*)wp, u1 = *(const float4*)(wp + 4);
+            const float wv[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+            for (int j = 0; j < 8; j++) xv[b][j] = xv[b][j] * sc * wv[j];
+        }
+    }
+    uint4 A[8];
+    const bool lo = c >= 8;
+#pragma unroll
+    for (uint32_t b = 0; b < 8; b++) {
+        uint32_t wd[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float x0 = xv[b][2 * i], x1 = xv[b][2 * i + 1];
+            const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
+            const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
+            wd[i] = lo ? (bfb(l0) | (bfb(l1) << 16)) : (bfb(h0) | (bfb(h1) << 16));
+        }
+        A[b] = u4(wd[0], wd[1], wd[2], wd[3]);
+    }
+    const uint32_t* s = (const uint32_t*)smem;
+    wait_vm((S - 1) * kHqLoads);   // unit 0 has landed
+    HqRaw r = hq_load<0>(s, so, g);
+    uint64_t best = 0;
+    for (uint32_t st = 0; st < nsteps; st++) {
+        const uint32_t tn = tile_of(st), tx = tile_of(st + 1);
+        float acc = 0.f;
+        hq_step<S, 0>(s, slots, so, g, A, acc, r, W, tx, tn, tiles);
+        hq_step<S, 1>(s, slots, so, g, A, acc, r, W, tx, tn, tiles);
+        hq_step<S, 2>(s, slots, so, g, A, acc, r, W, tx, tn, tiles);
+        hq_step<S, 3>(s, slots, so, g, A, acc, r, W, tx, tn, tiles);
+        hq_step<S, 4>(s, slots, so, g, A, acc, r, W, tx, tn, tiles);
+        hq_step<S, 5>(s, slots, so, g, A, acc, r, W, tx, tn, tiles);
+        hq_step<S, 6>(s, slots, so, g, A, acc, r, W, tx, tn, tiles);
+        hq_step<S, 7>(s, slots, so, g, A, acc, r, W, tx, tn, tiles);
+        acc += partner(acc, 16, lane);
+        acc += partner(acc, 32, lane);
+        if (g == 0 && tn < tiles) {
+            const uint32_t row = 16u * tn + n;
+            logits[row] = acc;
+            best = max_u64(best, amax_key(acc, row));
+        }
+    }
+    wait_vm(0);   // no LDS-direct load lands after the workgroup ends
+    best = wave_max_u64(best);
+    if (lane == 0) part[gw] = best;
+}
+
 __global__ void k_gather(const float* eo, const float* ew, const float* sh, float sw,
                          float* o, uint32_t dim, uint32_t top_k) {
     const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
@@ -1898,6 +2120,18 @@ int launch_argmax(const float* x, uint32_t n, uint64_t* part, uint32_t* out, hip
 // part: kHeadWaves words.
 int launch_head(const MatD& W, const float* x, const float* norm_w, float eps, float* logits,
                 uint64_t* part, uint32_t* out, hipStream_t st) {
+    if (W.fmt == F_Q6K && W.cols == 2048 && W.rows % 16 == 0 && ((uintptr_t)W.p & 15u) == 0 &&
+        ((uintptr_t)x & 15u) == 0 && ((uintptr_t)norm_w & 15u) == 0) {
+        // bf16-MFMA head: 16-row tiles, each wave a tile per step
+        const uint32_t tiles = W.rows / 16;
+        const uint32_t nwv = std::min(kHqWaves, (tiles + kHqWG - 1) / kHqWG * kHqWG);
+        const uint32_t nsteps = (tiles + nwv - 1) / nwv;
+        k_head_q6k<kHqSlots, kHqWG><<<nwv / kHqWG, 64 * kHqWG, kHqWG * kHqSlots * kHqSlot, st>>>(
+            W.p, tiles, nsteps, x, norm_w, eps, logits, part);
+        k_argmax_final<<<1, 256, 0, st>>>(logits, part, nwv, out);
+        CK(hipGetLastError());
+        return 0;
+    }
     if (W.fmt < 0 || !fast_k(W.cols)) return 1;
     const uint32_t U = W.cols / 32, rps = 64 / U;
     if (W.rows % rps) return 1;
