@@ -100,8 +100,11 @@ def parse():
                          "without the profiler (PLAIN_JSON)")
     ap.add_argument("--summarize-counters", nargs="+", metavar="PMC_DIR",
                     help="print the mean per dispatch of every counter in these rocprofv3 --pmc "
-                         "csv outputs for each k_moe_/k_pre_ kernel as markdown (FETCH_SIZE and "
+                         "csv outputs for each k_moe_/k_pre_/k_head/k_argmax kernel as markdown (FETCH_SIZE and "
                          "WRITE_SIZE scaled by the --calib-copy copy kernel, when present)")
+    ap.add_argument("--summarize-stats", nargs="+", metavar="TRACE_DIR",
+                    help="print the k_ kernels' duration statistics of rocprofv3 --kernel-trace "
+                         "--stats outputs as markdown")
     ap.add_argument("--command", default="", help="command line recorded in the summary")
     return ap.parse_args()
 
@@ -172,7 +175,7 @@ def summarize_pmc(fetch_dir, write_dir, calib_mib, command):
 
 
 def _short_kernel(name):
-    n = name.replace("void ", "").replace("(anonymous namespace)::", "")
+    n = name.replace("void ", "").replace("(anonymous namespace)::", "").replace("qw6::", "")
     return n.split("(")[0]
 
 
@@ -188,7 +191,7 @@ def summarize_counters(dirs, calib_mib, command):
             if "MulFunctor" in k:
                 calib[c] = v
                 continue
-            if "k_moe_" not in k and "k_pre_" not in k:
+            if "k_moe_" not in k and "k_pre_" not in k and "k_head" not in k and "k_argmax" not in k:
                 continue
             table.setdefault(_short_kernel(k), {})[c] = (v, n)
     nbytes = calib_mib * 1024 * 1024
@@ -213,6 +216,30 @@ def summarize_counters(dirs, calib_mib, command):
             for k in sorted(table):
                 if c in table[k]:
                     print("- `%s`: %.0f B" % (k, table[k][c][0] * 1024.0 * fac))
+
+
+def summarize_stats(dirs, command):
+    """Markdown table of the k_* kernels' durations in rocprofv3 --kernel-trace
+    --stats outputs (one column group per trace directory, named by it)."""
+    print("Command (repository root R):\n\n```\n%s\n```\n" % command)
+    print("| Trace | Kernel | Dispatches | Avg us | Min us | Max us | Share of the trace's k_ kernel time |")
+    print("|---|---|---|---|---|---|---|")
+    for d in dirs:
+        files = glob.glob(os.path.join(d, "**", "*kernel_stats.csv"), recursive=True)
+        if not files:
+            raise SystemExit("no kernel_stats.csv under %s" % d)
+        rows = []
+        with open(files[0]) as fh:
+            for r in csv.DictReader(fh):
+                name = _short_kernel(r["Name"])
+                if name.startswith("k_") and not name.startswith("k_synth"):
+                    rows.append((name, int(r["Calls"]), float(r["TotalDurationNs"]),
+                                 float(r["AverageNs"]), float(r["MinNs"]), float(r["MaxNs"])))
+        tot = sum(x[2] for x in rows) or 1.0
+        for name, calls, total, avg, mn, mx in sorted(rows, key=lambda x: -x[2]):
+            print("| %s | `%s` | %d | %.2f | %.2f | %.2f | %.1f %% |"
+                  % (os.path.basename(d.rstrip("/")), name, calls, avg / 1e3, mn / 1e3, mx / 1e3,
+                     100.0 * total / tot))
 
 
 def summarize_trace(trace_dir, bench_json, command, plain_json=None):
@@ -717,6 +744,9 @@ def main():
         return
     if args.summarize_counters:
         summarize_counters(args.summarize_counters, args.calib_copy or 512, args.command)
+        return
+    if args.summarize_stats:
+        summarize_stats(args.summarize_stats, args.command)
         return
     if args.summarize_trace:
         st = args.summarize_trace
