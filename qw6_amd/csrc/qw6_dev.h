@@ -157,6 +157,35 @@ __device__ __forceinline__ uint32_t lds16(const uint32_t* s, uint32_t off) {
 __device__ __forceinline__ uint32_t lds8(const uint32_t* s, uint32_t off) {
     return (s[off >> 2] >> ((off & 3) * 8)) & 0xffu;
 }
+// Reads at R + c from an even LDS byte offset R (every staged block starts at
+// an even byte) with c a constant after inlining: R is kept as the word
+// indices and byte shifts of R and R + 2, so a read needs no address
+// arithmetic (the word is w0 + c / 4 or w2 + (c - 2) / 4, a ds_read offset)
+// and a dword one v_alignbyte. Build the cursor once per block with lds_row.
+struct LdsRow {
+    uint32_t w0, w2;   // (R >> 2), ((R + 2) >> 2)
+    uint32_t s0, s2;   // R & 3, (R + 2) & 3 (bytes: 0 or 2)
+};
+__device__ __forceinline__ LdsRow lds_row(uint32_t R) {
+    return LdsRow{R >> 2, (R + 2u) >> 2, R & 3u, (R + 2u) & 3u};
+}
+__device__ __forceinline__ uint32_t row_word(const LdsRow& r, uint32_t c) {   // c even
+    return (c & 2u) ? r.w2 + ((c - 2u) >> 2) : r.w0 + (c >> 2);
+}
+__device__ __forceinline__ uint32_t row_shift(const LdsRow& r, uint32_t c) {   // bytes
+    return ((c & 2u) ? r.s2 : r.s0) + (c & 1u);
+}
+__device__ __forceinline__ uint32_t rd32(const uint32_t* s, const LdsRow& r, uint32_t c) {   // c even
+    const uint32_t w = row_word(r, c);
+    return __builtin_amdgcn_alignbyte(s[w + 1], s[w], row_shift(r, c));
+}
+__device__ __forceinline__ uint32_t rd16(const uint32_t* s, const LdsRow& r, uint32_t c) {   // c even
+    return (s[row_word(r, c)] >> (8u * row_shift(r, c))) & 0xffffu;
+}
+__device__ __forceinline__ uint32_t rd8(const uint32_t* s, const LdsRow& r, uint32_t c) {
+    return (s[row_word(r, c & ~1u)] >> (8u * row_shift(r, c))) & 0xffu;
+}
+
 __device__ __forceinline__ uint64_t lds64_tab(const uint32_t* s, uint32_t off) {
     const uint2 v = *(const uint2*)(s + (off >> 2));   // 8-byte aligned table entry
     return (uint64_t)v.x | ((uint64_t)v.y << 32);

@@ -312,7 +312,7 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
     if constexpr (is_iq(F)) {
         float d[RT];
 #pragma unroll
-        for (int r = 0; r < RT; r++) d[r] = h2f(lds16(S.raw, R[r]));
+        for (int r = 0; r < RT; r++) d[r] = h2f(rd16(S.raw, lds_row(R[r]), 0));
 #pragma unroll 2
         for (int sb = 0; sb < 8; sb++) {
             uint4 b[RT];

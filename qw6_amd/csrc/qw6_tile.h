@@ -122,11 +122,12 @@ __device__ __forceinline__ void tile_scales(const uint32_t* s, uint32_t R, TileS
         ts.scw[0] = sc_lo;
         ts.scw[1] = sc_hi;
     } else {   // Q6_K: sub-block 4h + k uses scale 8h + 2k (qw6.c:1550-1578)
-        ts.d = h2f(lds16(s, R + 208));
+        const LdsRow row = lds_row(R);
+        ts.d = h2f(rd16(s, row, 208));
         ts.dmin = 0.f;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
-            const uint32_t w0 = lds32(s, R + 192 + 8 * h), w1 = lds32(s, R + 196 + 8 * h);
+            const uint32_t w0 = rd32(s, row, 192 + 8 * h), w1 = rd32(s, row, 196 + 8 * h);
             ts.scw[h] = __builtin_amdgcn_perm(w1, w0, 0x06040200u);   // bytes 0, 2 of w0, w1
             sc[4 * h + 0] = (float)(int8_t)(w0 & 0xffu);
             sc[4 * h + 1] = (float)(int8_t)((w0 >> 16) & 0xffu);
@@ -177,9 +178,10 @@ __device__ __forceinline__ void tile_codes(const uint32_t* s, uint32_t R, uint32
         // 64 h + l (a) and 64 h + 32 + l (b), low nibbles for i = 0, high for
         // i = 1; 2-bit fields 2k of qh byte 128 + 32 h + l (k = 2i, 2i + 1)
         const uint32_t h = (uint32_t)p >> 1, i = (uint32_t)p & 1u;
-        const uint32_t a0 = lds32(s, R + 64 * h + 8 * q), a1 = lds32(s, R + 64 * h + 8 * q + 4);
-        const uint32_t c0 = lds32(s, R + 64 * h + 32 + 8 * q), c1 = lds32(s, R + 64 * h + 36 + 8 * q);
-        const uint32_t x0 = lds32(s, R + 128 + 32 * h + 8 * q), x1 = lds32(s, R + 132 + 32 * h + 8 * q);
+        const LdsRow rq = lds_row(R + 8 * q);
+        const uint32_t a0 = rd32(s, rq, 64 * h), a1 = rd32(s, rq, 64 * h + 4);
+        const uint32_t c0 = rd32(s, rq, 64 * h + 32), c1 = rd32(s, rq, 64 * h + 36);
+        const uint32_t x0 = rd32(s, rq, 128 + 32 * h), x1 = rd32(s, rq, 132 + 32 * h);
         const uint32_t sh = 4 * i;   // nibble shift; also the qh shift 2k of k = 2i
         b0 = codes8(((a0 >> sh) & 0x0f0f0f0fu) | (((x0 >> sh) & 0x03030303u) << 4),
                     ((a1 >> sh) & 0x0f0f0f0fu) | (((x1 >> sh) & 0x03030303u) << 4));
@@ -248,8 +250,9 @@ __device__ __forceinline__ void tile_iq(const uint32_t* s, const uint8_t* tab, c
                                         uint32_t R, uint32_t q, int sb, float d, uint4& b,
                                         float& db, float& db2) {
     const uint4* sgn = (const uint4*)sgt;
+    const LdsRow row = lds_row(R);
     if (F == F_IQ2XXS) {   // 8 B per 32 weights: 4 grid indices, 4 x 7 sign bits + scale
-        const uint32_t aux0 = lds32(s, R + 2 + 8 * sb), aux1 = lds32(s, R + 6 + 8 * sb);
+        const uint32_t aux0 = rd32(s, row, 2 + 8 * sb), aux1 = rd32(s, row, 6 + 8 * sb);
         const uint32_t idx = (aux0 >> (8 * q)) & 255u;
         const uint32_t s7 = (aux1 >> (7 * q)) & 127u;
         const uint32_t sg = s7 | ((__builtin_popcount(s7) & 1u) << 7);   // ksigns_iq2xs
@@ -257,19 +260,20 @@ __device__ __forceinline__ void tile_iq(const uint32_t* s, const uint8_t* tab, c
         db = d * (0.5f + (float)(aux1 >> 28)) * 0.25f;
         db2 = db;
     } else if (F == F_IQ2S) {   // grid index: qs byte + 2 bits of qh; own sign byte
-        const uint32_t qsb = lds8(s, R + 2 + 4 * sb + q);
-        const uint32_t qh = lds8(s, R + 66 + sb);
-        const uint32_t sg = lds8(s, R + 34 + 4 * sb + q);
-        const uint32_t sc = lds8(s, R + 74 + sb);
+        const uint32_t qsb = (rd32(s, row, 2 + 4 * sb) >> (8 * q)) & 0xffu;
+        const uint32_t qh = rd8(s, row, 66 + sb);
+        const uint32_t sg = (rd32(s, row, 34 + 4 * sb) >> (8 * q)) & 0xffu;
+        const uint32_t sc = rd8(s, row, 74 + sb);
         const uint32_t gi = qsb | ((qh << (8 - 2 * q)) & 0x300u);
         b = xor4(((const uint4*)tab)[gi], sgn[sg]);
         db = d * (0.5f + (float)(sc & 15u)) * 0.25f;
         db2 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
     } else {   // IQ3_S: two 4-value grid entries per 8 weights, 9-bit indices
-        const uint32_t qw = lds32(s, R + 2 + 8 * sb + 4 * (q >> 1));
-        const uint32_t qh = lds8(s, R + 66 + sb);
-        const uint32_t sg = lds8(s, R + 74 + 4 * sb + q);
-        const uint32_t scb = lds8(s, R + 106 + (sb >> 1));
+        const LdsRow rq = lds_row(R + 4 * (q >> 1));
+        const uint32_t qw = rd32(s, rq, 2 + 8 * sb);
+        const uint32_t qh = rd8(s, row, 66 + sb);
+        const uint32_t sg = (rd32(s, row, 74 + 4 * sb) >> (8 * q)) & 0xffu;
+        const uint32_t scb = rd8(s, row, 106 + (sb >> 1));
         const uint32_t nib = (sb & 1) ? (scb >> 4) : (scb & 15u);
         const uint32_t sh = 16 * (q & 1u);
         const uint32_t i1 = ((qw >> sh) & 255u) | ((qh << (8 - 2 * q)) & 256u);
@@ -293,7 +297,7 @@ __device__ __forceinline__ void mx_block(const uint32_t* s, const uint8_t* grid,
                                          const uint4& c0, const uint4& c1, f32x4& acc) {
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
     if constexpr (is_iq(F)) {
-        const float d = h2f(lds16(s, R));
+        const float d = h2f(rd16(s, lds_row(R), 0));
 #pragma unroll
         for (int sb = 0; sb < 8; sb++) {
             uint4 b;
