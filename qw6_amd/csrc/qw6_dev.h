@@ -372,13 +372,13 @@ __device__ __forceinline__ void unit_q6k(const uint32_t* s, uint32_t bo, int j,
                                          const float (&xr)[T][32], const float (&sx)[T][4],
                                          float (&acc)[T]) {
     const int h = j >> 2, lq = j & 3;
-    const uint32_t oa = bo + 64 * h + 8 * lq;
-    const uint32_t a0 = lds32(s, oa), a1 = lds32(s, oa + 4);
-    const uint32_t b0 = lds32(s, oa + 32), b1 = lds32(s, oa + 36);
-    const uint32_t oh = bo + 128 + 32 * h + 8 * lq;
-    const uint32_t h0 = lds32(s, oh), h1 = lds32(s, oh + 4);
-    const uint32_t sc0 = lds32(s, bo + 192 + 8 * h), sc1 = lds32(s, bo + 196 + 8 * h);
-    const float d = h2f(lds16(s, bo + 208));
+    const LdsRow ra = lds_row(bo + 64 * h + 8 * lq), rh = lds_row(bo + 128 + 32 * h + 8 * lq);
+    const LdsRow rs = lds_row(bo + 8 * h), rb = lds_row(bo);
+    const uint32_t a0 = rd32(s, ra, 0), a1 = rd32(s, ra, 4);
+    const uint32_t b0 = rd32(s, ra, 32), b1 = rd32(s, ra, 36);
+    const uint32_t h0 = rd32(s, rh, 0), h1 = rd32(s, rh, 4);
+    const uint32_t sc0 = rd32(s, rs, 192), sc1 = rd32(s, rs, 196);
+    const float d = h2f(rd16(s, rb, 208));
     const float sc[4] = {(float)(int8_t)(sc0 & 0xff), (float)(int8_t)((sc0 >> 16) & 0xff),
                          (float)(int8_t)(sc1 & 0xff), (float)(int8_t)((sc1 >> 16) & 0xff)};
     const uint32_t aw[2] = {a0, a1}, bw[2] = {b0, b1}, hw[2] = {h0, h1};
@@ -418,8 +418,9 @@ template <int T>
 __device__ __forceinline__ void unit_iq2xxs(const uint32_t* s, uint32_t bo, int j,
                                             const uint32_t* tab, const float (&xr)[T][32],
                                             float (&acc)[T]) {
-    const uint32_t aux0 = lds32(s, bo + 2 + 8 * j), aux1 = lds32(s, bo + 6 + 8 * j);
-    const float d = h2f(lds16(s, bo));
+    const LdsRow rj = lds_row(bo + 8 * j);
+    const uint32_t aux0 = rd32(s, rj, 2), aux1 = rd32(s, rj, 6);
+    const float d = h2f(rd16(s, lds_row(bo), 0));
     const float db = d * (0.5f + (float)(aux1 >> 28)) * 0.25f;
     float sum[T];
 #pragma unroll
@@ -446,9 +447,10 @@ template <int T>
 __device__ __forceinline__ void unit_iq2s(const uint32_t* s, uint32_t bo, int j,
                                           const uint32_t* tab, const float (&xr)[T][32],
                                           float (&acc)[T]) {
-    const uint32_t qs4 = lds32(s, bo + 2 + 4 * j), sg4 = lds32(s, bo + 34 + 4 * j);
+    const LdsRow rj = lds_row(bo + 4 * j), rb = lds_row(bo);
+    const uint32_t qs4 = rd32(s, rj, 2), sg4 = rd32(s, rj, 34);
     const uint32_t qh = lds8(s, bo + 66 + j), sc = lds8(s, bo + 74 + j);
-    const float d = h2f(lds16(s, bo));
+    const float d = h2f(rd16(s, rb, 0));
     const float db0 = d * (0.5f + (float)(sc & 0xf)) * 0.25f;
     const float db1 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
     float s0[T], s1[T];
@@ -480,12 +482,13 @@ template <int T>
 __device__ __forceinline__ void unit_iq3s(const uint32_t* s, uint32_t bo, int j,
                                           const uint32_t* tab, const float (&xr)[T][32],
                                           float (&acc)[T]) {
-    const uint32_t qa = lds32(s, bo + 2 + 8 * j), qb = lds32(s, bo + 6 + 8 * j);
+    const LdsRow r8 = lds_row(bo + 8 * j), r4 = lds_row(bo + 4 * j);
+    const uint32_t qa = rd32(s, r8, 2), qb = rd32(s, r8, 6);
     const uint32_t qh = lds8(s, bo + 66 + j);
-    const uint32_t sg4 = lds32(s, bo + 74 + 4 * j);
+    const uint32_t sg4 = rd32(s, r4, 74);
     const uint32_t scb = lds8(s, bo + 106 + (j >> 1));
     const uint32_t nib = (j & 1) ? (scb >> 4) : (scb & 0xf);
-    const float d = h2f(lds16(s, bo));
+    const float d = h2f(rd16(s, lds_row(bo), 0));
     const float db = d * (float)(1 + 2 * (int)nib);
     float sum[T];
 #pragma unroll
