@@ -197,3 +197,36 @@ def test_output_greedy_other_shapes(torch_dev, ctx, hidden, rows):
     olog = O.matvec(q, w, rows, hidden, O.rmsnorm(x, nw, 1e-6))
     assert cases.rel_l2(glog, olog) <= TOL
     assert gtok == O.argmax(glog)
+
+
+@pytest.mark.parametrize("rows,offset", [(4008, 0), (4096, 2), (1600, 0)])
+def test_output_greedy_q6k_2048_dispatch(torch_dev, ctx, rows, offset):
+    """Q6_K rows of 2048 columns either side of the bf16-MFMA head's
+    conditions: 4008 rows (not a multiple of its 16-row tiles) take the fp32
+    kernel, 1600 rows (100 tiles, a small grid) the MFMA kernel; logits and
+    token against the oracle. Weight data 2 bytes past 16-byte alignment is
+    refused before any launch (the matrix contract)."""
+    torch = torch_dev
+    q = S.Q_Q6_K
+    w = S.quant_matrix(44, S.stream_id(2, S.K_OUTPUT), q, rows, HIDDEN)
+    buf = torch.zeros(w.nbytes + 16, dtype=torch.uint8, device="cuda")
+    buf[offset:offset + w.nbytes] = torch.from_numpy(np.ascontiguousarray(w).view(np.uint8)).cuda()
+    x = cases.token_x(45, 0)
+    nw = S.f32_normal(46, S.stream_id(2, S.K_ONORM), HIDDEN, 0.1, mean=1.0)
+    dx, dn = torch.from_numpy(x).cuda(), torch.from_numpy(nw).cuda()
+    logits = torch.zeros(rows, dtype=torch.float32, device="cuda")
+    tok = torch.zeros(1, dtype=torch.int32, device="cuda")
+    if offset % 16:
+        with pytest.raises(Q.Qw6HipError, match="aligned"):
+            ctx.output_greedy((buf.data_ptr() + offset, q, rows, HIDDEN), dx, logits, tok, norm_w=dn, eps=1e-6)
+        return
+    ctx.output_greedy((buf.data_ptr() + offset, q, rows, HIDDEN), dx, logits, tok, norm_w=dn, eps=1e-6)
+    torch.cuda.synchronize()
+    glog = logits.cpu().numpy()
+    gtok = int(tok.cpu().numpy().view(np.uint32)[0])
+    olog = O.matvec(q, w, rows, HIDDEN, O.rmsnorm(x, nw, 1e-6))
+    rel = cases.rel_l2(glog, olog)
+    say("Q6_K x 2048, %d rows, offset %d: rel-L2 %.2e" % (rows, offset, rel))
+    assert rel <= TOL
+    assert gtok == O.argmax(glog)
+
