@@ -1154,15 +1154,15 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
 // the weights' per-lane decode work (qw6_tile.h) no longer grows with T, and
 // the registers no longer hold every token's activations.
 
-// LDS of the bf16 lattice tables of the IQ formats in a fmt_table_mask: the
-// 256 sign masks, then the grids present (IQ2_XXS, IQ2_S, IQ3_S).
+// LDS of the bf16 lattice grids of the IQ formats in a fmt_table_mask, the
+// grids present in the order IQ2_XXS, IQ2_S, IQ3_S (signs are computed).
 struct MxTab {
     uint32_t g[3];
     uint32_t bytes;
 };
 __host__ __device__ inline MxTab mx_tab(uint32_t mask) {
     MxTab t;
-    uint32_t o = mask ? 4096u : 0u;
+    uint32_t o = 0u;
     const uint32_t gb[3] = {256u * 16u, 1024u * 16u, 512u * 8u};
     for (int i = 0; i < 3; i++) {
         t.g[i] = o;
@@ -1174,7 +1174,6 @@ __host__ __device__ inline MxTab mx_tab(uint32_t mask) {
 __device__ __forceinline__ void stage_mx_tables(uint8_t* tab, uint32_t mask, uint32_t nthr) {
     if (!mask) return;
     const MxTab tb = mx_tab(mask);
-    stage_iq_signs(tab, nthr);
     if (mask & 1u) stage_iq_grid<F_IQ2XXS>(tab + tb.g[0], g_tabs, nthr);
     if (mask & 2u) stage_iq_grid<F_IQ2S>(tab + tb.g[1], g_tabs, nthr);
     if (mask & 4u) stage_iq_grid<F_IQ3S>(tab + tb.g[2], g_tabs, nthr);
@@ -1230,12 +1229,12 @@ __device__ __forceinline__ void mx_block_fmt(int f, const uint32_t* s, const uin
                                              uint32_t R, uint32_t q, const uint4 (&av)[8], const uint4& c0,
                                              const uint4& c1, f32x4& acc) {
     switch (f) {
-    case F_Q4K: mx_block<F_Q4K>(s, tab, tab, R, q, av, c0, c1, acc); break;
-    case F_Q5K: mx_block<F_Q5K>(s, tab, tab, R, q, av, c0, c1, acc); break;
-    case F_Q6K: mx_block<F_Q6K>(s, tab, tab, R, q, av, c0, c1, acc); break;
-    case F_IQ2XXS: mx_block<F_IQ2XXS>(s, tab + tb.g[0], tab, R, q, av, c0, c1, acc); break;
-    case F_IQ2S: mx_block<F_IQ2S>(s, tab + tb.g[1], tab, R, q, av, c0, c1, acc); break;
-    default: mx_block<F_IQ3S>(s, tab + tb.g[2], tab, R, q, av, c0, c1, acc); break;
+    case F_Q4K: mx_block<F_Q4K>(s, tab, R, q, av, c0, c1, acc); break;
+    case F_Q5K: mx_block<F_Q5K>(s, tab, R, q, av, c0, c1, acc); break;
+    case F_Q6K: mx_block<F_Q6K>(s, tab, R, q, av, c0, c1, acc); break;
+    case F_IQ2XXS: mx_block<F_IQ2XXS>(s, tab + tb.g[0], R, q, av, c0, c1, acc); break;
+    case F_IQ2S: mx_block<F_IQ2S>(s, tab + tb.g[1], R, q, av, c0, c1, acc); break;
+    default: mx_block<F_IQ3S>(s, tab + tb.g[2], R, q, av, c0, c1, acc); break;
     }
 }
 
@@ -1314,9 +1313,9 @@ __device__ __forceinline__ void mx_gu_blocks(const MoeArgs& a, const MatD& Gm, c
         const uint32_t Rg = mx_row_off(so + 2 * i * SB, g0, Gm.rb, kb * bb, n, FW);
         const uint32_t Ru = mx_row_off(so + (2 * i + 1) * SB, u0, Um.rb, kb * bb, n, FW);
         const uint8_t* grid = smem + tb.g[FW >= F_IQ2XXS ? FW - F_IQ2XXS : 0];
-        mx_block<FW>((const uint32_t*)smem, grid, smem, Rg, q, av, c0, c1, ag);
+        mx_block<FW>((const uint32_t*)smem, grid, Rg, q, av, c0, c1, ag);
         __builtin_amdgcn_sched_barrier(0);   // gate then up: one block's temporaries live at a time
-        mx_block<FW>((const uint32_t*)smem, grid, smem, Ru, q, av, c0, c1, au);
+        mx_block<FW>((const uint32_t*)smem, grid, Ru, q, av, c0, c1, au);
     }
 }
 

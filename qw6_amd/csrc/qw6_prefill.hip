@@ -309,6 +309,62 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
                                            const uint4& sxa, f32x4 (&acc)[RT]) {
     constexpr float bias = F == F_Q6K ? 160.f : 128.f;
     const uint32_t q = lane >> 4;
+    if constexpr (F == F_IQ2XXS) {
+        // Software pipeline over the sub-blocks: the grid reads of every row
+        // tile are issued together (the signs are computed), and the 3 words
+        // holding the next sub-block's 8 bytes (4 grid indices, 4 x 7 sign
+        // bits, scale: bytes 2 + 8 sb of the 2-byte-aligned block) load while
+        // this one's products run. db = d (0.5 + s) / 4 as one fma of exact terms.
+        const uint4* grid = (const uint4*)tab;
+        uint32_t wb[RT], sh[RT], w[RT][3];
+        float d4[RT], d8[RT];
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const LdsRow row = lds_row(R[r]);
+            const float d = h2f(rd16(S.raw, row, 0));
+            d4[r] = 0.25f * d;
+            d8[r] = 0.125f * d;
+            wb[r] = row.w2;
+            sh[r] = row.s2;
+#pragma unroll
+            for (int k = 0; k < 3; k++) w[r][k] = S.raw[wb[r] + k];
+        }
+#pragma unroll
+        for (int sb = 0; sb < 8; sb++) {
+            uint4 g[RT];
+            uint32_t sg[RT];
+            float db[RT];
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const uint32_t aux0 = __builtin_amdgcn_alignbyte(w[r][1], w[r][0], sh[r]);
+                const uint32_t aux1 = __builtin_amdgcn_alignbyte(w[r][2], w[r][1], sh[r]);
+                const uint32_t idx = (aux0 >> (8 * q)) & 255u;
+                const uint32_t s7 = (aux1 >> (7 * q)) & 127u;
+                g[r] = grid[idx];
+                sg[r] = sign_pairs7(s7);
+                db[r] = fmaf((float)(aux1 >> 28), d4[r], d8[r]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const uint4 ah = S.a[0][sb][lane], al = S.a[1][sb][lane];
+            if (sb < 7) {
+#pragma unroll
+                for (int r = 0; r < RT; r++) {
+#pragma unroll
+                    for (int k = 0; k < 3; k++) w[r][k] = S.raw[wb[r] + 2 * (sb + 1) + k];
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const uint4 b = apply_signs(g[r], sg[r]);
+                f32x4 c = mfma(ah, b, f32x4{0.f, 0.f, 0.f, 0.f});
+                c = mfma(al, b, c);
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[r][j] = fmaf(db[r], c[j], acc[r][j]);
+            }
+        }
+        return;
+    }
     if constexpr (is_iq(F)) {
         float d[RT];
 #pragma unroll
@@ -319,7 +375,7 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
             float db[RT], db2[RT];
 #pragma unroll
             for (int r = 0; r < RT; r++)
-                tile_iq<F>(S.raw, tab, tab + iq_grid_bytes(F), R[r], q, sb, d[r], b[r], db[r], db2[r]);
+                tile_iq<F>(S.raw, tab, R[r], q, sb, d[r], b[r], db[r], db2[r]);
             const uint4 ah = S.a[0][sb][lane], al = S.a[1][sb][lane];
 #pragma unroll
             for (int r = 0; r < RT; r++) {
@@ -446,7 +502,7 @@ __host__ __device__ inline uint32_t gemm_ny(uint32_t hidden, uint32_t inter) {  
 }
 template <int MODE, int F>
 __host__ __device__ constexpr size_t gemm_lds() {
-    return offsetof(GemmLds, raw) + (size_t)64 * gemm_rt<MODE, F>() * raw_chunks(F) * 16 + iq_tab_bytes(F);
+    return offsetof(GemmLds, raw) + (size_t)64 * gemm_rt<MODE, F>() * raw_chunks(F) * 16 + iq_grid_bytes(F);
 }
 
 // Row block yb of tile `tile` (format F).
@@ -528,8 +584,8 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
     }
     if constexpr (kAl) rowp[0] = nullptr;
     u32x4 rawv[NR], av[4], sxv;
-    uint8_t* tab = (uint8_t*)S.raw + (size_t)NR * kPWG * 16;   // IQ lattice tables
-    if constexpr (is_iq(F)) stage_iq_tables<F>(tab, g_tabs_pre, kPWG);   // visible after the loop's first barrier
+    uint8_t* tab = (uint8_t*)S.raw + (size_t)NR * kPWG * 16;   // IQ lattice grid
+    if constexpr (is_iq(F)) stage_iq_grid<F>(tab, g_tabs_pre, kPWG);   // visible after the loop's first barrier
     f32x4 acc[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};

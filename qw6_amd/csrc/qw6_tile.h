@@ -31,14 +31,10 @@ __host__ __device__ constexpr uint32_t raw_chunks(int f) {
 __host__ __device__ constexpr bool is_iq(int f) {
     return f == F_IQ2XXS || f == F_IQ2S || f == F_IQ3S;
 }
-// LDS of the bf16 lattice tables of an IQ format: the grid (8 or 4 values
-// per entry, 16 or 8 B) then 256 sign masks (16 B: bit j of the sign byte ->
-// the sign bit of bf16 value j).
+// LDS of the bf16 lattice grid of an IQ format (8 or 4 values per entry,
+// 16 or 8 B); the signs are applied in registers (apply_signs).
 __host__ __device__ constexpr uint32_t iq_grid_bytes(int f) {
     return f == F_IQ2XXS ? 256 * 16 : f == F_IQ2S ? 1024 * 16 : f == F_IQ3S ? 512 * 8 : 0;
-}
-__host__ __device__ constexpr uint32_t iq_tab_bytes(int f) {
-    return is_iq(f) ? iq_grid_bytes(f) + 256 * 16 : 0;
 }
 
 // ---- bf16 operand preparation -----------------------------------------------------
@@ -195,10 +191,9 @@ __device__ __forceinline__ void tile_codes(const uint32_t* s, uint32_t R, uint32
 // exact in bf16, and every weight is db * (+-value): the B operand is the
 // bf16 grid entry with the sign bits flipped, with no bias or minimum term.
 
-// Expand the lattice tables of format F into LDS as bf16: the grid at `grid`
-// (8 or 4 values per entry, 16 or 8 B), and (with sgn set) the 256 sign masks
-// at `sgn` (16 B: bit j of the sign byte -> the sign bit of bf16 value j).
-// All nthr threads of the workgroup take part; g: the format's lattice tables.
+// Expand the lattice grid of format F into LDS as bf16 at `grid` (8 or 4
+// values per entry, 16 or 8 B). All nthr threads of the workgroup take part;
+// g: the lattice tables.
 template <int F>
 __device__ __forceinline__ void stage_iq_grid(uint8_t* grid, const IqTables& g, uint32_t nthr) {
     const uint32_t tid = threadIdx.x;
@@ -222,41 +217,49 @@ __device__ __forceinline__ void stage_iq_grid(uint8_t* grid, const IqTables& g, 
         }
     }
 }
-__device__ __forceinline__ void stage_iq_signs(uint8_t* sgn, uint32_t nthr) {
-    for (uint32_t s8 = threadIdx.x; s8 < 256; s8 += nthr) {
-        uint32_t w[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++)
-            w[k] = (((s8 >> (2 * k)) & 1u) << 15) | (((s8 >> (2 * k + 1)) & 1u) << 31);
-        ((uint4*)sgn)[s8] = u4(w[0], w[1], w[2], w[3]);
-    }
-}
-// Grid then sign masks, contiguous (one IQ format).
-template <int F>
-__device__ __forceinline__ void stage_iq_tables(uint8_t* tab, const IqTables& g, uint32_t nthr) {
-    stage_iq_grid<F>(tab, g, nthr);
-    stage_iq_signs(tab + iq_grid_bytes(F), nthr);
-}
 
 __device__ __forceinline__ uint4 xor4(const uint4& a, const uint4& b) {
     return u4(a.x ^ b.x, a.y ^ b.y, a.z ^ b.z, a.w ^ b.w);
 }
 
+// Signs of 8 bf16 values g (value h: 16-bit half h of g) from bits 0-7 of
+// both 16-bit halves of y (bit h -> value h): the halves of word k shift by
+// 15 - 2k and 14 - 2k (one packed 16-bit shift), which puts bit 2k, 2k + 1
+// on bits 15, 31; bits that leave a half are dropped and the rest masked off.
+// Bits 8-15 of a half shift out for every k, so they may hold anything.
+typedef unsigned short us2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint4 apply_signs(const uint4& g, uint32_t y) {
+    const us2_t v = __builtin_bit_cast(us2_t, y);
+    uint32_t m[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const us2_t sh = {(unsigned short)(15 - 2 * k), (unsigned short)(14 - 2 * k)};
+        m[k] = __builtin_bit_cast(uint32_t, (us2_t)(v << sh)) & 0x80008000u;
+    }
+    return u4(g.x ^ m[0], g.y ^ m[1], g.z ^ m[2], g.w ^ m[3]);
+}
+// y for apply_signs from a sign byte s8 (bits 8+ of s8 may be set), and from
+// IQ2_XXS's 7 stored bits s7, whose eighth is their parity (ksigns_iq2xs):
+// the popcount lands on bits 23-25, its low bit on bit 7 of the high half;
+// the low half's bit 7 goes to no value (even values take bits 0, 2, 4, 6).
+__device__ __forceinline__ uint32_t sign_pairs(uint32_t s8) { return s8 | (s8 << 16); }
+__device__ __forceinline__ uint32_t sign_pairs7(uint32_t s7) {
+    return s7 | (s7 << 16) | ((uint32_t)__builtin_popcount(s7) << 23);
+}
+
 // B operand of sub-block sb of row n (this lane's 8 weights, group q of the
-// sub-block; tab: the bf16 grid, sgt: the sign masks) and its scale(s): db for all 32 weights, or (IQ2_S) db for
-// groups 0-1 and db2 for groups 2-3 (qw6.c:1580-1672).
+// sub-block; tab: the bf16 grid) and its scale(s): db for all 32 weights, or
+// (IQ2_S) db for groups 0-1 and db2 for groups 2-3 (qw6.c:1580-1672).
 template <int F>
-__device__ __forceinline__ void tile_iq(const uint32_t* s, const uint8_t* tab, const uint8_t* sgt,
+__device__ __forceinline__ void tile_iq(const uint32_t* s, const uint8_t* tab,
                                         uint32_t R, uint32_t q, int sb, float d, uint4& b,
                                         float& db, float& db2) {
-    const uint4* sgn = (const uint4*)sgt;
     const LdsRow row = lds_row(R);
     if (F == F_IQ2XXS) {   // 8 B per 32 weights: 4 grid indices, 4 x 7 sign bits + scale
         const uint32_t aux0 = rd32(s, row, 2 + 8 * sb), aux1 = rd32(s, row, 6 + 8 * sb);
         const uint32_t idx = (aux0 >> (8 * q)) & 255u;
         const uint32_t s7 = (aux1 >> (7 * q)) & 127u;
-        const uint32_t sg = s7 | ((__builtin_popcount(s7) & 1u) << 7);   // ksigns_iq2xs
-        b = xor4(((const uint4*)tab)[idx], sgn[sg]);
+        b = apply_signs(((const uint4*)tab)[idx], sign_pairs7(s7));
         db = d * (0.5f + (float)(aux1 >> 28)) * 0.25f;
         db2 = db;
     } else if (F == F_IQ2S) {   // grid index: qs byte + 2 bits of qh; own sign byte
@@ -265,7 +268,7 @@ __device__ __forceinline__ void tile_iq(const uint32_t* s, const uint8_t* tab, c
         const uint32_t sg = (rd32(s, row, 34 + 4 * sb) >> (8 * q)) & 0xffu;
         const uint32_t sc = rd8(s, row, 74 + sb);
         const uint32_t gi = qsb | ((qh << (8 - 2 * q)) & 0x300u);
-        b = xor4(((const uint4*)tab)[gi], sgn[sg]);
+        b = apply_signs(((const uint4*)tab)[gi], sign_pairs(sg));
         db = d * (0.5f + (float)(sc & 15u)) * 0.25f;
         db2 = d * (0.5f + (float)(sc >> 4)) * 0.25f;
     } else {   // IQ3_S: two 4-value grid entries per 8 weights, 9-bit indices
@@ -279,7 +282,7 @@ __device__ __forceinline__ void tile_iq(const uint32_t* s, const uint8_t* tab, c
         const uint32_t i1 = ((qw >> sh) & 255u) | ((qh << (8 - 2 * q)) & 256u);
         const uint32_t i2 = ((qw >> (sh + 8)) & 255u) | ((qh << (7 - 2 * q)) & 256u);
         const uint2 g1 = ((const uint2*)tab)[i1], g2 = ((const uint2*)tab)[i2];
-        b = xor4(u4(g1.x, g1.y, g2.x, g2.y), sgn[sg]);
+        b = apply_signs(u4(g1.x, g1.y, g2.x, g2.y), sign_pairs(sg));
         db = d * (float)(1 + 2 * (int)nib);
         db2 = db;
     }
@@ -292,7 +295,7 @@ __device__ __forceinline__ void tile_iq(const uint32_t* s, const uint8_t* tab, c
 // sub-blocks (3-part half-sums in k-slots 8 part + j, zero elsewhere).
 // acc += the block's contribution to D[m][n], this lane's rows m = 4 q + i.
 template <int F>
-__device__ __forceinline__ void mx_block(const uint32_t* s, const uint8_t* grid, const uint8_t* sgn,
+__device__ __forceinline__ void mx_block(const uint32_t* s, const uint8_t* grid,
                                          uint32_t R, uint32_t q, const uint4 (&a)[8],
                                          const uint4& c0, const uint4& c1, f32x4& acc) {
     const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
@@ -302,7 +305,7 @@ __device__ __forceinline__ void mx_block(const uint32_t* s, const uint8_t* grid,
         for (int sb = 0; sb < 8; sb++) {
             uint4 b;
             float db, db2;
-            tile_iq<F>(s, grid, sgn, R, q, sb, d, b, db, db2);
+            tile_iq<F>(s, grid, R, q, sb, d, b, db, db2);
             if (F == F_IQ2S) {   // scales per 16 weights: groups 0-1, then 2-3
                 const uint4 z = u4(0, 0, 0, 0);
                 const f32x4 c = mfma(a[sb], q < 2 ? b : z, z4);
