@@ -365,6 +365,119 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
         }
         return;
     }
+    if constexpr (F == F_IQ3S) {
+        // The same pipeline over IQ3_S's bytes, read as bytes (the LDS unit
+        // extracts them): for group q of sub-block sb, grid index bytes
+        // 2 + 8 sb + 2q, +1 (two 4-value entries), the high index bits at byte
+        // 66 + sb (bits 2q, 2q + 1), the sign byte 74 + 4 sb + q and the scale
+        // nibble of byte 106 + sb / 2; db = d (1 + 2 s) as one fma.
+        const uint8_t* rb = (const uint8_t*)S.raw;
+        const uint2* grid = (const uint2*)tab;
+        uint32_t qa[RT], qb[RT], qh[RT], sg[RT], sc[RT];
+        float d[RT], d2[RT];
+        const uint32_t s1 = 8u - 2u * q, s2 = 7u - 2u * q;
+        auto load = [&](int sb) {
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                qa[r] = rb[R[r] + 2 + 8 * sb + 2 * q];
+                qb[r] = rb[R[r] + 3 + 8 * sb + 2 * q];
+                qh[r] = rb[R[r] + 66 + sb];
+                sg[r] = rb[R[r] + 74 + 4 * sb + q];
+                if ((sb & 1) == 0) sc[r] = rb[R[r] + 106 + sb / 2];
+            }
+        };
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            d[r] = h2f(rd16(S.raw, lds_row(R[r]), 0));
+            d2[r] = 2.f * d[r];
+        }
+        load(0);
+#pragma unroll
+        for (int sb = 0; sb < 8; sb++) {
+            uint2 g1[RT], g2[RT];
+            uint32_t y[RT];
+            float db[RT];
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                g1[r] = grid[qa[r] | ((qh[r] << s1) & 256u)];
+                g2[r] = grid[qb[r] | ((qh[r] << s2) & 256u)];
+                y[r] = sign_pairs(sg[r]);
+                const uint32_t nib = (sb & 1) ? sc[r] >> 4 : sc[r] & 15u;
+                db[r] = fmaf((float)nib, d2[r], d[r]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const uint4 ah = S.a[0][sb][lane], al = S.a[1][sb][lane];
+            if (sb < 7) load(sb + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const uint4 b = apply_signs(u4(g1[r].x, g1[r].y, g2[r].x, g2[r].y), y[r]);
+                f32x4 c = mfma(ah, b, f32x4{0.f, 0.f, 0.f, 0.f});
+                c = mfma(al, b, c);
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[r][j] = fmaf(db[r], c[j], acc[r][j]);
+            }
+        }
+        return;
+    }
+    if constexpr (F == F_IQ2S) {
+        // The same pipeline over IQ2_S's bytes: for group q of sub-block sb,
+        // the grid index byte 2 + 4 sb + q with bits 2q, 2q + 1 of byte
+        // 66 + sb above it, the sign byte 34 + 4 sb + q, and byte 74 + sb
+        // holding the scales of groups 0-1 (low nibble) and 2-3 (high). The
+        // two scales take one MFMA pair each, over B with the other groups
+        // zeroed; db = d (0.5 + s) / 4 as one fma.
+        const uint8_t* rb = (const uint8_t*)S.raw;
+        const uint4* grid = (const uint4*)tab;
+        uint32_t qs[RT], qh[RT], sg[RT], sc[RT];
+        float d4[RT], d8[RT];
+        const uint32_t s1 = 8u - 2u * q;
+        auto load = [&](int sb) {
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                qs[r] = rb[R[r] + 2 + 4 * sb + q];
+                sg[r] = rb[R[r] + 34 + 4 * sb + q];
+                qh[r] = rb[R[r] + 66 + sb];
+                sc[r] = rb[R[r] + 74 + sb];
+            }
+        };
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            const float d = h2f(rd16(S.raw, lds_row(R[r]), 0));
+            d4[r] = 0.25f * d;
+            d8[r] = 0.125f * d;
+        }
+        load(0);
+#pragma unroll
+        for (int sb = 0; sb < 8; sb++) {
+            uint4 g[RT];
+            uint32_t y[RT];
+            float db[RT], db2[RT];
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                g[r] = grid[qs[r] | ((qh[r] << s1) & 0x300u)];
+                y[r] = sign_pairs(sg[r]);
+                db[r] = fmaf((float)(sc[r] & 15u), d4[r], d8[r]);
+                db2[r] = fmaf((float)(sc[r] >> 4), d4[r], d8[r]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const uint4 ah = S.a[0][sb][lane], al = S.a[1][sb][lane];
+            if (sb < 7) load(sb + 1);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const uint4 b = apply_signs(g[r], y[r]), z = u4(0, 0, 0, 0);
+                const uint4 b0 = q < 2 ? b : z, b1 = q < 2 ? z : b;
+                f32x4 c = mfma(ah, b0, f32x4{0.f, 0.f, 0.f, 0.f});
+                c = mfma(al, b0, c);
+                f32x4 c1 = mfma(ah, b1, f32x4{0.f, 0.f, 0.f, 0.f});
+                c1 = mfma(al, b1, c1);
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[r][j] = fmaf(db2[r], c1[j], fmaf(db[r], c[j], acc[r][j]));
+            }
+        }
+        return;
+    }
     if constexpr (is_iq(F)) {
         float d[RT];
 #pragma unroll
