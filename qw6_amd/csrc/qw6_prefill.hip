@@ -613,9 +613,13 @@ __host__ __device__ inline uint32_t gemm_ny(uint32_t hidden, uint32_t inter) {  
     constexpr int RT = gemm_rt<MODE, F>();
     return MODE == 0 ? inter / (32 * RT) : hidden / (64 * RT);
 }
+// LDS row stride of the staged raw blocks in 16-byte chunks: one more than
+// a row needs where that many would put the 16 rows of a row tile on two of
+// the 64 banks (IQ3_S: 8 chunks, 128 bytes; 9 spread them over all 16).
+__host__ __device__ constexpr uint32_t raw_stride(int f) { return raw_chunks(f) + (f == F_IQ3S ? 1u : 0u); }
 template <int MODE, int F>
 __host__ __device__ constexpr size_t gemm_lds() {
-    return offsetof(GemmLds, raw) + (size_t)64 * gemm_rt<MODE, F>() * raw_chunks(F) * 16 + iq_grid_bytes(F);
+    return offsetof(GemmLds, raw) + (size_t)64 * gemm_rt<MODE, F>() * raw_stride(F) * 16 + iq_grid_bytes(F);
 }
 
 // Row block yb of tile `tile` (format F).
@@ -634,6 +638,7 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
     constexpr uint32_t bb = fmt_block_bytes(F);
     constexpr uint32_t ROWS = 64 * RT;            // weight rows staged per block
     constexpr uint32_t NR = ROWS * NCH / kPWG;    // raw chunks per thread
+    constexpr uint32_t RS = raw_stride(F);        // LDS row stride in chunks
     static_assert(ROWS * NCH % kPWG == 0, "raw chunks split evenly over the threads");
     const uint32_t rb = nblk * bb;
     const uint32_t r0 = yb * (MODE == 0 ? 32u * RT : 64u * RT);
@@ -697,7 +702,7 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
     }
     if constexpr (kAl) rowp[0] = nullptr;
     u32x4 rawv[NR], av[4], sxv;
-    uint8_t* tab = (uint8_t*)S.raw + (size_t)NR * kPWG * 16;   // IQ lattice grid
+    uint8_t* tab = (uint8_t*)S.raw + (size_t)ROWS * RS * 16;   // IQ lattice grid
     if constexpr (is_iq(F)) stage_iq_grid<F>(tab, g_tabs_pre, kPWG);   // visible after the loop's first barrier
     f32x4 acc[RT];
 #pragma unroll
@@ -706,7 +711,10 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
     for (uint32_t kb = 0; kb < nblk; kb++) {
         __syncthreads();   // every wave is done with block kb - 1's LDS data
 #pragma unroll
-        for (uint32_t i = 0; i < NR; i++) *(u32x4*)((uint8_t*)S.raw + 16u * (i * kPWG + tid)) = rawv[i];
+        for (uint32_t i = 0; i < NR; i++) {
+            const uint32_t c = i * kPWG + tid;
+            *(u32x4*)((uint8_t*)S.raw + 16u * (c / NCH * RS + c % NCH)) = rawv[i];
+        }
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) *(u32x4*)&S.a[hl][sb0 + i][lane] = av[i];
         const uint4 sxa = q < 3 ? u4(sxv.x, sxv.y, sxv.z, sxv.w) : u4(0, 0, 0, 0);
@@ -715,7 +723,7 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
         uint32_t R[RT];
 #pragma unroll
         for (int r = 0; r < RT; r++)
-            R[r] = rrow[r] * NCH * 16 +
+            R[r] = rrow[r] * RS * 16 +
                    (kAl ? 0u : (uint32_t)((uintptr_t)(row_ptr(rrow[r]) + (size_t)kb * bb) & 15u));
         gemm_block<F, RT>(S, tab, R, lane, sxa, acc);
     }
