@@ -5,8 +5,8 @@
 // moe, qw6.c:2226-2290; qw6_prefill, qw6.c:2867-2882). With T tokens of top-8
 // routing, expert e sees M_e of them; its gate/up/down are then T x K by K x N
 // products over the M_e gathered rows. Kernels, in stream order:
-//   k_pre_route   one wave per token: softmax top-k (wave_route), the
-//                 shared-expert weight, the shared entries.
+//   k_pre_route   four waves per token: softmax top-k (wave_route), the
+//                 shared-expert weight, the shared entries, the bf16 operands.
 //   k_pre_sort    one workgroup: counting sort of the (token, k) pairs by
 //                 expert into "entries", a tile list of <= 16 entries of
 //                 one expert (the shared expert last, with every token), and
@@ -73,37 +73,36 @@ __device__ __forceinline__ float split8(const float (&v)[8], uint4& h, uint4& l)
 
 // ---- routing -----------------------------------------------------------------------
 
-// One wave per token t: routing, the shared-expert weight, the shared entry.
-__global__ __launch_bounds__(64) void k_pre_route(PrefillLayer L, PrefillWs ws,
-                                                  const float* __restrict__ xin,
-                                                  const float* __restrict__ logits) {
+// One workgroup of four waves per token t: wave 0 routes it (wave_route);
+// all four split its activations and take part in the shared-expert weight;
+// thread 0 writes the shared entry.
+constexpr uint32_t kRouteThreads = 256;
+__global__ __launch_bounds__(kRouteThreads) void k_pre_route(PrefillLayer L, PrefillWs ws,
+                                                             const float* __restrict__ xin,
+                                                             const float* __restrict__ logits) {
     __shared__ uint2 scr[kRouteScr];
-    const uint32_t t = blockIdx.x, lane = threadIdx.x;
-    wave_route(logits + (size_t)t * L.n_experts, L.n_experts, L.top_k, scr,
-               ws.pidx + (size_t)t * L.top_k, ws.pw + (size_t)t * L.top_k);
-    __builtin_amdgcn_wave_barrier();
-    if (lane < L.top_k) {
-        const size_t i = (size_t)t * L.top_k + lane;
-        if (L.idx_out) L.idx_out[i] = ws.pidx[i];
-        if (L.w_out) L.w_out[i] = ws.pw[i];
+    __shared__ float red[kRouteThreads / 64];
+    const uint32_t t = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const float* xr = xin + (size_t)t * L.hidden;
+    if (wave == 0) {
+        wave_route(logits + (size_t)t * L.n_experts, L.n_experts, L.top_k, scr,
+                   ws.pidx + (size_t)t * L.top_k, ws.pw + (size_t)t * L.top_k);
+        __builtin_amdgcn_wave_barrier();
+        if (lane < L.top_k) {
+            const size_t i = (size_t)t * L.top_k + lane;
+            if (L.idx_out) L.idx_out[i] = ws.pidx[i];
+            if (L.w_out) L.w_out[i] = ws.pw[i];
+        }
     }
-    float sw = 1.0f;
-    if (L.shared_router) {   // sigmoid(shared_router . x) (qw6.c:2267-2285)
+    if (L.shared_router) {   // sigmoid(shared_router . x) (qw6.c:2267-2285): per-thread, per-wave, then wave order
         float acc = 0.f;
-        const float* xr = xin + (size_t)t * L.hidden;
-        for (uint32_t c = lane; c < L.hidden; c += 64) acc = fmaf(L.shared_router[c], xr[c], acc);
+        for (uint32_t c = tid; c < L.hidden; c += kRouteThreads) acc = fmaf(L.shared_router[c], xr[c], acc);
         acc = group_sum<64>(acc);
-        sw = 1.0f / (1.0f + expf(-acc));
-    }
-    if (lane == 0) {
-        const uint32_t e = L.T * L.top_k + t;
-        ws.ent_tok[e] = t;
-        ws.ent_w[e] = sw;
+        if (lane == 0) red[wave] = acc;
     }
     // the token's bf16 hi / lo operands and its 32-column sums (lanes 4k .. 4k+3
     // hold one 32-column sub-block, 8 columns each)
-    const float* xr = xin + (size_t)t * L.hidden;
-    for (uint32_t c = lane; c < L.hidden / 8; c += 64) {
+    for (uint32_t c = tid; c < L.hidden / 8; c += kRouteThreads) {
         float v[8];
         const float4 a = ((const float4*)xr)[2 * c], b = ((const float4*)xr)[2 * c + 1];
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
@@ -120,6 +119,19 @@ __global__ __launch_bounds__(64) void k_pre_route(PrefillLayer L, PrefillWs ws,
             uint16_t* dst = ws.xs3 + ((size_t)t * (L.hidden / 256) + sb / 8) * 24 + sb % 8;
             dst[0] = p3[0]; dst[8] = p3[1]; dst[16] = p3[2];
         }
+    }
+    __syncthreads();   // red[] complete
+    if (tid == 0) {
+        float sw = 1.0f;
+        if (L.shared_router) {
+            float acc = 0.f;
+#pragma unroll
+            for (uint32_t w = 0; w < kRouteThreads / 64; w++) acc += red[w];
+            sw = 1.0f / (1.0f + expf(-acc));
+        }
+        const uint32_t e = L.T * L.top_k + t;
+        ws.ent_tok[e] = t;
+        ws.ent_w[e] = sw;
     }
 }
 
@@ -1011,7 +1023,7 @@ int prefill_forward(const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) 
     }
     PrefillLayer Lx = L;
     Lx.x = xin;
-    k_pre_route<<<L.T, 64, 0, st>>>(Lx, ws, xin, logits);
+    k_pre_route<<<L.T, kRouteThreads, 0, st>>>(Lx, ws, xin, logits);
     k_pre_sort<<<1, 1024, 0, st>>>(Lx, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return qw6_fail("batched routing launch: %s", hipGetErrorString(e));
