@@ -490,40 +490,7 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
         }
         return;
     }
-    if constexpr (is_iq(F)) {
-        float d[RT];
-#pragma unroll
-        for (int r = 0; r < RT; r++) d[r] = h2f(rd16(S.raw, lds_row(R[r]), 0));
-#pragma unroll 2
-        for (int sb = 0; sb < 8; sb++) {
-            uint4 b[RT];
-            float db[RT], db2[RT];
-#pragma unroll
-            for (int r = 0; r < RT; r++)
-                tile_iq<F>(S.raw, tab, R[r], q, sb, d[r], b[r], db[r], db2[r]);
-            const uint4 ah = S.a[0][sb][lane], al = S.a[1][sb][lane];
-#pragma unroll
-            for (int r = 0; r < RT; r++) {
-                if (F == F_IQ2S) {   // scales per 16 weights: groups 0-1, then 2-3
-                    const uint4 z = u4(0, 0, 0, 0);
-                    const uint4 b0 = q < 2 ? b[r] : z, b1 = q < 2 ? z : b[r];
-                    f32x4 c = mfma(ah, b0, f32x4{0.f, 0.f, 0.f, 0.f});
-                    c = mfma(al, b0, c);
-                    f32x4 c1 = mfma(ah, b1, f32x4{0.f, 0.f, 0.f, 0.f});
-                    c1 = mfma(al, b1, c1);
-#pragma unroll
-                    for (int j = 0; j < 4; j++)
-                        acc[r][j] = fmaf(db2[r], c1[j], fmaf(db[r], c[j], acc[r][j]));
-                } else {
-                    f32x4 c = mfma(ah, b[r], f32x4{0.f, 0.f, 0.f, 0.f});
-                    c = mfma(al, b[r], c);
-#pragma unroll
-                    for (int j = 0; j < 4; j++) acc[r][j] = fmaf(db[r], c[j], acc[r][j]);
-                }
-            }
-        }
-        return;
-    }
+    // K-quant formats (every IQ format returned above)
     TileScales ts[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) {

@@ -218,10 +218,6 @@ __device__ __forceinline__ void stage_iq_grid(uint8_t* grid, const IqTables& g, 
     }
 }
 
-__device__ __forceinline__ uint4 xor4(const uint4& a, const uint4& b) {
-    return u4(a.x ^ b.x, a.y ^ b.y, a.z ^ b.z, a.w ^ b.w);
-}
-
 // Signs of 8 bf16 values g (value h: 16-bit half h of g) from bits 0-7 of
 // both 16-bit halves of y (bit h -> value h): the halves of word k shift by
 // 15 - 2k and 14 - 2k (one packed 16-bit shift), which puts bit 2k, 2k + 1
