@@ -157,6 +157,57 @@ def test_grouped_other_shape_vs_oracle(torch_dev, ctx):
         L.free()
 
 
+@pytest.mark.parametrize("T", [40, 96])
+def test_grouped_shared_gate_vs_oracle(torch_dev, ctx, T):
+    """The shared expert weighted by sigmoid(shared_router . x) (qw6.c:
+    2267-2285) on the batched path: the gate is a dot product split over the
+    route kernel's four waves, then the weight rides with the shared entries
+    through the down kernel. Router GEMV on; every token against the oracle."""
+    torch = torch_dev
+    from qw6_amd.workload import SynthLayer
+    say("grouped shared gate", T)
+    L = SynthLayer(ctx, 73, 0, "q4k")
+    try:
+        sr = S.f32_normal(73, S.stream_id(0, S.K_SROUTER), L.hidden, 0.05)
+        dsr = torch.from_numpy(sr).cuda()
+        desc = Q.make_layer(L.hidden, L.inter, L.top_k, L.experts, router=L.router,
+                            shared=L.shared, shared_router=dsr)
+        xs = np.stack([cases.token_x(73, 6, t) for t in range(T)])
+        dx = torch.from_numpy(xs).cuda()
+        dout = torch.zeros(T, L.hidden, dtype=torch.float32, device="cuda")
+        didx = torch.zeros(T, L.top_k, dtype=torch.int32, device="cuda")
+        ctx.set_mode(2)
+        try:
+            ctx.moe_forward(desc, dx, dout, n_tok=T, idx=didx)
+            torch.cuda.synchronize()
+        finally:
+            ctx.set_mode(0)
+        out, idx = dout.cpu().numpy(), didx.cpu().numpy()
+        router = L.router_host()
+        lg = np.stack([O.matvec(0, router, L.n_experts, L.hidden, xs[t]) for t in range(T)])
+        need = set()
+        for t in range(T):
+            need.update(int(i) for i in O.moe_route(lg[t], L.top_k)[0])
+        ex = [L.expert_host(e) if e in need else None for e in range(L.n_experts)]
+        ol = O.Layer(L.hidden, L.inter, L.n_experts, L.top_k, router, ex, L.shared_host(), sr)
+        gates = 1.0 / (1.0 + np.exp(-(xs.astype(np.float64) @ sr.astype(np.float64))))
+        assert gates.min() < 0.45 and gates.max() > 0.55   # the gate weights differ by token
+        ties, rels = 0, []
+        for t in range(T):
+            oo, oi, _ = O.moe_layer(ol, xs[t], nthreads=8)
+            if cases.route_gap(lg[t]) < 1e-4:
+                ties += 1
+                continue
+            assert np.array_equal(idx[t], oi), t
+            rels.append(cases.rel_l2(out[t], oo))
+        assert ties <= 1
+        tol, tol_mean = (TOL_SMALL, TOL_SMALL_MEAN) if T < 64 else (TOL_BF16, TOL_MEAN)
+        say("rel-L2 max %.2e mean %.2e" % (max(rels), np.mean(rels)))
+        assert max(rels) <= tol and np.mean(rels) <= tol_mean, (max(rels), np.mean(rels))
+    finally:
+        L.free()
+
+
 def test_grouped_router_and_norm_vs_oracle(torch_dev, ctx):
     """Router GEMV and the fused RMSNorm on the batched path (T = 40)."""
     torch = torch_dev
