@@ -592,6 +592,18 @@ __host__ __device__ inline uint32_t gemm_ny(uint32_t hidden, uint32_t inter) {  
     constexpr int RT = gemm_rt<MODE, F>();
     return MODE == 0 ? inter / (32 * RT) : hidden / (64 * RT);
 }
+template <int MODE, int F>
+__host__ __device__ inline uint32_t gemm_rblocks(uint32_t hidden, uint32_t inter) {
+    return gemm_ny<MODE, F>(hidden, inter);
+}
+// Workgroup slots of one XCD (32 CUs) for a format's occupancy class.
+__host__ __device__ constexpr uint32_t gemm_slots_per_xcd(int f) { return 32u * (uint32_t)gemm_class(f); }
+// A gate/up launch whose last group (FS) runs at four row tiles per wave
+// runs that group's last-round tiles at two (k_pre_gemm).
+template <int MODE, int F, int FS>
+__host__ __device__ constexpr bool gemm_tail_split() {
+    return MODE == 0 && gemm_rt<MODE, FS>() == 4;
+}
 // LDS row stride of the staged raw blocks in 16-byte chunks: one more than
 // a row needs where that many would put the 16 rows of a row tile on two of
 // the 64 banks (IQ3_S: 8 chunks, 128 bytes; 9 spread them over all 16).
@@ -601,11 +613,10 @@ __host__ __device__ constexpr size_t gemm_lds() {
     return offsetof(GemmLds, raw) + (size_t)64 * gemm_rt<MODE, F>() * raw_stride(F) * 16 + iq_grid_bytes(F);
 }
 
-// Row block yb of tile `tile` (format F).
-template <int MODE, int F>
+// Row block yb of tile `tile` (format F), RT row tiles per wave.
+template <int MODE, int F, int RT = gemm_rt<MODE, F>()>
 __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs& ws, uint4 tile,
                                           uint32_t yb, uint8_t* smem) {
-    constexpr int RT = gemm_rt<MODE, F>();
     GemmLds& S = *(GemmLds*)smem;
     const uint32_t mid_e = tile.x, ent0 = tile.y, cnt = tile.z;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
@@ -616,9 +627,11 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
     constexpr uint32_t NCH = raw_chunks(F);
     constexpr uint32_t bb = fmt_block_bytes(F);
     constexpr uint32_t ROWS = 64 * RT;            // weight rows staged per block
-    constexpr uint32_t NR = ROWS * NCH / kPWG;    // raw chunks per thread
+    constexpr uint32_t NC = ROWS * NCH;           // raw chunks per block
+    constexpr uint32_t NR = (NC + kPWG - 1) / kPWG;   // raw chunks per thread (the last maybe none)
     constexpr uint32_t RS = raw_stride(F);        // LDS row stride in chunks
-    static_assert(ROWS * NCH % kPWG == 0, "raw chunks split evenly over the threads");
+    // a thread without a last chunk loads its previous one again and does not store it
+    const bool last = (NR - 1) * kPWG + tid < NC;
     const uint32_t rb = nblk * bb;
     const uint32_t r0 = yb * (MODE == 0 ? 32u * RT : 64u * RT);
     const uint8_t* m0;
@@ -668,7 +681,8 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
     uint32_t psel = 0;
 #pragma unroll
     for (uint32_t i = 0; i < NR; i++) {
-        const uint32_t c = i * kPWG + tid;    // chunk: row c / NCH, 16-B piece c % NCH
+        uint32_t c = i * kPWG + tid;    // chunk: row c / NCH, 16-B piece c % NCH
+        if (i + 1 == NR && !last) c -= kPWG;
         if constexpr (kAl) {
             const uint32_t rr = c / NCH;
             const bool up = MODE == 0 && rr >= ROWS / 2;
@@ -692,7 +706,7 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
 #pragma unroll
         for (uint32_t i = 0; i < NR; i++) {
             const uint32_t c = i * kPWG + tid;
-            *(u32x4*)((uint8_t*)S.raw + 16u * (c / NCH * RS + c % NCH)) = rawv[i];
+            if (i + 1 < NR || last) *(u32x4*)((uint8_t*)S.raw + 16u * (c / NCH * RS + c % NCH)) = rawv[i];
         }
 #pragma unroll
         for (uint32_t i = 0; i < 4; i++) *(u32x4*)&S.a[hl][sb0 + i][lane] = av[i];
@@ -784,6 +798,42 @@ template <int MODE, int F, int FS>
 __global__ __launch_bounds__(kPWG, (gemm_min_blocks<F, FS>()))
 void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    if constexpr (gemm_tail_split<MODE, F, FS>()) {
+        // The group dispatched last (FS) has its last-round tiles run as
+        // items of half the rows (two row tiles per wave), dispatched after
+        // everything else: the last round of workgroup slots, which would
+        // be part-empty, is filled by twice as many items of half the length.
+        // Per XCD the slots run [F's items (F != FS)][FS at 4][FS at 2].
+        const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
+        const uint32_t first_f = ws.fseg[(MODE * 8 + F) * 2 + 0];
+        const uint32_t n_f = F != FS ? ws.fseg[(MODE * 8 + F) * 2 + 1] : 0u;
+        const uint32_t first = ws.fseg[(MODE * 8 + FS) * 2 + 0], n = ws.fseg[(MODE * 8 + FS) * 2 + 1];
+        const uint32_t ny_f = gemm_ny<MODE, F>(L.hidden, L.inter);
+        const uint32_t ny4 = gemm_rblocks<MODE, FS>(L.hidden, L.inter), ny2 = 2 * ny4;
+        const uint32_t items_f = n_f * ny_f, pf = (items_f + 7) / 8;   // per XCD
+        const uint32_t last = (pf + (n * ny4 + 7) / 8) % gemm_slots_per_xcd(gemm_class(F) < gemm_class(FS) ? F : FS);
+        const uint32_t nb = min(n, last * 8 / ny4), na = n - nb;   // FS tiles at 4 / 2 row tiles per wave
+        const uint32_t items_a = na * ny4, items_b = nb * ny2;
+        const uint32_t pa = (items_a + 7) / 8, pb = (items_b + 7) / 8;
+        const uint32_t slot = blockIdx.x / 8, xcd = blockIdx.x % 8;
+        if (slot >= pf + pa + pb) return;
+        const uint32_t seg = slot < pf ? 0u : slot < pf + pa ? 1u : 2u;
+        const uint32_t it = seg == 0 ? xcd * pf + slot : seg == 1 ? xcd * pa + (slot - pf) : xcd * pb + (slot - pf - pa);
+        if (it >= (seg == 0 ? items_f : seg == 1 ? items_a : items_b)) return;
+        const uint32_t pos = seg == 0 ? first_f + it / ny_f : seg == 1 ? first + it / ny4 : first + na + it / ny2;
+        const uint32_t oi = ws.forder[(size_t)MODE * cap + pos];
+        if (oi >= ws.n_tiles[0] + ws.n_tiles[1]) return;   // not a tile of this call
+        const uint4 tile = ws.tiles[oi];
+        if constexpr (F != FS) {
+            if (seg == 0) {
+                gemm_item<MODE, F>(L, ws, tile, it % ny_f, smem);
+                return;
+            }
+        }
+        if (seg == 2) gemm_item<MODE, FS, 2>(L, ws, tile, it % ny2, smem);
+        else gemm_item<MODE, FS, 4>(L, ws, tile, it % ny4, smem);
+        return;
+    }
     const uint32_t ny_a = gemm_ny<MODE, F>(L.hidden, L.inter);
     const uint32_t ny_b = gemm_ny<MODE, FS>(L.hidden, L.inter);
     const uint32_t first_a = ws.fseg[(MODE * 8 + F) * 2 + 0], n_a = ws.fseg[(MODE * 8 + F) * 2 + 1];
@@ -890,10 +940,12 @@ __global__ __launch_bounds__(64) void k_pre_router(const float* __restrict__ rou
 template <int MODE, int F, int FS>
 void launch_gemm_ff(const PrefillLayer& L, const PrefillWs& ws, uint32_t cap, hipStream_t st) {
     const size_t lds = gemm_lds<MODE, F>() > gemm_lds<MODE, FS>() ? gemm_lds<MODE, F>() : gemm_lds<MODE, FS>();
-    const uint32_t ny_a = gemm_ny<MODE, F>(L.hidden, L.inter), ny_b = gemm_ny<MODE, FS>(L.hidden, L.inter);
+    uint32_t ny_a = gemm_ny<MODE, F>(L.hidden, L.inter), ny_b = gemm_ny<MODE, FS>(L.hidden, L.inter);
+    if (gemm_tail_split<MODE, F, FS>()) ny_b = 2 * ny_b;   // at most every FS tile at half the rows
     // at most cap tiles in all; the kernel maps workgroups to its groups'
     // items, per XCD a rounded-up share of each group
-    const uint32_t nwg = (cap * (ny_a > ny_b ? ny_a : ny_b) + 7) / 8 * 8 + (FS != F ? 8u : 0u);
+    const uint32_t nwg = (cap * (ny_a > ny_b ? ny_a : ny_b) + 7) / 8 * 8 +
+                         (gemm_tail_split<MODE, F, FS>() ? 24u : FS != F ? 8u : 0u);
     k_pre_gemm<MODE, F, FS><<<nwg, kPWG, lds, st>>>(L, ws);
 }
 // Groups of one occupancy class only (no other pair is instantiated).
