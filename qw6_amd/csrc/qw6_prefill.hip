@@ -307,6 +307,22 @@ struct GemmLds {
     uint32_t raw[1];             // rows x raw_chunks(F) x 16 B
 };
 
+// LDS bytes of an IQ format's grid in the grouped kernels: bf16 entries,
+// except IQ2_S's 1024 entries kept as their 8 byte values (8 KB).
+__host__ __device__ constexpr uint32_t gemm_grid_bytes(int f) { return f == F_IQ2S ? 1024u * 8u : iq_grid_bytes(f); }
+__device__ __forceinline__ uint2 u64_as_u2(uint64_t v) { return make_uint2((uint32_t)v, (uint32_t)(v >> 32)); }
+// Eight byte values (v.x: values 0-3) as eight bf16: the float conversion of
+// a byte is exact and so is its upper half for integers below 256.
+__device__ __forceinline__ uint4 bytes_bf16(uint2 v) {
+    uint32_t w[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint32_t src = k < 2 ? v.x : v.y;
+        const float f0 = ub(src, 2 * (k & 1)), f1 = ub(src, 2 * (k & 1) + 1);
+        w[k] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+    }
+    return u4(w[0], w[1], w[2], w[3]);
+}
 template <int MODE, int F>
 __host__ __device__ constexpr int gemm_rt() {   // row tiles per wave
     return (F == F_Q6K || F == F_IQ3S) ? 2 : 4;   // larger raw blocks: fewer rows
@@ -439,8 +455,10 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
         // holding the scales of groups 0-1 (low nibble) and 2-3 (high). The
         // two scales take one MFMA pair each, over B with the other groups
         // zeroed; db = d (0.5 + s) / 4 as one fma.
+        // The grid sits in LDS as its 8 byte values per entry (8 KB, so three
+        // workgroups fit a CU) and widens to bf16 in registers.
         const uint8_t* rb = (const uint8_t*)S.raw;
-        const uint4* grid = (const uint4*)tab;
+        const uint2* grid = (const uint2*)tab;
         uint32_t qs[RT], qh[RT], sg[RT], sc[RT];
         float d4[RT], d8[RT];
         const uint32_t s1 = 8u - 2u * q;
@@ -462,7 +480,7 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
         load(0);
 #pragma unroll
         for (int sb = 0; sb < 8; sb++) {
-            uint4 g[RT];
+            uint2 g[RT];
             uint32_t y[RT];
             float db[RT], db2[RT];
 #pragma unroll
@@ -478,7 +496,7 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int r = 0; r < RT; r++) {
-                const uint4 b = apply_signs(g[r], y[r]), z = u4(0, 0, 0, 0);
+                const uint4 b = apply_signs(bytes_bf16(g[r]), y[r]), z = u4(0, 0, 0, 0);
                 const uint4 b0 = q < 2 ? b : z, b1 = q < 2 ? z : b;
                 f32x4 c = mfma(ah, b0, f32x4{0.f, 0.f, 0.f, 0.f});
                 c = mfma(al, b0, c);
@@ -582,10 +600,10 @@ __device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NP],
 // within a class; a shared launch is built for its class, a single format's
 // launch for three (Q4_K) or with room for two (the others, whose
 // allocations fit three workgroups per CU all the same).
-__host__ __device__ constexpr int gemm_class(int f) { return (f == F_Q5K || f == F_IQ2S) ? 2 : 3; }
+__host__ __device__ constexpr int gemm_class(int f) { return f == F_Q5K ? 2 : 3; }
 template <int F, int FS>
 __host__ __device__ constexpr int gemm_min_blocks() {
-    return F == FS ? (F == F_Q4K ? 3 : 2) : (gemm_class(F) < gemm_class(FS) ? gemm_class(F) : gemm_class(FS));
+    return F == FS ? ((F == F_Q4K || F == F_IQ2S) ? 3 : 2) : (gemm_class(F) < gemm_class(FS) ? gemm_class(F) : gemm_class(FS));
 }
 template <int MODE, int F>
 __host__ __device__ inline uint32_t gemm_ny(uint32_t hidden, uint32_t inter) {   // row blocks
@@ -610,7 +628,7 @@ __host__ __device__ constexpr bool gemm_tail_split() {
 __host__ __device__ constexpr uint32_t raw_stride(int f) { return raw_chunks(f) + (f == F_IQ3S ? 1u : 0u); }
 template <int MODE, int F>
 __host__ __device__ constexpr size_t gemm_lds() {
-    return offsetof(GemmLds, raw) + (size_t)64 * gemm_rt<MODE, F>() * raw_stride(F) * 16 + iq_grid_bytes(F);
+    return offsetof(GemmLds, raw) + (size_t)64 * gemm_rt<MODE, F>() * raw_stride(F) * 16 + gemm_grid_bytes(F);
 }
 
 // Row block yb of tile `tile` (format F), RT row tiles per wave.
@@ -696,7 +714,11 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
     if constexpr (kAl) rowp[0] = nullptr;
     u32x4 rawv[NR], av[4], sxv;
     uint8_t* tab = (uint8_t*)S.raw + (size_t)ROWS * RS * 16;   // IQ lattice grid
-    if constexpr (is_iq(F)) stage_iq_grid<F>(tab, g_tabs_pre, kPWG);   // visible after the loop's first barrier
+    if constexpr (F == F_IQ2S) {   // the byte grid (visible after the loop's first barrier)
+        for (uint32_t i = tid; i < 1024; i += kPWG) ((uint2*)tab)[i] = u64_as_u2(g_tabs_pre.iq2s[i]);
+    } else if constexpr (is_iq(F)) {
+        stage_iq_grid<F>(tab, g_tabs_pre, kPWG);
+    }
     f32x4 acc[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
