@@ -616,11 +616,12 @@ __host__ __device__ inline uint32_t gemm_rblocks(uint32_t hidden, uint32_t inter
 }
 // Workgroup slots of one XCD (32 CUs) for a format's occupancy class.
 __host__ __device__ constexpr uint32_t gemm_slots_per_xcd(int f) { return 32u * (uint32_t)gemm_class(f); }
-// A gate/up launch whose last group (FS) runs at four row tiles per wave
-// runs that group's last-round tiles at two (k_pre_gemm).
+// A launch whose last group (FS) can run at half its row tiles per wave
+// (gate/up: 4 -> 2, a gate and an up tile each; down: 2 -> 1, 4 -> 2) runs
+// that group's last-round tiles so (k_pre_gemm).
 template <int MODE, int F, int FS>
 __host__ __device__ constexpr bool gemm_tail_split() {
-    return MODE == 0 && gemm_rt<MODE, FS>() == 4;
+    return MODE == 0 ? gemm_rt<MODE, FS>() == 4 : gemm_rt<MODE, FS>() >= 2;
 }
 // LDS row stride of the staged raw blocks in 16-byte chunks: one more than
 // a row needs where that many would put the 16 rows of a row tile on two of
@@ -822,7 +823,7 @@ void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     if constexpr (gemm_tail_split<MODE, F, FS>()) {
         // The group dispatched last (FS) has its last-round tiles run as
-        // items of half the rows (two row tiles per wave), dispatched after
+        // items of half the rows (half the row tiles per wave), dispatched after
         // everything else: the last round of workgroup slots, which would
         // be part-empty, is filled by twice as many items of half the length.
         // Per XCD the slots run [F's items (F != FS)][FS at 4][FS at 2].
@@ -852,8 +853,9 @@ void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
                 return;
             }
         }
-        if (seg == 2) gemm_item<MODE, FS, 2>(L, ws, tile, it % ny2, smem);
-        else gemm_item<MODE, FS, 4>(L, ws, tile, it % ny4, smem);
+        constexpr int RT = gemm_rt<MODE, FS>();
+        if (seg == 2) gemm_item<MODE, FS, RT / 2>(L, ws, tile, it % ny2, smem);
+        else gemm_item<MODE, FS, RT>(L, ws, tile, it % ny4, smem);
         return;
     }
     const uint32_t ny_a = gemm_ny<MODE, F>(L.hidden, L.inter);
