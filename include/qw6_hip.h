@@ -173,8 +173,8 @@ int qw6_hip_moe_forward_noalloc(qw6_hip_ctx_t *ctx,
  * 0 = automatic (default): the fp32 per-token kernels for launches of 1-2
  *     tokens (and 3 when each matrix kind has one format), the small-batch
  *     MFMA per-token kernels for 4 (and 3 with mixed formats), the grouped
- *     MFMA kernels from 5 tokens on (when every matrix kind has one routed
- *     format, else per-token launches);
+ *     MFMA kernels from 5 tokens on (one launch per expert format present,
+ *     so layers whose experts differ in format take them too);
  * 1 = always the fp32 per-token kernels;
  * 2 = always the grouped MFMA kernels;
  * 3 = always the small-batch MFMA per-token kernels.
