@@ -819,8 +819,11 @@ __device__ __forceinline__ uint32_t wave_route_select(uint32_t (&k)[4], uint32_t
     uint32_t rank = 0xffffffffu, ncand = 0;
     uint32_t ix, key;
     if (route_rank(k, top_k, scr, me2, rank, ncand)) {
+        // fewer than u + 1 candidates (NaN logits are never candidates): rank
+        // u is taken when only -inf and NaN are left, and qw6 picks index 0
         const uint64_t b = __ballot(lane < ncand && rank == u);
-        const int w = b ? __ffsll((unsigned long long)b) - 1 : 0;
+        if (!b) return 0u;
+        const int w = __ffsll((unsigned long long)b) - 1;
         ix = (uint32_t)__builtin_amdgcn_readlane((int)me2.x, w);
         key = (uint32_t)__builtin_amdgcn_readlane((int)me2.y, w);
     } else {

@@ -405,9 +405,13 @@ struct MoeArgs {
     uint32_t mx_nsl;              // k_mx_down: staged blocks per round
 };
 
+// Addresses are formed from an index below n_experts whatever the routing
+// gave (a routing result is always below it; the bound keeps every weight
+// read inside the layer's experts by construction).
 __device__ __forceinline__ MatD expert_mat(const MoeArgs& a, uint32_t e, int k) {
     const PackRef& P = a.pk[k];
     const uint32_t rows = k < 2 ? a.inter : a.hidden, cols = k < 2 ? a.hidden : a.inter;
+    e = min(e, a.n_experts - 1u);
     if (P.regular) return MatD{P.base + P.stride * e, P.fmt, rows, cols, P.rb};
     const ExpertEnt& E = a.experts[e];
     return MatD{E.p[k], E.fmt[k], rows, cols, E.rb[k]};
@@ -419,7 +423,7 @@ __device__ __forceinline__ MatD expert_mat(const MoeArgs& a, uint32_t e, int k) 
 __device__ __forceinline__ MatD expert_mat_wave(const MoeArgs& a, uint32_t e, int k) {
     const PackRef& P = a.pk[k];
     const uint32_t rows = k < 2 ? a.inter : a.hidden, cols = k < 2 ? a.hidden : a.inter;
-    e = __builtin_amdgcn_readfirstlane(e);
+    e = min((uint32_t)__builtin_amdgcn_readfirstlane(e), a.n_experts - 1u);
     if (P.regular) return MatD{P.base + P.stride * e, P.fmt, rows, cols, P.rb};
     using CE = __attribute__((address_space(4))) const ExpertEnt;
     const CE& E = ((CE*)a.experts)[e];
@@ -533,7 +537,22 @@ __device__ __forceinline__ void route_prologue(const MoeArgs& a, uint32_t (&keys
         if (is_first) s_slot_e[slot] = e;
         if (lane == 0) *s_n = (uint32_t)__popcll(mask);
         __builtin_amdgcn_wave_barrier();
-        if (lane < ne) s_wt[slot * kMaxTok + lane / a.top_k] = s_w[lane];
+        // A token selects one expert at several ranks only once its logits
+        // are down to -inf and NaN (index 0 again, qw6.c:2808-2816); those
+        // later ranks weigh exactly 0 (or NaN, with every weight NaN), so the
+        // first rank of the expert in the token writes the sum over its ranks
+        // and qw6's sum w_k * y_k is kept. One writer per (slot, token).
+        if (lane < ne) {
+            const uint32_t k0 = lane - lane % a.top_k;
+            bool first_in_tok = true;
+            float wsum = 0.f;
+            for (uint32_t j = k0; j < k0 + a.top_k; j++) {
+                if (s_idx[j] != e) continue;
+                if (j < lane) first_in_tok = false;
+                wsum += s_w[j];
+            }
+            if (first_in_tok) s_wt[slot * kMaxTok + lane / a.top_k] = wsum;
+        }
     }
     __syncthreads();
 }
@@ -626,6 +645,11 @@ __device__ __forceinline__ bool route_slot_select(const MoeArgs& a, uint32_t (&k
         if (route_rank(keys, a.top_k, scr + wave * kRouteScr, me2, rank, ncand)) {
             if (lane < ncand && rank < a.top_k)   // only -inf left: qw6 picks index 0
                 s_sel[wave * a.top_k + rank] = me2.y > kKeyNegInf ? ~me2.x : 0u;
+            // ranks without a candidate (NaN logits are never candidates) are
+            // taken once only -inf and NaN are left: index 0, as in
+            // wave_route_keys. Candidates hold ranks [0, ncand), so these
+            // lanes write the other ranks and no slot is written twice.
+            if (lane >= ncand && lane < a.top_k) s_sel[wave * a.top_k + lane] = 0u;
         } else if (lane < a.top_k) {
             const uint2 me = scr[wave * kRouteScr + 32 + lane];
             s_sel[wave * a.top_k + lane] = me.y > kKeyNegInf ? ~me.x : 0u;

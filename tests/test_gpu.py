@@ -115,9 +115,8 @@ def test_host_route_nan_logits_vs_oracle():
     index 0 selected first, NaNs elsewhere never) and weights (all NaN when
     the first pick is a NaN), against the oracle; plus 256-expert vectors with
     NaNs scattered, at index 0 and not."""
-    from test_oracle import nan_route_cases
     rng = np.random.default_rng(17)
-    vecs = [(np.array(lg, np.float32), k) for lg, k, _ in nan_route_cases()]
+    vecs = [(np.array(lg, np.float32), k) for lg, k, _ in cases.nan_route_cases()]
     for trial in range(12):
         lg = rng.standard_normal(256).astype(np.float32)
         lg[rng.integers(0, 256, 1 + trial)] = np.nan

@@ -241,26 +241,8 @@ def test_route_kat_small():
     assert list(idx) == [1, 2] and abs(w.sum() - 1) < 1e-6 and w[0] > w[1]
 
 
-def nan_route_cases():
-    """Router logits with NaNs, and qw6's answer worked by hand from its loop
-    (qw6.c:2808-2816: each round scans with a strict '>' from best = index 0,
-    then sets the winner to -inf): a NaN at index 0 wins the first round, a
-    NaN elsewhere never wins, and once only -inf / NaN remain index 0 (by then
-    -inf) is picked again."""
-    nan, inf = np.float32(np.nan), np.float32(np.inf)
-    return [
-        ([1.0, nan, 3.0, 2.0], 2, [2, 3]),
-        ([nan, 5.0, 1.0], 2, [0, 1]),
-        ([-np.float32(np.nan), 5.0, 1.0], 2, [0, 1]),   # a NaN with the sign bit set
-        ([1.0, nan, nan, 2.0], 4, [3, 0, 0, 0]),
-        ([nan, nan, nan], 3, [0, 0, 0]),
-        ([-inf, nan, 4.0, nan, -inf], 3, [2, 0, 0]),
-        ([3.0, nan, inf, 3.0], 3, [2, 0, 3]),
-    ]
-
-
 def test_route_nan_kats():
-    for lg, k, want in nan_route_cases():
+    for lg, k, want in cases.nan_route_cases():
         lg = np.array(lg, np.float32)
         idx, w = O.moe_route(lg, k)
         assert list(idx) == want, (lg, idx, want)
@@ -270,6 +252,42 @@ def test_route_nan_kats():
             ri, rw = O.ref_moe_route(lg, k)
             assert np.array_equal(ri, idx)
             assert np.array_equal(bits(rw), bits(w))
+
+
+def test_route_vectors_of_the_layer_tests():
+    """The 256-expert routing vectors the layer-level GPU tests send through
+    qw6_hip_moe_forward: the oracle's selections follow qw6's rules, worked
+    by hand where the vector fixes them (an expert picked again once only
+    -inf / NaN is left is index 0), and equal qw6's own build where present."""
+    want = {n: list(O.moe_route(v, 8)[0]) for n, v in cases.route_vectors()}
+    vec = dict(cases.route_vectors())
+    assert want["allnan"] == [0] * 8
+    assert want["allneginf"] == [0] * 8
+    assert want["small_neginf"] == [1, 2, 0, 3, 0, 0, 0, 0]
+    assert want["three_finite"] == [100, 200, 5, 0, 0, 0, 0, 0]
+    assert want["allequal"] == list(range(8))
+    assert want["nan_at_0"][0] == 0 and 0 not in want["nan_at_0"][1:]
+    assert not set(want["nan_scattered"]) & {3, 17, 64, 65, 200, 255}
+    assert sorted(want["low_index0"][:7]) == [0, 250, 251, 252, 253, 254, 255]
+    assert want["low_index0"][7] == 0
+    for i, (lg, _, hand) in enumerate(cases.nan_route_cases()):
+        # padding with NaN keeps the hand-worked answer as the first ranks;
+        # no later rank is a NaN's index
+        got = want["nan%d" % i]
+        assert got[:len(hand)] == hand
+        assert all(k == 0 or not np.isnan(np.float32(lg[k])) for k in got)
+    for n, v in vec.items():
+        w = O.moe_route(v, 8)[1]
+        if np.isnan(v[0]) or np.isneginf(v).all():
+            assert np.isnan(w).all(), n   # the max is NaN, or -inf - -inf
+        elif n in ("small_neginf", "three_finite", "low_index0"):
+            assert np.isfinite(w).all() and w.sum() == pytest.approx(1.0, abs=1e-6), n
+            rep = [k for k in range(8) if want[n][k] == 0][1:]   # index 0 again
+            assert all(w[k] == 0.0 for k in rep), n
+        if O.ref() is not None:
+            ri, rw = O.ref_moe_route(v, 8)
+            assert list(ri) == want[n], n
+            assert np.array_equal(bits(rw), bits(w)), n
 
 
 def test_route_brute_force_ties():
