@@ -907,12 +907,12 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
             }
             if (tid < a.max_u) {
                 SlotTable* st = a.slots;
-                if (tid < nslot) {
-                    const MatD D = expert_mat(a, s_slot_e[tid], 2);
-                    st->p[tid] = D.p; st->fmt[tid] = D.fmt; st->rb[tid] = D.rb;
-                } else {
-                    st->p[tid] = nullptr; st->fmt[tid] = 0; st->rb[tid] = 0;
-                }
+                // entries past the count name slot 0's matrix (weight 0 for every
+                // token): each k_moe_down wave stages its first matrix before it
+                // knows the count, so every entry a wave may take must be a real
+                // matrix (nslot >= 1: top_k >= 1)
+                const MatD D = expert_mat(a, s_slot_e[tid < nslot ? tid : 0u], 2);
+                st->p[tid] = D.p; st->fmt[tid] = D.fmt; st->rb[tid] = D.rb;
 #pragma unroll
                 for (uint32_t t = 0; t < kMaxTok; t++) st->wt[tid][t] = s_wt[tid * kMaxTok + t];
             }
@@ -1081,7 +1081,7 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const uint32_t has_sh = a.sd.p != nullptr ? 1u : 0u;
     // The slot table is read in one round trip: the count and this wave's
-    // first slot (speculatively: entries past the count are null) are scalar
+    // first slot (speculatively: entries past the count repeat slot 0) are scalar
     // loads issued before anything else. Issued after the lattice tables'
     // LDS-direct loads they would be vector loads whose use waits for every
     // earlier vector load (the counter retires in order). The gate weights,
@@ -1112,10 +1112,15 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
     }
     const uint32_t ntot = nslot + has_sh;
     // One matrix of this wave. The first is peeled off the loop below: every
-    // wave has at least one (nw <= ntot) and issues its loads before the
-    // barrier that makes the lattice tables visible, and a loop around it
-    // would make the compiler wait for all earlier vector loads (the gate
-    // weights, residual, lattice tables) before its activation loads.
+    // wave takes one and issues its loads before the barrier that makes the
+    // lattice tables visible, and a loop around it (or a branch on the
+    // count) would make the compiler wait for earlier loads (the gate
+    // weights, residual, lattice tables, the count) before its activation
+    // loads. The launch has nw <= max_u + has_sh waves, but tokens that
+    // share experts (or select expert 0 at several ranks) leave fewer
+    // matrices: a wave past them takes slot-table entry wave - has_sh,
+    // which repeats slot 0's matrix, and writes its ybuf row, which the
+    // combine does not read (m < nw, so the row is inside the allocation).
     auto matrix = [&](uint32_t m, bool first) {
         const bool sh = has_sh && m == 0;
         const uint32_t u = m - has_sh;
@@ -1295,12 +1300,12 @@ __device__ __forceinline__ bool mx_route_block(const MoeArgs& a, uint32_t (&keys
         }
         if (tid < a.max_u) {
             SlotTable* st = a.slots;
-            if (tid < nslot) {
-                const MatD D = expert_mat(a, s_slot_e[tid], 2);
-                st->p[tid] = D.p; st->fmt[tid] = D.fmt; st->rb[tid] = D.rb;
-            } else {
-                st->p[tid] = nullptr; st->fmt[tid] = 0; st->rb[tid] = 0;
-            }
+            // entries past the count name slot 0's matrix (weight 0 for every
+            // token): each k_moe_down wave stages its first matrix before it
+            // knows the count, so every entry a wave may take must be a real
+            // matrix (nslot >= 1: top_k >= 1)
+            const MatD D = expert_mat(a, s_slot_e[tid < nslot ? tid : 0u], 2);
+            st->p[tid] = D.p; st->fmt[tid] = D.fmt; st->rb[tid] = D.rb;
 #pragma unroll
             for (uint32_t t = 0; t < kMaxTok; t++) st->wt[tid][t] = s_wt[tid * kMaxTok + t];
         }
@@ -1456,7 +1461,7 @@ __global__ __launch_bounds__(1024) void k_mx_down(MoeArgs a) {
     const uint32_t has_sh = a.sd.p != nullptr ? 1u : 0u;
     const uint32_t nkb = a.inter / 256;
     const MxTab tb = mx_tab(a.tmask_dn);
-    // the slot table in one round trip (entries past the count are null)
+    // the slot table in one round trip (only entries below the count are used)
     const uint32_t nslot = a.slots->n;
     if (tid < kMaxSlots * kMaxTok) s_wt[tid] = a.slots->wt[tid / kMaxTok][tid % kMaxTok];
     if (tid < kMaxSlots) {
