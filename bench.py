@@ -19,9 +19,13 @@ counter runs, each scaled by what the same counter reads for an elementwise
 y = 2x kernel over 512 MiB (read from the committed summary; null when
 absent).
 
-`cpu_baseline` times qw6's own CPU path (compiled from the reference where
-available, else the repository's bit-identical C restatement) on a bounded
-sample of the same workload on this host, single thread as qw6 runs it.
+`cpu_baseline` times the repository's C restatement of qw6's CPU path (the
+oracle port, pinned bitwise to qw6's own build where the repository is built)
+on a bounded sample of the headline workload on this host, single thread as
+qw6 runs it, with its OpenMP build beside it. `cpu_baselines` holds the same
+for every workload: the 512 x 2048 Q4_K matvec, the Q4_K and IQ2_M decode
+layers, two-token steps, tokens of the 512-token batch (per token-expert
+pair) and single-token steps of the 40-layer stack.
 
 `secondary` (with --workload all, the default) adds:
   iq2m_decode   the same layer with IQ2_XXS gate/up and IQ3_S / IQ2_S down;
@@ -83,7 +87,9 @@ def parse():
     ap.add_argument("--no-small-batch", action="store_true",
                     help="with --workload prefill: time the prefill_T512 case only (no T=2 and "
                          "small-batch cases), for a kernel profile of that workload alone")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0,
+                    help="CPU-baseline budget over all workloads (the oracle port, one thread "
+                         "and OpenMP)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-graph", action="store_true",
                     help="eager launches only (for counter collection)")
@@ -385,55 +391,183 @@ def host_cpu():
             "affinity": len(os.sched_getaffinity(0))}
 
 
-def cpu_baseline(L, xs_host, budget_s):
-    """qw6's CPU path on a bounded sample: tokens through pool layer 0."""
+# ---- CPU baseline: the oracle port on the host's cores ---------------------------
+# The port (oracle/qw6_oracle.c) restates qw6's CPU path in its own fp32
+# expression order and is pinned bitwise to qw6's build in the container the
+# repository is built in; the GPU host never loads qw6's build. Each figure is
+# a median over a bounded sample of the same workload, single-threaded as qw6
+# runs it, and again with the port's row-parallel OpenMP build (bitwise the
+# same outputs).
+
+CPU_THREADS_MAX = 16   # the host CPU share of one GPU on the machines this runs on
+
+
+def _cpu_threads():
+    return max(1, min(CPU_THREADS_MAX, len(os.sched_getaffinity(0))))
+
+
+def _timed(fn, budget_s, nmax, nmin=2):
+    """Durations (s) returned by fn(i) for i = 0, 1, ... until the budget or
+    nmax calls are spent (at least nmin calls)."""
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while (len(ts) < nmax and time.perf_counter() < t_end) or len(ts) < nmin:
+        ts.append(fn(len(ts)))
+    return ts
+
+
+class PortLayer:
+    """Host copies of one device layer for the oracle: router and shared
+    expert at once, routed experts copied on first use (never timed)."""
+
+    def __init__(self, L, norm_w=None):
+        import oracle as O
+        self.O, self.L = O, L
+        self.router = L.router_host() if L.router is not None else None
+        self.shared = L.shared_host()
+        self.norm_w = norm_w
+        self.cache = {}
+
+    def layer(self, logits):
+        O, L = self.O, self.L
+        idx, _ = O.moe_route(logits, L.top_k)
+        for e in set(int(i) for i in idx):
+            if e not in self.cache:
+                self.cache[e] = L.expert_host(e)
+        ex = [self.cache.get(e) for e in range(L.n_experts)]
+        return O.Layer(L.hidden, L.inter, L.n_experts, L.top_k, self.router, ex, self.shared)
+
+    def step(self, x, logits=None, nthreads=1):
+        """One token through the layer on the CPU: (output, seconds). The
+        router GEMV (when no logits are given), routing, the expert matvecs,
+        SiLU and the combine are timed; copying the selected experts to the
+        host beforehand is not."""
+        O = self.O
+        lg = logits if logits is not None else O.matvec(0, self.router, self.L.n_experts,
+                                                         self.L.hidden, x, nthreads=nthreads)
+        layer = self.layer(lg)
+        t0 = time.perf_counter()
+        out, _, _ = O.moe_layer(layer, x, logits=logits, nthreads=nthreads)
+        return out, time.perf_counter() - t0
+
+
+def _cpu_entry(unit, single, multi, nt, sample, scale=1.0, extra=None):
     import numpy as np
+    e = {"value": round(scale * 1e6 * float(np.median(single)), 1), "unit": unit, "cores": 1,
+         "kind": "port", "sample": sample,
+         "multicore": {"value": round(scale * 1e6 * float(np.median(multi)), 1), "cores": nt,
+                       "kind": "port",
+                       "sample": "%d of the same, OpenMP over %d threads" % (len(multi), nt)}}
+    if extra:
+        e.update(extra)
+    return e
+
+
+def cpu_matvec(budget_s):
+    """One 512 x 2048 Q4_K dequant-matvec (the seeded matrix of the golden
+    fixture) on the CPU."""
     sys.path.insert(0, HERE)
     import oracle as O
-    kind = "reference" if O.ref() is not None else "port"
-    router = L.router_host()
-    shared = L.shared_host()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    i = 0
-    while (time.perf_counter() < t_end and i < 200) or i < 3:
-        x = xs_host[i % len(xs_host)]
-        lg = O.matvec(0, router, N_EXPERTS, HIDDEN, x)
-        idx, _ = O.moe_route(lg, TOP_K)
-        sel = set(int(e) for e in idx)
-        ex = [L.expert_host(e) if e in sel else None for e in range(N_EXPERTS)]
-        layer = O.Layer(HIDDEN, INTER, N_EXPERTS, TOP_K, router, ex, shared)
-        t0 = time.perf_counter()
-        if kind == "reference":
-            O.ref_moe_layer(layer, x, want_route=False)
-        else:
-            O.moe_layer(layer, x)
-        times.append(time.perf_counter() - t0)
-        i += 1
-    us = 1e6 * float(np.median(times))
-    # the same steps through the oracle port's row-parallel OpenMP build on
-    # the host's cores (per-row sums unchanged, so the outputs are bitwise
-    # the single-thread ones)
-    nt = max(1, min(8, len(os.sched_getaffinity(0)) // 2))   # leave cores to the rest
-    mt = []
-    for j in range(min(len(times), 50)):
-        x = xs_host[j % len(xs_host)]
-        lg = O.matvec(0, router, N_EXPERTS, HIDDEN, x, nthreads=nt)
-        idx, _ = O.moe_route(lg, TOP_K)
-        sel = set(int(e) for e in idx)
-        ex = [L.expert_host(e) if e in sel else None for e in range(N_EXPERTS)]
-        layer = O.Layer(HIDDEN, INTER, N_EXPERTS, TOP_K, router, ex, shared)
-        t0 = time.perf_counter()
-        O.moe_layer(layer, x, nthreads=nt)
-        mt.append(time.perf_counter() - t0)
-    return {"value": round(us, 1), "unit": "us/layer", "cores": 1, "kind": kind,
-            "host_cpu": host_cpu(),
-            "sample": "%d single-token MoE layer steps (median), one pool layer, "
-                      "selected experts copied to host; single thread as qw6" % len(times),
-            "multicore": {"value": round(1e6 * float(np.median(mt)), 1), "cores": nt, "kind": "port",
-                          "sample": "%d of the same steps, the oracle's OpenMP row-parallel "
-                                    "build on %d of the host's %d logical CPUs"
-                                    % (len(mt), nt, os.cpu_count())}}
+    from qw6_amd import synth as S
+    w = S.quant_matrix(1, S.stream_id(0, S.K_GATE), S.Q_Q4_K_M, 512, 2048)
+    x = S.f32_normal(1, S.stream_id(0, S.K_X), 2048, 1.0)
+    nt = _cpu_threads()
+
+    def run(nthreads):
+        def f(_):
+            t0 = time.perf_counter()
+            O.matvec(S.Q_Q4_K_M, w, 512, 2048, x, nthreads=nthreads)
+            return time.perf_counter() - t0
+        return f
+    single = _timed(run(1), budget_s * 0.6, 2000, 20)
+    multi = _timed(run(nt), budget_s * 0.4, 2000, 20)
+    return _cpu_entry("us/matvec", single, multi, nt,
+                      "%d calls (median), Q4_K W[512 x 2048] x fp32 x[2048], one thread" % len(single))
+
+
+def cpu_decode_layer(L, xs_host, budget_s, what):
+    """Single-token MoE layer steps (router GEMV, top-8, experts, combine) on
+    the CPU through layer L, inputs xs_host in turn."""
+    pl = PortLayer(L)
+    nt = _cpu_threads()
+    single = _timed(lambda i: pl.step(xs_host[i % len(xs_host)])[1], budget_s * 0.7, 200, 3)
+    multi = _timed(lambda i: pl.step(xs_host[i % len(xs_host)], nthreads=nt)[1],
+                   budget_s * 0.3, 100, 3)
+    return _cpu_entry("us/layer", single, multi, nt,
+                      "%d single-token %s layer steps (median), one pool layer, one thread"
+                      % (len(single), what))
+
+
+def cpu_two_tokens(L, xs_host, budget_s):
+    """Two tokens (MTP draft verification) through layer L on the CPU: qw6
+    runs them one after the other."""
+    pl = PortLayer(L)
+    nt = _cpu_threads()
+
+    def pair(nthreads):
+        def f(i):
+            a = xs_host[(2 * i) % len(xs_host)]
+            b = xs_host[(2 * i + 1) % len(xs_host)]
+            return pl.step(a, nthreads=nthreads)[1] + pl.step(b, nthreads=nthreads)[1]
+        return f
+    single = _timed(pair(1), budget_s * 0.7, 100, 2)
+    multi = _timed(pair(nt), budget_s * 0.3, 50, 2)
+    return _cpu_entry("us/layer", single, multi, nt,
+                      "%d two-token steps (median) with the router GEMV, one thread" % len(single))
+
+
+def cpu_prefill_tokens(L, xs_host, lg_host, budget_s, T):
+    """Tokens of a T-token batch with given router logits through layer L on
+    the CPU (qw6 runs a batch token by token): microseconds per token-expert
+    pair (top_k routed + the shared expert per token), and per token and per
+    T-token layer beside it."""
+    pl = PortLayer(L)
+    nt = _cpu_threads()
+    n = len(xs_host)
+    pairs = L.top_k + (1 if L.shared is not None else 0)
+    single = _timed(lambda i: pl.step(xs_host[i % n], lg_host[i % n])[1], budget_s * 0.7, n, 3)
+    multi = _timed(lambda i: pl.step(xs_host[i % n], lg_host[i % n], nthreads=nt)[1],
+                   budget_s * 0.3, n, 3)
+    import numpy as np
+    tok_us = 1e6 * float(np.median(single))
+    return _cpu_entry("us/token-expert pair", single, multi, nt,
+                      "%d tokens of the %d-token batch (median), given Zipf logits, one thread; "
+                      "%d token-expert pairs per token" % (len(single), T, pairs),
+                      scale=1.0 / pairs,
+                      extra={"us_per_token": round(tok_us, 1),
+                             "us_per_layer_T%d" % T: round(T * tok_us, 1)})
+
+
+def cpu_stack_token(stk, xs_host, budget_s):
+    """Single-token steps of the whole stack on the CPU: h <- h + MoE_l(
+    RMSNorm(h, w_l)) for every layer (qw6.c:2475-2484), RMSNorm and the
+    residual add timed with the layers."""
+    sys.path.insert(0, HERE)
+    import numpy as np
+    import oracle as O
+    nw = stk.norm_w.cpu().numpy()
+    pls = [PortLayer(L) for L in stk.layers]
+    nt = _cpu_threads()
+
+    def token(nthreads):
+        def f(i):
+            h = np.array(xs_host[i % len(xs_host)], np.float32)
+            tot = 0.0
+            for l, pl in enumerate(pls):
+                t0 = time.perf_counter()
+                xn = O.rmsnorm(h, nw[l], stk.eps)
+                tot += time.perf_counter() - t0
+                out, dt = pl.step(xn, nthreads=nthreads)
+                t0 = time.perf_counter()
+                h = (h + out).astype(np.float32)
+                tot += dt + time.perf_counter() - t0
+            return tot
+        return f
+    single = _timed(token(1), budget_s * 0.7, 8, 1)
+    multi = _timed(token(nt), budget_s * 0.3, 8, 1)
+    return _cpu_entry("us/token", single, multi, nt,
+                      "%d single-token steps through all %d layers (median), one thread"
+                      % (len(single), len(pls)))
 
 
 # ---- workloads --------------------------------------------------------------------
@@ -601,7 +735,7 @@ def bench_head(torch, Q, S, ctx, args):
     return res
 
 
-def bench_stack(torch, Q, S, ctx, args):
+def bench_stack(torch, Q, S, ctx, args, cpu=None):
     """40 IQ2_M-mix layers, h <- h + MoE_l(RMSNorm(h, w_l)), single-token steps
     (qw6_amd.workload.SynthStack: the norm fused into each layer's call, the
     hidden state updated in place, the step captured as one HIP graph)."""
@@ -639,12 +773,15 @@ def bench_stack(torch, Q, S, ctx, args):
            "workload": "40 layers IQ2_XXS gate/up + IQ3_S/IQ2_S down, F32 router, shared "
                        "expert, RMSNorm (eps 1e-6) fused before each layer, residual in "
                        "place; 128 single-token steps with fresh inputs"}
+    if cpu is not None:
+        cpu["stack_40_layers_token"] = cpu_stack_token(stk, X[:8].cpu().numpy(),
+                                                       args.cpu_seconds * 0.3)
     stk.free()
     return res
 
 
 def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
-                  formats=PREFILL_FORMATS["q4k"]):
+                  formats=PREFILL_FORMATS["q4k"], cpu=None):
     """T tokens with Zipf-skewed logits through the grouped MFMA kernels, plus
     (with_t2) the T=2 MTP case through the per-token kernels with the router
     GEMV."""
@@ -690,6 +827,10 @@ def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
            "tokens_per_s": round(T / (us * 1e-6), 1),
            "workload": "T=%d, hidden 2048, 256 experts top-8 + shared, %s; router logits "
                        "given, Zipf(1.1)-skewed (Gumbel-top-k)" % (T, formats)}
+    if cpu is not None:   # a sample of the batch's tokens through the CPU port
+        n = min(T, 64)
+        cpu["prefill_T%d_pair" % T] = cpu_prefill_tokens(L0, X[0, :n].cpu().numpy(), lg_h[0][:n],
+                                                         args.cpu_seconds * 0.15, T)
     if not with_t2:
         return res, None
 
@@ -775,6 +916,7 @@ def main():
         torch.cuda.synchronize()
         del a, b
     want_prefill = args.workload in ("all", "prefill")
+    cpu_cfg = None if args.no_cpu else {}
     ctx = Q.Context(0, max_tokens=args.prefill_tokens if want_prefill else 4)
     P = args.pool
     mix = ("iq2m" if args.workload == "iq2m" else
@@ -799,7 +941,8 @@ def main():
     if want_prefill:
         pf, t2 = bench_prefill(torch, Q, S, ctx, pool, args,
                                with_t2=not args.no_small_batch and mix == "q4k",
-                               formats=PREFILL_FORMATS[mix])
+                               formats=PREFILL_FORMATS[mix],
+                               cpu=cpu_cfg if mix == "q4k" else None)
         secondary["prefill_T%d%s" % (args.prefill_tokens, "" if mix == "q4k" else "_" + mix)] = pf
         log("prefill: %s" % json.dumps(pf))
         if t2 is not None:
@@ -810,9 +953,15 @@ def main():
         gg = bench_gguf(torch, Q, S, ctx, pool, X, out, idx)
         secondary["gguf_layer"] = gg
         log("gguf layer: %s" % json.dumps(gg))
-    cpu = None
-    if res_main is not None and not args.no_cpu:
-        cpu = cpu_baseline(pool[0], X.cpu().numpy(), args.cpu_seconds)
+    if cpu_cfg is not None and pool and mix == "q4k" and args.workload != "prefill":
+        xh = X.cpu().numpy()
+        cpu_cfg["q4k_matvec_512x2048"] = cpu_matvec(args.cpu_seconds * 0.05)
+        cpu_cfg["decode_layer_q4k"] = cpu_decode_layer(pool[0], xh, args.cpu_seconds * 0.2,
+                                                       "Q4_K / Q6_K")
+        cpu_cfg["mtp_T2_q4k"] = cpu_two_tokens(pool[0], xh, args.cpu_seconds * 0.1)
+    if cpu_cfg is not None and pool and args.workload == "iq2m":
+        cpu_cfg["decode_layer_iq2m"] = cpu_decode_layer(pool[0], X.cpu().numpy(),
+                                                        args.cpu_seconds * 0.2, "IQ2_M-mix")
     for L in pool:
         L.free()
     pool = []
@@ -826,6 +975,9 @@ def main():
         o2 = torch.empty_like(X2)
         i2 = torch.zeros(P, TOP_K, dtype=torch.int32, device="cuda")
         r2 = bench_decode(torch, Q, S, ctx, pool2, X2, o2, i2, args)
+        if cpu_cfg is not None:
+            cpu_cfg["decode_layer_iq2m"] = cpu_decode_layer(pool2[0], X2.cpu().numpy(),
+                                                            args.cpu_seconds * 0.2, "IQ2_M-mix")
         r2["workload"] = ("decode layer, batch 1, IQ2_XXS gate/up, IQ3_S (even experts) / "
                           "IQ2_S (odd) down, F32 router, shared expert (Q4_K/Q6_K)")
         secondary["iq2m_decode"] = r2
@@ -850,7 +1002,7 @@ def main():
         for L in pool4:
             L.free()
     if args.workload in ("all", "stack"):
-        st = bench_stack(torch, Q, S, ctx, args)
+        st = bench_stack(torch, Q, S, ctx, args, cpu=cpu_cfg)
         secondary["stack"] = st
         log("stack: %s" % json.dumps(st))
     if args.workload in ("all", "head"):
@@ -863,9 +1015,17 @@ def main():
         log("dependent-kernel floor: %s" % json.dumps(fl))
 
     if res_main is None:
-        print(json.dumps({"secondary": secondary}), flush=True)
+        print(json.dumps({"secondary": secondary, "cpu_baselines": cpu_cfg}), flush=True)
         ctx.close()
         return
+
+    # the headline's CPU figure: the same decode layer through the port
+    cpu = None
+    if cpu_cfg and mix in ("q4k", "iq2m"):
+        head = cpu_cfg.get("decode_layer_%s" % mix)
+        if head is not None:
+            cpu = dict(head)
+            cpu["host_cpu"] = host_cpu()
 
     kname = "k_moe_gate_up1"   # the gate/up kernel of one-token launches
     gk = res_main["kernels"][kname]
@@ -909,6 +1069,7 @@ def main():
                      "algorithmic_bytes": gk["bytes"], "avg_us": gk["us"],
                      "traffic_source": traffic_src},
         "cpu_baseline": cpu,
+        "cpu_baselines": cpu_cfg,
         "secondary": secondary,
     }
     print(json.dumps(res), flush=True)

@@ -595,10 +595,11 @@ __device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NP],
 // A operands of block kb + 1 are loaded into registers while block kb is
 // multiplied, then written to LDS between two barriers.
 // Occupancy class of a format's contraction: three workgroups per CU (at
-// most 168 VGPRs; 53 KB of LDS or less each) except Q5_K and IQ2_S, whose
-// bodies need up to 198 VGPRs (two). Format groups share a launch only
-// within a class; a shared launch is built for its class, a single format's
-// launch for three (Q4_K) or with room for two (the others, whose
+// most 168 VGPRs; 53 KB of LDS or less each) except Q5_K, whose body needs
+// up to 198 VGPRs (two). IQ2_S, with its grid kept as byte values, is in
+// the three-workgroup class. Format groups share a launch only within a
+// class; a shared launch is built for its class, a single format's launch
+// for three (Q4_K and IQ2_S) or with room for two (the others, whose
 // allocations fit three workgroups per CU all the same).
 __host__ __device__ constexpr int gemm_class(int f) { return f == F_Q5K ? 2 : 3; }
 template <int F, int FS>

@@ -1,8 +1,9 @@
 """Seeded synthetic GGUF expert weights and activations (host-side generator).
 
 Every value is a pure function of (seed, stream, index), so any slice of a
-tensor can be generated on its own, and the device generator in
-csrc/qw6_synth.hip produces the same bytes:
+tensor can be generated on its own, and the device generator
+(k_synth_blocks / k_synth_normal in csrc/qw6_hip.hip, built on the sm_*
+hash functions of csrc/qw6_dev.h) produces the same bytes:
 
 * ``hash64(seed, stream, i)``: three SplitMix64 finalisations
   (seed key, stream key, then the counter ``i``).

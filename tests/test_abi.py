@@ -47,3 +47,18 @@ def test_host_ops_reject_bad_shapes_without_device_work():
     with pytest.raises(Q.Qw6HipError, match="bounds"):
         Q.moe_gather_host(np.zeros((9, 4), np.float32), np.zeros(9, np.float32), None, 0.0)
     assert Q.lib().qw6_hip_matmul_q4k_host(None, x, np.zeros(1, np.float32), 1, 256) == -1
+
+
+def test_gpu_processes_never_load_the_reference_build():
+    """qw6's compiled CPU path (oracle/_ref) checks the oracle in the
+    container the repository is built in; no process on the GPU host loads
+    it. Every GPU test, the smoke entry and the bench compare against (and
+    time) the oracle port only: none of them reaches oracle.ref(), a ref_*
+    wrapper, or the oracle test module that does."""
+    root = Path(__file__).resolve().parents[1]
+    files = sorted((root / "tests").glob("test_gpu*.py")) + sorted((root / "tests").glob("test_zz*.py"))
+    files += [root / "bench.py", root / "__graft_entry__.py", root / "tests" / "cases.py",
+              root / "tests" / "conftest.py"]
+    pat = re.compile(r"\bO\.ref\(|\bO\.ref_\w+|\bref_moe_\w+\(|\btest_oracle\b")
+    bad = [(f.name, m.group(0)) for f in files if f.exists() for m in pat.finditer(f.read_text())]
+    assert not bad, bad
