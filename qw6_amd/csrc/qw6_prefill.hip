@@ -642,6 +642,16 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
     const uint32_t n = lane & 15u, q = lane >> 4;
     const bool shared = mid_e == L.n_experts;
+    // Rows are addressed with format F's row bytes: the tile's expert must
+    // hold format F (k_pre_sort groups the tiles so). The check keeps every
+    // read inside the expert's own bytes whatever the grouping gave; the
+    // item is uniform over the workgroup, so the return is too.
+    {
+        const int k = MODE == 0 ? 0 : 2;
+        const int fe = shared ? (MODE == 0 ? L.sg.fmt : L.sd.fmt)
+                              : L.pk[k].regular ? L.pk[k].fmt : L.experts[mid_e].fmt[k];
+        if (fe != F) return;
+    }
     const uint32_t K = MODE == 0 ? L.hidden : L.inter;
     const uint32_t nblk = K / 256;
     constexpr uint32_t NCH = raw_chunks(F);

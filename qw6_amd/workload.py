@@ -23,6 +23,13 @@ MIXES = {
     # one IQ format per matrix kind (as in a GGUF expert pack)
     "iq2a": (S.Q_IQ2_XXS, lambda e: S.Q_IQ3_S),
     "iq2b": (S.Q_IQ2_S, lambda e: S.Q_IQ2_S),
+    # routed gate/up formats that differ by expert (qw6 keeps a tensor per
+    # expert, qw6.h:160-162): IQ2_XXS / IQ3_S by parity with IQ3_S / IQ2_XXS
+    # downs; Q5_K / Q4_K by parity (two occupancy classes of the grouped
+    # kernels) with Q6_K downs
+    "iqgu": (lambda e: S.Q_IQ2_XXS if e % 2 == 0 else S.Q_IQ3_S,
+             lambda e: S.Q_IQ3_S if e % 2 == 0 else S.Q_IQ2_XXS),
+    "q5q4": (lambda e: S.Q_Q5_K if e % 2 == 0 else S.Q_Q4_K_M, lambda e: S.Q_Q6_K),
 }
 SHARED_Q = (S.Q_Q4_K_M, S.Q_Q4_K_M, S.Q_Q6_K)
 # shared expert formats where they differ from SHARED_Q: the same formats as
@@ -46,7 +53,8 @@ class SynthLayer:
         self.hidden, self.inter, self.n_experts, self.top_k = hidden, inter, n_experts, top_k
         dev = torch.device("cuda", ctx.device)
         gq, down_fn = MIXES[mix]
-        self.quants = [(gq, gq, down_fn(e)) for e in range(n_experts)]
+        gate_fn = gq if callable(gq) else (lambda e: gq)
+        self.quants = [(gate_fn(e), gate_fn(e), down_fn(e)) for e in range(n_experts)]
         shapes = ((inter, hidden), (inter, hidden), (hidden, inter))
         kinds = (S.K_GATE, S.K_UP, S.K_DOWN)
         self.packs, self.offsets, self.mats = [], [], []

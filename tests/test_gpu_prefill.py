@@ -315,6 +315,60 @@ def test_grouped_mixed_formats_vs_oracle(torch_dev, ctx):
         L.free()
 
 
+@pytest.mark.parametrize("mix", ["iqgu", "q5q4"])
+def test_mixed_gate_up_formats_vs_oracle(torch_dev, ctx, mix):
+    """Routed experts whose gate/up formats differ (qw6.h:160-162): IQ2_XXS /
+    IQ3_S gate/up by expert parity (downs IQ3_S / IQ2_XXS), and Q5_K / Q4_K
+    gate/up (downs Q6_K), whose grouped contractions are in different
+    occupancy classes and so run as separate launches. Grouped: T = 64
+    against the oracle, T = 512 against the fp32 per-token kernels and an
+    oracle sample. Per-token paths (automatic choice): T = 1-4 against the
+    oracle at the fp32 bar."""
+    from qw6_amd.workload import SynthLayer
+    L = SynthLayer(ctx, 68, 0, mix)
+    try:
+        T = 64
+        lg = S.zipf_logits(68, T)
+        xs = np.stack([cases.token_x(68, 1, t) for t in range(T)])
+        say("mixed gate/up %s grouped T=%d" % (mix, T))
+        out, idx, w = run(torch_dev, ctx, L, xs, logits=lg)
+        want = oracle_tokens(L, xs, lg, range(T))
+        rels = []
+        for t in range(T):
+            oo, oi, ow = want[t]
+            assert np.array_equal(idx[t], oi), t
+            assert np.abs(w[t] - ow).max() <= 2e-5
+            rels.append(cases.rel_l2(out[t], oo))
+        say("rel-L2 max %.2e mean %.2e" % (max(rels), np.mean(rels)))
+        assert max(rels) <= TOL_BF16 and np.mean(rels) <= TOL_MEAN
+        for Tp in (1, 2, 3, 4):
+            say("mixed gate/up %s per-token T=%d" % (mix, Tp))
+            o2, i2, _ = run(torch_dev, ctx, L, xs[:Tp], logits=lg[:Tp], mode=0)
+            for t in range(Tp):
+                oo, oi, _ = want[t]
+                assert np.array_equal(i2[t], oi), (Tp, t)
+                assert cases.rel_l2(o2[t], oo) <= 1e-5, (Tp, t)
+        T = 512
+        lg = S.zipf_logits(69, T)
+        xs = np.stack([cases.token_x(69, 3, t) for t in range(T)])
+        say("mixed gate/up %s grouped T=%d" % (mix, T))
+        g_out, g_idx, _ = run(torch_dev, ctx, L, xs, logits=lg, mode=2)
+        d_out, d_idx, _ = run(torch_dev, ctx, L, xs, logits=lg, mode=1)
+        assert np.array_equal(g_idx, d_idx)
+        rels = [cases.rel_l2(g_out[t], d_out[t]) for t in range(T)]
+        say("T=512 grouped vs per-token: max %.2e mean %.2e" % (max(rels), np.mean(rels)))
+        assert max(rels) <= TOL_BF16 and np.mean(rels) <= TOL_MEAN
+        sample = [0, 77, 255, 511]
+        want = oracle_tokens(L, xs, lg, sample)
+        for t in sample:
+            oo, oi, _ = want[t]
+            assert np.array_equal(g_idx[t], oi)
+            assert cases.rel_l2(g_out[t], oo) <= TOL_BF16
+            assert cases.rel_l2(d_out[t], oo) <= 1e-5
+    finally:
+        L.free()
+
+
 def test_grouped_small_batch_vs_golden(torch_dev, ctx):
     """The 4-token golden fixture (qw6's own layer on Zipf logits, with a
     residual) through the grouped kernels."""

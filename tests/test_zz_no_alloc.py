@@ -34,8 +34,11 @@ def test_noalloc_matches_moe_forward():
         dbig.norm_w, dbig.norm_eps = nw.data_ptr(), 1e-6
         # (layer, hidden, tokens, residual, mode): both entry points run the
         # same per-token kernels in the same mode (the regular one would take
-        # the grouped kernels for 5 tokens in mode 0)
-        calls = [(dbig, 2048, 3, True, 0), (dbig, 2048, 5, True, 1), (small.desc, 1024, 1, False, 0)]
+        # the grouped kernels for 5 tokens in mode 0). 8 tokens in mode 3 and
+        # 4 in mode 0 run the small-batch MFMA kernels (k_mx_*) on the static
+        # array's operand regions, in two 4-token launches and in one.
+        calls = [(dbig, 2048, 3, True, 0), (dbig, 2048, 8, True, 3), (dbig, 2048, 4, True, 0),
+                 (dbig, 2048, 5, True, 1), (small.desc, 1024, 1, False, 0)]
         # warm both paths once (first-use allocations of the regular path
         # and of the runtime happen here, not in the measured calls)
         for d, H, T, res, mode in calls:
