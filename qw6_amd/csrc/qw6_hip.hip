@@ -2647,14 +2647,12 @@ int ensure_prefill_ws(qw6_hip_ctx_t* c, uint32_t hidden, uint32_t inter, uint32_
     w.logits = (float*)p;
     if (alloc_owned(c, (size_t)T * hidden * 4, &p)) return -1;
     w.xn = (float*)p;
-    if (alloc_owned(c, (size_t)T * hidden * 2, &p)) return -1;
-    w.xh = (uint16_t*)p;
-    if (alloc_owned(c, (size_t)T * hidden * 2, &p)) return -1;
-    w.xl = (uint16_t*)p;
-    if (alloc_owned(c, E * inter * 2, &p)) return -1;
-    w.mid_h = (uint16_t*)p;
-    if (alloc_owned(c, E * inter * 2, &p)) return -1;
-    w.mid_l = (uint16_t*)p;
+    for (int k = 0; k < 3; k++) {   // bf16 parts of the input and of mid
+        if (alloc_owned(c, (size_t)T * hidden * 2, &p)) return -1;
+        w.xp[k] = (uint16_t*)p;
+        if (alloc_owned(c, E * inter * 2, &p)) return -1;
+        w.mp[k] = (uint16_t*)p;
+    }
     if (alloc_owned(c, (size_t)T * (hidden / 32) * 3 * 2, &p)) return -1;
     w.xs3 = (uint16_t*)p;
     if (alloc_owned(c, E * (inter / 32) * 3 * 2, &p)) return -1;

@@ -48,10 +48,9 @@ struct PrefillWs {
     uint32_t* fseg;      // [2][8][2] {first, count} of each format's group in forder
     float* logits;       // [T][n_experts]
     float* xn;           // [T][hidden] (RMSNorm of the input)
-    uint16_t* xh;        // [T][hidden] bf16 of the input
-    uint16_t* xl;        // [T][hidden] bf16 of the input's rounding residue
-    uint16_t* mid_h;     // [E][inter] bf16 of silu(gate) * up
-    uint16_t* mid_l;     // [E][inter] bf16 of its rounding residue
+    uint16_t* xp[3];     // [T][hidden] each: the input's P bf16 parts, part p at xp[p]
+                         // (hi, then lo for P = 2; hi, mid, lo for P = 3)
+    uint16_t* mp[3];     // [E][inter] each: the same parts of silu(gate) * up
     uint16_t* xs3;       // [T][hidden / 256][3][8] input sums per 32 columns, 3 bf16 parts
     uint16_t* ms3;       // [E][inter / 256][3][8] the same for mid
     float* ybuf;         // [E][hidden]
@@ -79,6 +78,10 @@ struct PrefillLayer {
 inline uint32_t prefill_entries(uint32_t T, uint32_t top_k) { return T * top_k + T; }
 // Entries per tile of the grouped kernels (one MFMA row group).
 constexpr uint32_t kPrefillTileEntries = 16;
+// Calls of fewer tokens split the activations into three bf16 parts (hi,
+// mid, lo: 24 significant bits, the fp32 bar); from this many on into two
+// (hi, lo: 16 bits), the bf16-MFMA bar, at the lower LDS cost.
+constexpr uint32_t kPrefill3PartBelow = 64;
 // Tiles of a batch at most: the routed entries in tiles of one expert each
 // (at most one partial tile per expert), then the shared expert's.
 __host__ __device__ inline uint32_t prefill_tiles_max(uint32_t T, uint32_t top_k, uint32_t n_experts) {

@@ -52,21 +52,42 @@ __device__ const IqTables g_tabs_pre = make_tables();
 constexpr uint32_t kPM = kPrefillTileEntries;   // entries per tile (one MFMA row group)
 constexpr uint32_t kPWG = 256;    // threads per workgroup (4 waves)
 
-// Eight floats -> bf16 hi and lo parts (hi = bf16(x), lo = bf16(x - hi)), packed
-// in MFMA operand order; returns sum(hi + lo) in fp32.
-__device__ __forceinline__ float split8(const float (&v)[8], uint4& h, uint4& l) {
-    uint32_t hw[4], lw[4];
+// One float as P bf16 parts: P = 2: hi = bf16(x), lo = bf16(x - hi); P = 3:
+// hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid). Returns the
+// represented value (the parts' sum in fp32, in part order), which is what
+// the MFMAs multiply and what the sub-block sums of the corrections add up.
+template <int P>
+__device__ __forceinline__ float split_parts(float x, __bf16& h, __bf16& m, __bf16& l) {
+    h = (__bf16)x;
+    const float r = x - (float)h;
+    if (P == 2) {
+        m = (__bf16)0.f;
+        l = (__bf16)r;
+        return (float)h + (float)l;
+    }
+    m = (__bf16)r;
+    l = (__bf16)(r - (float)m);
+    return ((float)h + (float)m) + (float)l;
+}
+
+// Eight floats -> their P bf16 parts, packed in MFMA operand order (m unused
+// for P = 2); returns the sum of the represented values in fp32.
+template <int P>
+__device__ __forceinline__ float split8(const float (&v)[8], uint4& h, uint4& m, uint4& l) {
+    uint32_t hw[4], mw[4], lw[4];
     float sum = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        const float x0 = v[2 * i], x1 = v[2 * i + 1];
-        const __bf16 h0 = (__bf16)x0, h1 = (__bf16)x1;
-        const __bf16 l0 = (__bf16)(x0 - (float)h0), l1 = (__bf16)(x1 - (float)h1);
-        sum += ((float)h0 + (float)l0) + ((float)h1 + (float)l1);
+        __bf16 h0, m0, l0, h1, m1, l1;
+        const float s0 = split_parts<P>(v[2 * i], h0, m0, l0);
+        const float s1 = split_parts<P>(v[2 * i + 1], h1, m1, l1);
+        sum += s0 + s1;
         hw[i] = bfb(h0) | (bfb(h1) << 16);
+        mw[i] = bfb(m0) | (bfb(m1) << 16);
         lw[i] = bfb(l0) | (bfb(l1) << 16);
     }
     h = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    m = make_uint4(mw[0], mw[1], mw[2], mw[3]);
     l = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     return sum;
 }
@@ -74,8 +95,9 @@ __device__ __forceinline__ float split8(const float (&v)[8], uint4& h, uint4& l)
 // ---- routing -----------------------------------------------------------------------
 
 // One workgroup of four waves per token t: wave 0 routes it (wave_route);
-// all four split its activations and take part in the shared-expert weight;
-// thread 0 writes the shared entry.
+// all four split its activations (into 3 bf16 parts for calls of fewer than
+// kPrefill3PartBelow tokens, else 2) and take part in the shared-expert
+// weight; thread 0 writes the shared entry.
 constexpr uint32_t kRouteThreads = 256;
 __global__ __launch_bounds__(kRouteThreads) void k_pre_route(PrefillLayer L, PrefillWs ws,
                                                              const float* __restrict__ xin,
@@ -106,10 +128,17 @@ __global__ __launch_bounds__(kRouteThreads) void k_pre_route(PrefillLayer L, Pre
         float v[8];
         const float4 a = ((const float4*)xr)[2 * c], b = ((const float4*)xr)[2 * c + 1];
         v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
-        uint4 h, l;
-        float sum = split8(v, h, l);
-        ((uint4*)(ws.xh + (size_t)t * L.hidden))[c] = h;
-        ((uint4*)(ws.xl + (size_t)t * L.hidden))[c] = l;
+        uint4 h, m, l;
+        float sum;
+        const bool three = L.T < kPrefill3PartBelow;
+        if (three) {
+            sum = split8<3>(v, h, m, l);
+            ((uint4*)(ws.xp[1] + (size_t)t * L.hidden))[c] = m;
+        } else {
+            sum = split8<2>(v, h, m, l);
+        }
+        ((uint4*)(ws.xp[0] + (size_t)t * L.hidden))[c] = h;
+        ((uint4*)(ws.xp[three ? 2 : 1] + (size_t)t * L.hidden))[c] = l;
         sum += partner(sum, 1, lane);
         sum += partner(sum, 2, lane);
         if ((c & 3u) == 0) {
@@ -301,8 +330,9 @@ __global__ __launch_bounds__(1024) void k_pre_sort(PrefillLayer L, PrefillWs ws)
 // Shared memory of k_pre_gemm: the A operands of the tile for one 256-column
 // block, operand-major so the operand reads (lane l reads 16 B at l) are
 // conflict-free; then the raw weight block bytes of the workgroup's rows.
+template <int P>
 struct GemmLds {
-    uint4 a[2][8][64];           // [hi, lo][sub-block][lane]
+    uint4 a[P][8][64];           // [part][sub-block][lane]: parts hi, (mid), lo
     float part[4][kPM];          // epilogue: per-wave sums of mid
     uint32_t raw[1];             // rows x raw_chunks(F) x 16 B
 };
@@ -328,11 +358,32 @@ __host__ __device__ constexpr int gemm_rt() {   // row tiles per wave
     return (F == F_Q6K || F == F_IQ3S) ? 2 : 4;   // larger raw blocks: fewer rows
 }
 
+// The A operand parts of sub-block sb (this lane's), and one product of them
+// with B: the parts' MFMAs chained into one fp32 accumulator, hi first.
+template <int P>
+struct AParts {
+    uint4 v[P];
+};
+template <int P>
+__device__ __forceinline__ AParts<P> a_parts(const GemmLds<P>& S, int sb, uint32_t lane) {
+    AParts<P> a;
+#pragma unroll
+    for (int p = 0; p < P; p++) a.v[p] = S.a[p][sb][lane];
+    return a;
+}
+template <int P>
+__device__ __forceinline__ f32x4 mfma_parts(const AParts<P>& a, const uint4& b) {
+    f32x4 c = mfma(a.v[0], b, f32x4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+    for (int p = 1; p < P; p++) c = mfma(a.v[p], b, c);
+    return c;
+}
+
 // The products of one block for RT row tiles: acc[r] += sum over sub-blocks
 // of d*sc * (codes . x), plus the bias / minimum corrections from one MFMA
 // each against the 3-part sums (sxa: A operand, zero in lanes q = 3).
-template <int F, int RT>
-__device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
+template <int F, int RT, int P>
+__device__ __forceinline__ void gemm_block(const GemmLds<P>& S, const uint8_t* tab,
                                            const uint32_t (&R)[RT], uint32_t lane,
                                            const uint4& sxa, f32x4 (&acc)[RT]) {
     constexpr float bias = F == F_Q6K ? 160.f : 128.f;
@@ -373,7 +424,7 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
                 db[r] = fmaf((float)(aux1 >> 28), d4[r], d8[r]);
             }
             __builtin_amdgcn_sched_barrier(0);
-            const uint4 ah = S.a[0][sb][lane], al = S.a[1][sb][lane];
+            const AParts<P> a = a_parts<P>(S, sb, lane);
             if (sb < 7) {
 #pragma unroll
                 for (int r = 0; r < RT; r++) {
@@ -385,8 +436,7 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
 #pragma unroll
             for (int r = 0; r < RT; r++) {
                 const uint4 b = apply_signs(g[r], sg[r]);
-                f32x4 c = mfma(ah, b, f32x4{0.f, 0.f, 0.f, 0.f});
-                c = mfma(al, b, c);
+                const f32x4 c = mfma_parts<P>(a, b);
 #pragma unroll
                 for (int j = 0; j < 4; j++) acc[r][j] = fmaf(db[r], c[j], acc[r][j]);
             }
@@ -434,14 +484,13 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
                 db[r] = fmaf((float)nib, d2[r], d[r]);
             }
             __builtin_amdgcn_sched_barrier(0);
-            const uint4 ah = S.a[0][sb][lane], al = S.a[1][sb][lane];
+            const AParts<P> a = a_parts<P>(S, sb, lane);
             if (sb < 7) load(sb + 1);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int r = 0; r < RT; r++) {
                 const uint4 b = apply_signs(u4(g1[r].x, g1[r].y, g2[r].x, g2[r].y), y[r]);
-                f32x4 c = mfma(ah, b, f32x4{0.f, 0.f, 0.f, 0.f});
-                c = mfma(al, b, c);
+                const f32x4 c = mfma_parts<P>(a, b);
 #pragma unroll
                 for (int j = 0; j < 4; j++) acc[r][j] = fmaf(db[r], c[j], acc[r][j]);
             }
@@ -491,17 +540,14 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
                 db2[r] = fmaf((float)(sc[r] >> 4), d4[r], d8[r]);
             }
             __builtin_amdgcn_sched_barrier(0);
-            const uint4 ah = S.a[0][sb][lane], al = S.a[1][sb][lane];
+            const AParts<P> a = a_parts<P>(S, sb, lane);
             if (sb < 7) load(sb + 1);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int r = 0; r < RT; r++) {
                 const uint4 b = apply_signs(bytes_bf16(g[r]), y[r]), z = u4(0, 0, 0, 0);
                 const uint4 b0 = q < 2 ? b : z, b1 = q < 2 ? z : b;
-                f32x4 c = mfma(ah, b0, f32x4{0.f, 0.f, 0.f, 0.f});
-                c = mfma(al, b0, c);
-                f32x4 c1 = mfma(ah, b1, f32x4{0.f, 0.f, 0.f, 0.f});
-                c1 = mfma(al, b1, c1);
+                const f32x4 c = mfma_parts<P>(a, b0), c1 = mfma_parts<P>(a, b1);
 #pragma unroll
                 for (int j = 0; j < 4; j++) acc[r][j] = fmaf(db2[r], c1[j], fmaf(db[r], c[j], acc[r][j]));
             }
@@ -528,20 +574,16 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
     // instead of 8 RT), against the A operands of the two sub-blocks
 #pragma unroll
     for (int p = 0; p < 4; p++) {
-        uint4 ah[2], al[2];
+        AParts<P> a[2];
 #pragma unroll
-        for (int t = 0; t < 2; t++) {
-            ah[t] = S.a[0][2 * p + t][lane];
-            al[t] = S.a[1][2 * p + t][lane];
-        }
+        for (int t = 0; t < 2; t++) a[t] = a_parts<P>(S, 2 * p + t, lane);
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             uint4 b[2];
             tile_codes<F>(S.raw, R[r], q, p, b[0], b[1]);
 #pragma unroll
             for (int t = 0; t < 2; t++) {
-                f32x4 c = mfma(ah[t], b[t], f32x4{0.f, 0.f, 0.f, 0.f});
-                c = mfma(al[t], b[t], c);
+                const f32x4 c = mfma_parts<P>(a[t], b[t]);
                 const float dsc = tile_dsc<F>(ts[r], 2 * p + t);
 #pragma unroll
                 for (int j = 0; j < 4; j++) acc[r][j] = fmaf(dsc, c[j], acc[r][j]);
@@ -563,13 +605,22 @@ __device__ __forceinline__ void gemm_block(const GemmLds& S, const uint8_t* tab,
 template <int F>
 __host__ __device__ constexpr bool gemm_aligned() { return F == F_Q4K || F == F_Q5K; }
 
-template <int F, uint32_t NR, uint32_t NP>
+// A operand pieces (16 B) per thread and block: P parts x 8 sub-blocks x 64
+// lanes over the workgroup's 256 threads. Thread (wave w, lane l) loads
+// pieces u = NU w + i (i < NU): part u / 8, sub-block u % 8 of entry l % 16,
+// columns 8 (l / 16) .. + 8; the pieces of a thread span at most two parts,
+// whose rows are arow0 (part (NU w) / 8) and arow1 (the next part).
+template <int P>
+__host__ __device__ constexpr uint32_t a_pieces() { return 2 * P; }
+
+template <int F, int P, uint32_t NR, uint32_t NP>
 __device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NP],
                                            const uint32_t (&piece)[NR], const uint8_t* m0,
                                            const uint8_t* m1, uint32_t sel,
-                                           const uint16_t* arow, const uint16_t* srow,
-                                           uint32_t sb0, uint32_t q, uint32_t kb,
-                                           u32x4 (&rawv)[NR], u32x4 (&av)[4], u32x4& sxv) {
+                                           const uint16_t* arow0, const uint16_t* arow1,
+                                           const uint16_t* srow, uint32_t ua, uint32_t q,
+                                           uint32_t kb, u32x4 (&rawv)[NR],
+                                           u32x4 (&av)[a_pieces<P>()], u32x4& sxv) {
     constexpr uint32_t bb = fmt_block_bytes(F);
 #pragma unroll
     for (uint32_t i = 0; i < NR; i++) {
@@ -584,7 +635,12 @@ __device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NP],
         }
     }
 #pragma unroll
-    for (uint32_t i = 0; i < 4; i++) av[i] = *(const u32x4*)(arow + kb * 256 + 32 * (sb0 + i) + 8 * q);
+    for (uint32_t i = 0; i < a_pieces<P>(); i++) {
+        const uint32_t u = ua + i;
+        // (P = 2: the four pieces of a thread are in one part)
+        const uint16_t* ar = P == 2 || (u >> 3) == (ua >> 3) ? arow0 : arow1;
+        av[i] = *(const u32x4*)(ar + kb * 256 + 32 * (u & 7u) + 8 * q);
+    }
     sxv = *(const u32x4*)(srow + kb * 24 + 8 * min(q, 2u));
 }
 
@@ -602,9 +658,14 @@ __device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NP],
 // for three (Q4_K and IQ2_S) or with room for two (the others, whose
 // allocations fit three workgroups per CU all the same).
 __host__ __device__ constexpr int gemm_class(int f) { return f == F_Q5K ? 2 : 3; }
-template <int F, int FS>
+// Three activation parts (launches of fewer than kPrefill3PartBelow tokens)
+// add 8 KB of A operands, so LDS fits two workgroups per CU: they take the
+// register budget of two.
+template <int F, int FS, int P>
 __host__ __device__ constexpr int gemm_min_blocks() {
-    return F == FS ? ((F == F_Q4K || F == F_IQ2S) ? 3 : 2) : (gemm_class(F) < gemm_class(FS) ? gemm_class(F) : gemm_class(FS));
+    return P == 3 ? 2
+                  : F == FS ? ((F == F_Q4K || F == F_IQ2S) ? 3 : 2)
+                            : (gemm_class(F) < gemm_class(FS) ? gemm_class(F) : gemm_class(FS));
 }
 template <int MODE, int F>
 __host__ __device__ inline uint32_t gemm_ny(uint32_t hidden, uint32_t inter) {   // row blocks
@@ -628,16 +689,17 @@ __host__ __device__ constexpr bool gemm_tail_split() {
 // a row needs where that many would put the 16 rows of a row tile on two of
 // the 64 banks (IQ3_S: 8 chunks, 128 bytes; 9 spread them over all 16).
 __host__ __device__ constexpr uint32_t raw_stride(int f) { return raw_chunks(f) + (f == F_IQ3S ? 1u : 0u); }
-template <int MODE, int F>
+template <int MODE, int F, int P>
 __host__ __device__ constexpr size_t gemm_lds() {
-    return offsetof(GemmLds, raw) + (size_t)64 * gemm_rt<MODE, F>() * raw_stride(F) * 16 + gemm_grid_bytes(F);
+    return offsetof(GemmLds<P>, raw) + (size_t)64 * gemm_rt<MODE, F>() * raw_stride(F) * 16 + gemm_grid_bytes(F);
 }
 
-// Row block yb of tile `tile` (format F), RT row tiles per wave.
-template <int MODE, int F, int RT = gemm_rt<MODE, F>()>
+// Row block yb of tile `tile` (format F), RT row tiles per wave, the
+// activations in P bf16 parts.
+template <int MODE, int F, int P, int RT = gemm_rt<MODE, F>()>
 __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs& ws, uint4 tile,
                                           uint32_t yb, uint8_t* smem) {
-    GemmLds& S = *(GemmLds*)smem;
+    GemmLds<P>& S = *(GemmLds<P>*)smem;
     const uint32_t mid_e = tile.x, ent0 = tile.y, cnt = tile.z;
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u;
     const uint32_t n = lane & 15u, q = lane >> 4;
@@ -690,19 +752,24 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
             rrow[r] = 16 * RT * wave + 16 * r + n;
     }
 
-    // A operands: thread (wave w, lane l) loads half hl = w / 2 of entry
-    // l % 16 (clamped into the tile), columns 8 (l / 16) .. + 8 of sub-blocks
-    // 4 (w % 2) .. + 4; the 3-part sub-block sums of entry l % 16 (part l / 16)
+    // A operands: thread (wave w, lane l) loads pieces NU w .. NU w + NU - 1
+    // (load_block) of entry l % 16 (clamped into the tile); the 3-part
+    // sub-block sums of entry l % 16 (part l / 16)
     const uint32_t sm = min(n, cnt - 1);
-    const uint32_t hl = wave >> 1, sb0 = 4 * (wave & 1u);
-    const uint16_t* arow;
+    constexpr uint32_t NU = a_pieces<P>();
+    const uint32_t ua = NU * (uint32_t)__builtin_amdgcn_readfirstlane(wave);
+    const uint32_t pa = ua >> 3, pb = min(pa + 1, (uint32_t)P - 1);   // the thread's two parts
+    const uint16_t* arow0;
+    const uint16_t* arow1;
     const uint16_t* srow;
     if (MODE == 0) {
         const uint32_t tok = ws.ent_tok[ent0 + sm];
-        arow = (hl ? ws.xl : ws.xh) + (size_t)tok * L.hidden;
+        arow0 = (pa == 0 ? ws.xp[0] : pa == 1 ? ws.xp[1] : ws.xp[2]) + (size_t)tok * L.hidden;
+        arow1 = (pb == 0 ? ws.xp[0] : pb == 1 ? ws.xp[1] : ws.xp[2]) + (size_t)tok * L.hidden;
         srow = ws.xs3 + (size_t)tok * (L.hidden / 256) * 24;
     } else {
-        arow = (hl ? ws.mid_l : ws.mid_h) + (size_t)(ent0 + sm) * L.inter;
+        arow0 = (pa == 0 ? ws.mp[0] : pa == 1 ? ws.mp[1] : ws.mp[2]) + (size_t)(ent0 + sm) * L.inter;
+        arow1 = (pb == 0 ? ws.mp[0] : pb == 1 ? ws.mp[1] : ws.mp[2]) + (size_t)(ent0 + sm) * L.inter;
         srow = ws.ms3 + (size_t)(ent0 + sm) * (L.inter / 256) * 24;
     }
     constexpr bool kAl = gemm_aligned<F>();
@@ -724,7 +791,7 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
         }
     }
     if constexpr (kAl) rowp[0] = nullptr;
-    u32x4 rawv[NR], av[4], sxv;
+    u32x4 rawv[NR], av[NU], sxv;
     uint8_t* tab = (uint8_t*)S.raw + (size_t)ROWS * RS * 16;   // IQ lattice grid
     if constexpr (F == F_IQ2S) {   // the byte grid (visible after the loop's first barrier)
         for (uint32_t i = tid; i < 1024; i += kPWG) ((uint2*)tab)[i] = u64_as_u2(g_tabs_pre.iq2s[i]);
@@ -734,7 +801,7 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
     f32x4 acc[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) acc[r] = f32x4{0.f, 0.f, 0.f, 0.f};
-    load_block<F, NR>(rowp, piece, m0, m1, psel, arow, srow, sb0, q, 0, rawv, av, sxv);
+    load_block<F, P, NR>(rowp, piece, m0, m1, psel, arow0, arow1, srow, ua, q, 0, rawv, av, sxv);
     for (uint32_t kb = 0; kb < nblk; kb++) {
         __syncthreads();   // every wave is done with block kb - 1's LDS data
 #pragma unroll
@@ -743,21 +810,22 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
             if (i + 1 < NR || last) *(u32x4*)((uint8_t*)S.raw + 16u * (c / NCH * RS + c % NCH)) = rawv[i];
         }
 #pragma unroll
-        for (uint32_t i = 0; i < 4; i++) *(u32x4*)&S.a[hl][sb0 + i][lane] = av[i];
+        for (uint32_t i = 0; i < NU; i++) ((u32x4*)&S.a[0][0][0])[(ua + i) * 64 + lane] = av[i];
         const uint4 sxa = q < 3 ? u4(sxv.x, sxv.y, sxv.z, sxv.w) : u4(0, 0, 0, 0);
-        if (kb + 1 < nblk) load_block<F, NR>(rowp, piece, m0, m1, psel, arow, srow, sb0, q, kb + 1, rawv, av, sxv);
+        if (kb + 1 < nblk)
+            load_block<F, P, NR>(rowp, piece, m0, m1, psel, arow0, arow1, srow, ua, q, kb + 1, rawv, av, sxv);
         __syncthreads();   // block kb's bytes are in LDS
         uint32_t R[RT];
 #pragma unroll
         for (int r = 0; r < RT; r++)
             R[r] = rrow[r] * RS * 16 +
                    (kAl ? 0u : (uint32_t)((uintptr_t)(row_ptr(rrow[r]) + (size_t)kb * bb) & 15u));
-        gemm_block<F, RT>(S, tab, R, lane, sxa, acc);
+        gemm_block<F, RT, P>(S, tab, R, lane, sxa, acc);
     }
 
     // epilogue: lane holds entries 4 q + j of row n of its tiles
     if (MODE == 0) {
-        // mid = silu(gate) * up as bf16 hi / lo, plus the 32-row sums of mid:
+        // mid = silu(gate) * up as its P bf16 parts, plus the 32-row sums of mid:
         // wave w's 8 RT rows are part of sub-block (r0 + 8 RT w) / 32. Each
         // 16-row tile is summed over its lanes first and the tiles are added in
         // row order, so a sub-block's sum rounds the same for every tile shape.
@@ -772,11 +840,12 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
                 if (m < cnt) {
                     const float gv = acc[r][j], uv = acc[r + RT / 2][j];
                     const float y = gv / (1.0f + expf(-gv)) * uv;
-                    const __bf16 h = (__bf16)y, l = (__bf16)(y - (float)h);
+                    __bf16 h, md, l;
+                    hs = split_parts<P>(y, h, md, l);
                     const size_t o = (size_t)(ent0 + m) * L.inter + r0 + 8 * RT * wave + 16 * r + n;
-                    ws.mid_h[o] = __builtin_bit_cast(uint16_t, h);
-                    ws.mid_l[o] = __builtin_bit_cast(uint16_t, l);
-                    hs = (float)h + (float)l;
+                    ws.mp[0][o] = __builtin_bit_cast(uint16_t, h);
+                    if (P == 3) ws.mp[1][o] = __builtin_bit_cast(uint16_t, md);
+                    ws.mp[P - 1][o] = __builtin_bit_cast(uint16_t, l);
                 }
                 psum += group_sum<16>(hs);   // over the 16 rows n of tile r
             }
@@ -828,8 +897,8 @@ __device__ __forceinline__ void gemm_item(const PrefillLayer& L, const PrefillWs
 // blocks of one tile (same A rows) and the tiles of one expert (same
 // weights) then share that XCD's L2, and every XCD gets the same share of
 // each format.
-template <int MODE, int F, int FS>
-__global__ __launch_bounds__(kPWG, (gemm_min_blocks<F, FS>()))
+template <int MODE, int F, int FS, int P>
+__global__ __launch_bounds__(kPWG, (gemm_min_blocks<F, FS, P>()))
 void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     if constexpr (gemm_tail_split<MODE, F, FS>()) {
@@ -860,13 +929,13 @@ void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
         const uint4 tile = ws.tiles[oi];
         if constexpr (F != FS) {
             if (seg == 0) {
-                gemm_item<MODE, F>(L, ws, tile, it % ny_f, smem);
+                gemm_item<MODE, F, P>(L, ws, tile, it % ny_f, smem);
                 return;
             }
         }
         constexpr int RT = gemm_rt<MODE, FS>();
-        if (seg == 2) gemm_item<MODE, FS, RT / 2>(L, ws, tile, it % ny2, smem);
-        else gemm_item<MODE, FS, RT>(L, ws, tile, it % ny4, smem);
+        if (seg == 2) gemm_item<MODE, FS, P, RT / 2>(L, ws, tile, it % ny2, smem);
+        else gemm_item<MODE, FS, P, RT>(L, ws, tile, it % ny4, smem);
         return;
     }
     const uint32_t ny_a = gemm_ny<MODE, F>(L.hidden, L.inter);
@@ -887,10 +956,10 @@ void k_pre_gemm(PrefillLayer L, PrefillWs ws) {
     if (oi >= ws.n_tiles[0] + ws.n_tiles[1]) return;   // not a tile of this call
     const uint4 tile = ws.tiles[oi];
     if constexpr (FS == F) {
-        gemm_item<MODE, F>(L, ws, tile, it % ny, smem);
+        gemm_item<MODE, F, P>(L, ws, tile, it % ny, smem);
     } else {
-        if (in_b) gemm_item<MODE, FS>(L, ws, tile, it % ny, smem);
-        else gemm_item<MODE, F>(L, ws, tile, it % ny, smem);
+        if (in_b) gemm_item<MODE, FS, P>(L, ws, tile, it % ny, smem);
+        else gemm_item<MODE, F, P>(L, ws, tile, it % ny, smem);
     }
 }
 
@@ -972,36 +1041,37 @@ __global__ __launch_bounds__(64) void k_pre_router(const float* __restrict__ rou
     }
 }
 
-template <int MODE, int F, int FS>
+template <int MODE, int F, int FS, int P>
 void launch_gemm_ff(const PrefillLayer& L, const PrefillWs& ws, uint32_t cap, hipStream_t st) {
-    const size_t lds = gemm_lds<MODE, F>() > gemm_lds<MODE, FS>() ? gemm_lds<MODE, F>() : gemm_lds<MODE, FS>();
+    const size_t lds = gemm_lds<MODE, F, P>() > gemm_lds<MODE, FS, P>() ? gemm_lds<MODE, F, P>()
+                                                                        : gemm_lds<MODE, FS, P>();
     uint32_t ny_a = gemm_ny<MODE, F>(L.hidden, L.inter), ny_b = gemm_ny<MODE, FS>(L.hidden, L.inter);
     if (gemm_tail_split<MODE, F, FS>()) ny_b = 2 * ny_b;   // at most every FS tile at half the rows
     // at most cap tiles in all; the kernel maps workgroups to its groups'
     // items, per XCD a rounded-up share of each group
     const uint32_t nwg = (cap * (ny_a > ny_b ? ny_a : ny_b) + 7) / 8 * 8 +
                          (gemm_tail_split<MODE, F, FS>() ? 24u : FS != F ? 8u : 0u);
-    k_pre_gemm<MODE, F, FS><<<nwg, kPWG, lds, st>>>(L, ws);
+    k_pre_gemm<MODE, F, FS, P><<<nwg, kPWG, lds, st>>>(L, ws);
 }
 // Groups of one occupancy class only (no other pair is instantiated).
-template <int MODE, int F, int FS>
+template <int MODE, int F, int FS, int P>
 int launch_pair(const PrefillLayer& L, const PrefillWs& ws, uint32_t cap, hipStream_t st) {
     if constexpr (gemm_class(F) == gemm_class(FS)) {
-        launch_gemm_ff<MODE, F, FS>(L, ws, cap, st);
+        launch_gemm_ff<MODE, F, FS, P>(L, ws, cap, st);
         return 0;
     } else {
         return qw6_fail("batched path: formats %d and %d paired across occupancy classes", F, FS);
     }
 }
-template <int MODE, int F>
+template <int MODE, int F, int P>
 int launch_gemm_f(int fs, const PrefillLayer& L, const PrefillWs& ws, uint32_t cap, hipStream_t st) {
     switch (fs) {
-    case F_Q4K: return launch_pair<MODE, F, F_Q4K>(L, ws, cap, st);
-    case F_Q5K: return launch_pair<MODE, F, F_Q5K>(L, ws, cap, st);
-    case F_Q6K: return launch_pair<MODE, F, F_Q6K>(L, ws, cap, st);
-    case F_IQ2XXS: return launch_pair<MODE, F, F_IQ2XXS>(L, ws, cap, st);
-    case F_IQ2S: return launch_pair<MODE, F, F_IQ2S>(L, ws, cap, st);
-    default: return launch_pair<MODE, F, F_IQ3S>(L, ws, cap, st);
+    case F_Q4K: return launch_pair<MODE, F, F_Q4K, P>(L, ws, cap, st);
+    case F_Q5K: return launch_pair<MODE, F, F_Q5K, P>(L, ws, cap, st);
+    case F_Q6K: return launch_pair<MODE, F, F_Q6K, P>(L, ws, cap, st);
+    case F_IQ2XXS: return launch_pair<MODE, F, F_IQ2XXS, P>(L, ws, cap, st);
+    case F_IQ2S: return launch_pair<MODE, F, F_IQ2S, P>(L, ws, cap, st);
+    default: return launch_pair<MODE, F, F_IQ3S, P>(L, ws, cap, st);
     }
 }
 
@@ -1009,8 +1079,8 @@ int launch_gemm_f(int fs, const PrefillLayer& L, const PrefillWs& ws, uint32_t c
 // expert's `fsh`, or -1), up to two to a launch: in the order the shared
 // expert's group (when no routed expert has its format), then the routed
 // groups by format, each group not yet launched takes the next one of its
-// occupancy class as its partner.
-template <int MODE>
+// occupancy class as its partner. P: the activations' bf16 parts.
+template <int MODE, int P>
 int launch_gemm(uint32_t routed, int fsh, const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) {
     const uint32_t cap = prefill_tiles_max(L.T, L.top_k, L.n_experts);
     int order[F_NFMT + 1], n = 0;
@@ -1030,12 +1100,12 @@ int launch_gemm(uint32_t routed, int fsh, const PrefillLayer& L, const PrefillWs
             }
         int rc;
         switch (fa) {
-        case F_Q4K: rc = launch_gemm_f<MODE, F_Q4K>(fb, L, ws, cap, st); break;
-        case F_Q5K: rc = launch_gemm_f<MODE, F_Q5K>(fb, L, ws, cap, st); break;
-        case F_Q6K: rc = launch_gemm_f<MODE, F_Q6K>(fb, L, ws, cap, st); break;
-        case F_IQ2XXS: rc = launch_gemm_f<MODE, F_IQ2XXS>(fb, L, ws, cap, st); break;
-        case F_IQ2S: rc = launch_gemm_f<MODE, F_IQ2S>(fb, L, ws, cap, st); break;
-        default: rc = launch_gemm_f<MODE, F_IQ3S>(fb, L, ws, cap, st); break;
+        case F_Q4K: rc = launch_gemm_f<MODE, F_Q4K, P>(fb, L, ws, cap, st); break;
+        case F_Q5K: rc = launch_gemm_f<MODE, F_Q5K, P>(fb, L, ws, cap, st); break;
+        case F_Q6K: rc = launch_gemm_f<MODE, F_Q6K, P>(fb, L, ws, cap, st); break;
+        case F_IQ2XXS: rc = launch_gemm_f<MODE, F_IQ2XXS, P>(fb, L, ws, cap, st); break;
+        case F_IQ2S: rc = launch_gemm_f<MODE, F_IQ2S, P>(fb, L, ws, cap, st); break;
+        default: rc = launch_gemm_f<MODE, F_IQ3S, P>(fb, L, ws, cap, st); break;
         }
         if (rc) return -1;
         const hipError_t e = hipGetLastError();
@@ -1081,8 +1151,14 @@ int prefill_forward(const PrefillLayer& L, const PrefillWs& ws, hipStream_t st) 
     k_pre_sort<<<1, 1024, 0, st>>>(Lx, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return qw6_fail("batched routing launch: %s", hipGetErrorString(e));
-    if (launch_gemm<0>(L.fmask_gu, L.sg.p ? L.sg.fmt : -1, Lx, ws, st)) return -1;
-    if (launch_gemm<1>(L.fmask_dn, L.sg.p ? L.sd.fmt : -1, Lx, ws, st)) return -1;
+    // the activations' bf16 parts (k_pre_route split them the same way)
+    if (L.T < kPrefill3PartBelow) {
+        if (launch_gemm<0, 3>(L.fmask_gu, L.sg.p ? L.sg.fmt : -1, Lx, ws, st)) return -1;
+        if (launch_gemm<1, 3>(L.fmask_dn, L.sg.p ? L.sd.fmt : -1, Lx, ws, st)) return -1;
+    } else {
+        if (launch_gemm<0, 2>(L.fmask_gu, L.sg.p ? L.sg.fmt : -1, Lx, ws, st)) return -1;
+        if (launch_gemm<1, 2>(L.fmask_dn, L.sg.p ? L.sd.fmt : -1, Lx, ws, st)) return -1;
+    }
     k_pre_combine<<<dim3(L.T, (L.hidden / 4 + 255) / 256), 256, 0, st>>>(Lx, ws);
     e = hipGetLastError();
     if (e != hipSuccess) return qw6_fail("batched combine launch: %s", hipGetErrorString(e));

@@ -263,8 +263,8 @@ def test_auto_mode_mixed_chunks_vs_oracle(torch_dev, ctx):
     grouped kernels) runs launches of up to 4 tokens -- 5 tokens = 4 on the
     MFMA kernels then 1 on the fp32 kernels, 6 = 4 (MFMA) + 2 (fp32), 7 = 4
     (MFMA) + 3 (MFMA, as for mixed formats); the automatic path of the same
-    calls takes the grouped kernels (one launch per down format, held to
-    2e-5 as for every grouped call below 64 tokens). A uniform Q4_K layer
+    calls takes the grouped kernels (one launch per down format, held to the
+    fp32 bar 1e-5 as every grouped call below 64 tokens). A uniform Q4_K layer
     under the per-token mode (1) takes 4 + 1 on the fp32 kernels."""
     torch = torch_dev
     from qw6_amd.workload import SynthLayer
@@ -281,7 +281,7 @@ def test_auto_mode_mixed_chunks_vs_oracle(torch_dev, ctx):
             torch.cuda.synchronize()
             n += check_tokens(L, xs, dout.cpu().numpy(), didx.cpu().numpy(), router=router)
             out, idx = run(torch_dev, ctx, L, xs, 0)
-            n += check_tokens(L, xs, out, idx, router=router, tol=2e-5)
+            n += check_tokens(L, xs, out, idx, router=router, tol=1e-5)
         assert n >= 30
     finally:
         L.free()

@@ -2,9 +2,10 @@
 C ABI. Bars: expert indices exact for given router logits. Outputs: calls of
 64 tokens or more, rel-L2 <= 2e-3 per token (the bf16-MFMA bar) with a mean
 <= 1e-4; calls of fewer tokens (where the automatic path also takes these
-kernels) are held near the fp32 bar: rel-L2 <= 2e-5 per token and <= 1e-5 in
-the mean (the construction -- exact integer codes, hi/lo activations, fp32
-scales -- measures 4e-6 to 1.05e-5 per token). The full T = 512 batch is
+kernels) are held to the fp32 bar, rel-L2 <= 1e-5 per token: they split the
+activations into three bf16 parts (hi, mid, lo: 24 significant bits) beside
+the exact integer weight codes and fp32 scales, where calls of 64 tokens or
+more use two (hi, lo). The full T = 512 batch is
 checked against the per-token fp32 kernels of the same library (a
 size-independent consistency check) and on a sample of tokens against the
 oracle.
@@ -25,7 +26,7 @@ pytestmark = pytest.mark.gpu
 
 TOL_BF16 = 2e-3
 TOL_MEAN = 1e-4
-TOL_SMALL = 2e-5        # fewer than 64 tokens: per token
+TOL_SMALL = 1e-5        # fewer than 64 tokens: per token (three activation parts)
 TOL_SMALL_MEAN = 1e-5   # and in the mean
 
 
