@@ -10,6 +10,17 @@ namespace qw6 {
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
 
+// A load through a pointer to device global memory, emitted as a global
+// load. A load through a generic pointer whose address space the compiler
+// cannot infer (one read from memory, or a select of such pointers) is a
+// FLAT load, which also counts in lgkmcnt: every later wait for an LDS
+// operation then waits for it too, and a load issued ahead for the next
+// step holds up the current step's LDS reads.
+template <typename T>
+__device__ __forceinline__ T ld_global(const void* p) {
+    return *(const __attribute__((address_space(1))) T*)p;
+}
+
 // One weight matrix on the device (fmt: internal format, -1 = F32).
 struct MatD {
     const uint8_t* p;

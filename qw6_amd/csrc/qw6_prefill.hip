@@ -626,12 +626,12 @@ __device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NP],
     for (uint32_t i = 0; i < NR; i++) {
         if constexpr (gemm_aligned<F>()) {   // piece[i]: byte offset of the piece at block 0
             const uint8_t* base = (sel >> i) & 1u ? m1 : m0;
-            rawv[i] = *(const u32x4*)(base + piece[i] + kb * bb);
+            rawv[i] = ld_global<u32x4>(base + piece[i] + kb * bb);
         } else {
             const uint8_t* p = rowp[i] + (size_t)kb * bb;
             const uint32_t off = (uint32_t)((uintptr_t)p & 15u);
             const uint32_t ch = 16 * piece[i] < off + bb ? piece[i] : 0u;
-            rawv[i] = *(const u32x4*)(p - off + 16 * ch);
+            rawv[i] = ld_global<u32x4>(p - off + 16 * ch);
         }
     }
 #pragma unroll
