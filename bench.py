@@ -331,6 +331,23 @@ def algorithmic_bytes(pool, sel, hidden=HIDDEN, inter=INTER):
     return r_b, gu_b, d_b, step_b
 
 
+def hbm_roofline(nbytes, us):
+    """Roofline of an HBM-bound call: the bytes it must read over its time."""
+    gbps = nbytes / us / 1e3
+    return {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "bytes": int(nbytes)}
+
+
+def flop_roofline(flops, nbytes, us):
+    """Roofline of a batched call: its FLOP rate against the lower of the bf16
+    MFMA peak and arithmetic intensity x HBM peak."""
+    tf = flops / (us * 1e-6) / 1e12
+    roof = min(MFMA_BF16_PEAK_TFLOPS, flops / nbytes * HBM_PEAK_GBPS / 1e3)
+    return {"bound": "hbm" if roof < MFMA_BF16_PEAK_TFLOPS else "mfma", "achieved": round(tf, 2),
+            "peak": round(roof, 1), "unit": "TFLOP/s", "frac": round(tf / roof, 4),
+            "flops": int(flops), "bytes": int(nbytes)}
+
+
 def capture_graph(torch, fn):
     """fn(stream) captured as one HIP graph on a side stream (after one eager
     call that makes first-use allocations); returns (graph, stream)."""
@@ -856,24 +873,40 @@ def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
     res_t2 = {"tokens": 2, "us_per_layer": round(us2, 3), "bytes": int(b2m),
               "hbm_GBps": round(b2m / us2 / 1e3, 1),
               "distinct_experts_mean": round(float(np.mean([len(np.unique(s)) for s in sel])), 2),
+              "roofline": hbm_roofline(b2m, us2),
               "workload": "T=2 through the per-token fp32 kernels with the router GEMV, "
                           "Q4_K/Q6_K layer pool"}
     # small batches through the automatic path: 3 tokens per launch take the
     # fp32 per-token kernels (one format per matrix kind), 4 the small-batch
     # MFMA kernels, 8 the grouped ones
-    small = {}
+    small, small_roof = {}, {}
     for Ts in (3, 4, 8):
         Xs = torch.empty(len(pool), Ts, HIDDEN, dtype=torch.float32, device="cuda")
         for j in range(len(pool)):
             Q.synth_normal(Xs[j], Ts * HIDDEN, 1.0, 4010 + Ts, S.stream_id(j, S.K_X))
         os_ = torch.empty_like(Xs)
+        is_ = torch.zeros(len(pool), Ts, TOP_K, dtype=torch.int32, device="cuda")
 
-        def fwds(sp, Ts=Ts, Xs=Xs, os_=os_):
+        def fwds(sp, Ts=Ts, Xs=Xs, os_=os_, is_=is_):
             for j in range(len(pool)):
-                ctx.moe_forward(pool[j].desc, Xs[j], os_[j], n_tok=Ts, stream=sp)
+                ctx.moe_forward(pool[j].desc, Xs[j], os_[j], n_tok=Ts, idx=is_[j], stream=sp)
         secs, _ = graph_time(torch, fwds, max(1, args.steps // len(pool)))
-        small["T%d" % Ts] = round(1e6 * secs / len(pool), 3)
+        us_s = 1e6 * secs / len(pool)
+        small["T%d" % Ts] = round(us_s, 3)
+        # bytes one call must read: the distinct selected experts' matrices,
+        # the shared expert, the router and the inputs (the 8-token calls
+        # take the grouped kernels: their roof is the lower of HBM and MFMA)
+        ss = is_.cpu().numpy()
+        bs = float(np.mean([sum(L.expert_bytes(int(e)) for e in np.unique(ss[j])) + L.shared_bytes()
+                            + N_EXPERTS * HIDDEN * 4 + 2 * Ts * HIDDEN * 4
+                            for j, L in enumerate(pool)]))
+        if Ts >= 5:
+            fl = 2.0 * (Ts * TOP_K + Ts) * 3 * HIDDEN * INTER
+            small_roof["T%d" % Ts] = flop_roofline(fl, bs, us_s)
+        else:
+            small_roof["T%d" % Ts] = hbm_roofline(bs, us_s)
     res_t2["small_batch_us_per_layer"] = small
+    res_t2["small_batch_roofline"] = small_roof
     return res, res_t2
 
 
