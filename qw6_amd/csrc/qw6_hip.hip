@@ -430,6 +430,31 @@ __device__ __forceinline__ MatD expert_mat_wave(const MoeArgs& a, uint32_t e, in
     return MatD{E.p[k], E.fmt[k], rows, cols, E.rb[k]};
 }
 
+// Format template argument of the expert kernels: F >= 0 one format known
+// at compile time; -1 any of the six (a switch per matrix); F <= -2 the set
+// of formats in the mask -(F + 2) (bit f: format f), a switch over those
+// only. A layer mixes two or three formats, and a switch over all six makes
+// the kernel three to six times the code of a one-format one.
+__host__ __device__ constexpr bool fmt_in(int FS, int f) {
+    return FS >= 0 ? FS == f : FS == -1 ? true : (((uint32_t)(-(FS + 2)) >> f) & 1u) != 0;
+}
+__host__ __device__ constexpr int fmt_set(uint32_t mask) { return -(int)mask - 2; }
+
+// fn(std::integral_constant<int, f>) for the runtime format f, compiled for
+// the formats of the set FS only (another f does nothing: the host passes the
+// set of the formats the layer holds).
+template <int FS, typename Fn>
+__device__ __forceinline__ void by_fmt(int f, Fn fn) {
+    switch (f) {
+    case F_Q4K: if constexpr (fmt_in(FS, F_Q4K)) fn(std::integral_constant<int, F_Q4K>{}); break;
+    case F_Q5K: if constexpr (fmt_in(FS, F_Q5K)) fn(std::integral_constant<int, F_Q5K>{}); break;
+    case F_Q6K: if constexpr (fmt_in(FS, F_Q6K)) fn(std::integral_constant<int, F_Q6K>{}); break;
+    case F_IQ2XXS: if constexpr (fmt_in(FS, F_IQ2XXS)) fn(std::integral_constant<int, F_IQ2XXS>{}); break;
+    case F_IQ2S: if constexpr (fmt_in(FS, F_IQ2S)) fn(std::integral_constant<int, F_IQ2S>{}); break;
+    default: if constexpr (fmt_in(FS, F_IQ3S)) fn(std::integral_constant<int, F_IQ3S>{}); break;
+    }
+}
+
 // Stage one step group (the rows one wave step covers: 8 GGUF blocks, a
 // multiple of 16 bytes, <= 1680 B) into a 2 KB LDS slot with exactly two
 // 16-byte direct-to-LDS loads per lane. Lanes past the group's end reload the
@@ -937,14 +962,11 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
         wave_gate_up<T, FG, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds);
         return;
     }
-    switch (G.fmt) {   // mixed formats: one switch per wave, each body specialised
-    case F_Q4K: wave_gate_up<T, F_Q4K, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_Q5K: wave_gate_up<T, F_Q5K, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_Q6K: wave_gate_up<T, F_Q6K, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_IQ2XXS: wave_gate_up<T, F_IQ2XXS, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_IQ2S: wave_gate_up<T, F_IQ2S, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    default: wave_gate_up<T, F_IQ3S, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    }
+    // mixed formats: one switch per wave, each body specialised
+    by_fmt<FG>(G.fmt, [&](auto fc) {
+        wave_gate_up<T, decltype(fc)::value, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds,
+                                                 slot_off, a.gu_pb, lds);
+    });
 }
 
 // One token, every gate/up pair of the layer in each workgroup: workgroup b
@@ -1014,14 +1036,11 @@ __global__ __launch_bounds__(64 * 9) void k_moe_gate_up1(MoeArgs a) {
         wave_gate_up<1, FG, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds);
         return;
     }
-    switch (G.fmt) {   // mixed formats: one switch per wave, each body specialised
-    case F_Q4K: wave_gate_up<1, F_Q4K, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_Q5K: wave_gate_up<1, F_Q5K, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_Q6K: wave_gate_up<1, F_Q6K, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_IQ2XXS: wave_gate_up<1, F_IQ2XXS, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    case F_IQ2S: wave_gate_up<1, F_IQ2S, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    default: wave_gate_up<1, F_IQ3S, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds); break;
-    }
+    // mixed formats: one switch per wave, each body specialised
+    by_fmt<FG>(G.fmt, [&](auto fc) {
+        wave_gate_up<1, decltype(fc)::value, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds,
+                                                 slot_off, a.gu_pb, lds);
+    });
 }
 
 // Down projection + combine for rows [r0, r0 + R), R = S * rps. Matrix m of
@@ -1149,14 +1168,9 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
         if (FD >= 0) {
             down_rows<T, FD, KU>((const uint32_t*)smem, boff, j, xr, ym);
         } else {   // mixed formats: one switch per matrix, each body specialised
-            switch (f) {
-            case F_Q4K: down_rows<T, F_Q4K, KU>((const uint32_t*)smem, boff, j, xr, ym); break;
-            case F_Q5K: down_rows<T, F_Q5K, KU>((const uint32_t*)smem, boff, j, xr, ym); break;
-            case F_Q6K: down_rows<T, F_Q6K, KU>((const uint32_t*)smem, boff, j, xr, ym); break;
-            case F_IQ2XXS: down_rows<T, F_IQ2XXS, KU>((const uint32_t*)smem, boff, j, xr, ym); break;
-            case F_IQ2S: down_rows<T, F_IQ2S, KU>((const uint32_t*)smem, boff, j, xr, ym); break;
-            default: down_rows<T, F_IQ3S, KU>((const uint32_t*)smem, boff, j, xr, ym); break;
-            }
+            by_fmt<FD>(f, [&](auto fc) {
+                down_rows<T, decltype(fc)::value, KU>((const uint32_t*)smem, boff, j, xr, ym);
+            });
         }
         TRACE_MARK_IF(first, 3, 1);
     };
@@ -2689,18 +2703,32 @@ struct MoeLaunch {
     uint32_t grid_b1, nw_b1;
     size_t lds_b1;
     int fg, fd;              // format of the gate/up (down) kernels, -1: mixed
+    uint32_t mg, md;         // the formats present (bit f: format f), gate/up and down
     size_t lds_b, lds_c;
     uint32_t grid_b, grid_c, nw_b, nw_c;
 };
 
+// The format sets with their own instantiations of the mixed-format expert
+// kernels (1-2 tokens, the model's row length): the IQ2_M layer's, IQ2_XXS
+// routed gate/up beside a Q4_K shared one, and IQ3_S / IQ2_S routed downs
+// beside a Q6_K shared one. Other mixes take the six-format switch.
+constexpr uint32_t kSetGateUpIq2m = (1u << F_Q4K) | (1u << F_IQ2XXS);
+constexpr uint32_t kSetDownIq2m = (1u << F_Q6K) | (1u << F_IQ2S) | (1u << F_IQ3S);
+
 // Run fn(IC<T>, IC<F>, IC<KU>) for the expert-kernel instantiation of T
-// tokens, format f and KU = K/32 units per row: format- and size-specialised
-// kernels for 1-2 tokens at the model's row length KU_fast, the generic
-// (format switch) kernel otherwise.
-template <int KU_fast, typename Fn>
-void launch_expert_kernel(int f, uint32_t T, uint32_t KU, Fn fn) {
+// tokens, format f (mask: the formats present) and KU = K/32 units per row:
+// format- and size-specialised kernels for 1-2 tokens at the model's row
+// length KU_fast (one format, or one of the sets above), the generic
+// (six-format switch) kernel otherwise.
+template <int KU_fast, uint32_t kSet, typename Fn>
+void launch_expert_kernel(int f, uint32_t mask, uint32_t T, uint32_t KU, Fn fn) {
     if (T <= 2 && f >= 0 && KU == (uint32_t)KU_fast) {
         launch_by_fmt(f, T, [&](auto tc, auto fc) { fn(tc, fc, IC<KU_fast>{}); });
+        return;
+    }
+    if (T <= 2 && f < 0 && KU == (uint32_t)KU_fast && mask == kSet) {
+        if (T == 1) fn(IC<1>{}, IC<fmt_set(kSet)>{}, IC<KU_fast>{});
+        else fn(IC<2>{}, IC<fmt_set(kSet)>{}, IC<KU_fast>{});
         return;
     }
     auto by_ku = [&](auto tc) {
@@ -2760,18 +2788,18 @@ int launch_moe(const MoeArgs& a, const MoeLaunch& m, hipStream_t st, hipEvent_t*
         return rc;
     }
     if (m.gu1) {
-        launch_expert_kernel<64>(m.fg, 1, a.hidden / 32, [&](auto, auto fc, auto kc) {
+        launch_expert_kernel<64, kSetGateUpIq2m>(m.fg, m.mg, 1, a.hidden / 32, [&](auto, auto fc, auto kc) {
             rc = launch_k(k_moe_gate_up1<decltype(fc)::value, decltype(kc)::value>, m.grid_b1,
                           64 * m.nw_b1, m.lds_b1, st, ev ? ev + 2 : nullptr, a);
         });
     } else {
-        launch_expert_kernel<64>(m.fg, a.T, a.hidden / 32, [&](auto tc, auto fc, auto kc) {
+        launch_expert_kernel<64, kSetGateUpIq2m>(m.fg, m.mg, a.T, a.hidden / 32, [&](auto tc, auto fc, auto kc) {
             rc = launch_k(k_moe_gate_up<decltype(tc)::value, decltype(fc)::value, decltype(kc)::value>,
                           m.grid_b, kWG, m.lds_b, st, ev ? ev + 2 : nullptr, a);
         });
     }
     if (rc) return rc;
-    launch_expert_kernel<16>(m.fd, a.T, a.inter / 32, [&](auto tc, auto fc, auto kc) {
+    launch_expert_kernel<16, kSetDownIq2m>(m.fd, m.md, a.T, a.inter / 32, [&](auto tc, auto fc, auto kc) {
         rc = launch_k(k_moe_down<decltype(tc)::value, decltype(fc)::value, decltype(kc)::value>,
                       m.grid_c, 64 * m.nw_c, m.lds_c, st, ev ? ev + 4 : nullptr, a);
     });
@@ -2902,6 +2930,8 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
     MoeLaunch m;
     m.fg = (has_sh && sg.fmt != E->fmt_gu) ? -1 : E->fmt_gu;
     m.fd = (has_sh && sd.fmt != E->fmt_dn) ? -1 : E->fmt_dn;
+    m.mg = (E->fmask_gu & ((1u << F_NFMT) - 1u)) | (has_sh ? 1u << sg.fmt : 0u);
+    m.md = (E->fmask_dn & ((1u << F_NFMT) - 1u)) | (has_sh ? 1u << sd.fmt : 0u);
     const uint32_t rpsg = 64 / (L->hidden / 32), rpsd = 64 / (L->inter / 32);
     // k_moe_gate_up: LDS pair slot of the widest (gate, up) step pair in use
     uint32_t pl = has_sh ? pair_loads(sg.fmt) : 1u;
