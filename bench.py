@@ -60,6 +60,14 @@ HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 HIDDEN, INTER, N_EXPERTS, TOP_K = 2048, 512, 256, 8
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "moe_gate_up_q4k_decode_traffic.json")
+# The headline's kernel instantiations in a trace or counter file (the
+# one-token kernels of the Q4_K / Q6_K layer at hidden 2048, inter 512:
+# router <T = 1, 8 float4 per lane>, gate/up <format 0 = Q4_K, 64 units per
+# row>, down <T = 1, format 2 = Q6_K, 16 units>). The default run dispatches
+# them first; other workloads of the same run use other instantiations or
+# come later.
+HEADLINE_KERNELS = {"k_moe_router": "k_moe_router<1, 8>", "k_moe_gate_up1": "k_moe_gate_up1<0, 64>",
+                    "k_moe_down": "k_moe_down<1, 2, 16>"}
 
 
 # --prefill-mix layer kinds and the formats they hold
@@ -160,8 +168,8 @@ def summarize_pmc(fetch_dir, write_dir, calib_mib, command):
     ck_w = pick(w, "MulFunctor")
     fac_f = nbytes / (f[ck_f][0] * 1024.0)
     fac_w = nbytes / (w[ck_w][0] * 1024.0)
-    gu_f = pick(f, "k_moe_gate_up1")
-    gu_w = pick(w, "k_moe_gate_up1")
+    gu_f = pick(f, HEADLINE_KERNELS["k_moe_gate_up1"])
+    gu_w = pick(w, HEADLINE_KERNELS["k_moe_gate_up1"])
     fetch = f[gu_f][0] * 1024.0 * fac_f
     write = w[gu_w][0] * 1024.0 * fac_w
     out = {
@@ -174,7 +182,8 @@ def summarize_pmc(fetch_dir, write_dir, calib_mib, command):
         "copy_kernel": {"bytes": nbytes, "fetch_KiB": f[ck_f][0], "write_KiB": w[ck_w][0],
                         "fetch_factor": fac_f, "write_factor": fac_w},
         "other_kernels_KiB": {k: [round(f[k][0], 1), round(w.get(k, (0.0, 0))[0], 1)]
-                              for k in f if k not in (gu_f, ck_f)},
+                              for k in f if k not in (gu_f, ck_f) and
+                              any(v in k for v in HEADLINE_KERNELS.values())},
         "command": command,
     }
     print(json.dumps(out, indent=1))
@@ -251,7 +260,9 @@ def summarize_stats(dirs, command):
 def summarize_trace(trace_dir, bench_json, command, plain_json=None):
     """Per-kernel duration statistics of a decode run's kernel trace, split
     into the run's phases by dispatch order (bench_decode's dispatch_plan:
-    every layer step dispatches each of the three kernels once, in order)."""
+    every layer step dispatches each of the three kernels once, in order).
+    The headline's instantiations are taken (HEADLINE_KERNELS), and of each
+    the first dispatches the plan counts: the headline workload runs first."""
     import numpy as np
     with open(bench_json) as fh:
         line = [l for l in fh if l.startswith("{")][-1]
@@ -265,13 +276,15 @@ def summarize_trace(trace_dir, bench_json, command, plain_json=None):
         with open(f) as fh:
             for r in csv.DictReader(fh):
                 name = r["Kernel_Name"]
-                if "k_moe_" not in name:
+                if not any(v in name for v in HEADLINE_KERNELS.values()):
                     continue
                 per.setdefault(name, []).append(
                     (int(r["Start_Timestamp"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
     total = sum(n for _, n in plan)
     if len(per) != 3:
         raise SystemExit("expected the three decode kernels, found %s" % sorted(per))
+    for name in per:   # the headline's dispatches come first
+        per[name] = sorted(per[name])[:total]
     order = sorted(per, key=lambda k: min(t for t, _ in per[k]))
     print("# Kernel durations of `%s` by phase (rocprofv3 kernel trace, %d dispatches per kernel)\n"
           % (bj["config"]["workload"], total))
