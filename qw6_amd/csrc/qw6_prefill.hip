@@ -653,7 +653,10 @@ __device__ __forceinline__ void load_block(const uint8_t* const (&rowp)[NP],
 // Occupancy class of a format's contraction: three workgroups per CU (at
 // most 168 VGPRs; 53 KB of LDS or less each) except Q5_K, whose body needs
 // up to 198 VGPRs (two). IQ2_S, with its grid kept as byte values, is in
-// the three-workgroup class. Format groups share a launch only within a
+// the three-workgroup class: at 168 VGPRs the gate/up launches whose first
+// group is IQ2_S keep 3 dwords in scratch, and the down launches pairing
+// Q4_K or IQ2_XXS with IQ2_S 5 (the others, IQ3_S + IQ2_S downs included,
+// none). Format groups share a launch only within a
 // class; a shared launch is built for its class, a single format's launch
 // for three (Q4_K and IQ2_S) or with room for two (the others, whose
 // allocations fit three workgroups per CU all the same).
