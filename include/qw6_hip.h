@@ -100,7 +100,8 @@ typedef struct {
 } qw6_hip_matrix_t;
 
 /* y[t][rows] = deq(W) x[t][cols] for t < n_tok tokens (x, y row-major,
- * device pointers). Role of qw6_vk_pipe_matvec (qw6_vk.c:2386-2430). */
+ * device pointers; x 16-byte aligned for a quantized W). Role of
+ * qw6_vk_pipe_matvec (qw6_vk.c:2386-2430). */
 int qw6_hip_matvec(qw6_hip_ctx_t *ctx, const qw6_hip_matrix_t *w,
                    const float *x, float *y, uint32_t n_tok, void *stream);
 
@@ -142,9 +143,10 @@ typedef struct {
  * [n_tok x n_experts] router logits (batched prefill). idx/w: optional device
  * outputs [n_tok x top_k] of the routing. residual: optional device
  * [n_tok x hidden] added to the output (hidden = resid + ffn, qw6.c:2482).
- * Tokens are processed per launch of up to 4 tokens (decode, MTP
- * verification) or by the grouped bf16-MFMA kernels (prefill); see
- * qw6_hip_set_mode. */
+ * x, out, residual and the layer's router, shared_router and norm_w are
+ * 16-byte aligned (a call with another alignment fails). Tokens are processed
+ * per launch of up to 4 tokens (decode, MTP verification) or by the grouped
+ * bf16-MFMA kernels (prefill); see qw6_hip_set_mode. */
 int qw6_hip_moe_forward(qw6_hip_ctx_t *ctx, const qw6_hip_moe_layer_t *layer,
                         const float *x, const float *logits,
                         const float *residual, uint32_t n_tok, float *out,
@@ -226,8 +228,9 @@ int qw6_hip_sampling_greedy_host(const float *logits, uint32_t n,
  * then qw6_cpu_argmax; the GPU path of qw6_vk_pipe_forward_greedy,
  * qw6_vk.c:3447-3478): logits = deq(W) rmsnorm(x) * norm_w, *token =
  * argmax(logits). W: [vocab x hidden] (GGUF format or F32); norm_w NULL skips
- * the norm; logits: device buffer of W->rows floats (written, as qw6's
- * scr_logits); token: one device uint32. Asynchronous on `stream`. */
+ * the norm; x and norm_w 16-byte aligned; logits: device buffer of W->rows
+ * floats (written, as qw6's scr_logits); token: one device uint32.
+ * Asynchronous on `stream`. */
 int qw6_hip_output_greedy(qw6_hip_ctx_t *ctx, const qw6_hip_matrix_t *w,
                           const float *x, const float *norm_w, float eps,
                           float *logits, uint32_t *token, void *stream);

@@ -2499,6 +2499,8 @@ int qw6_hip_matvec(qw6_hip_ctx_t* c, const qw6_hip_matrix_t* w, const float* x, 
     int f;
     if (check_matrix(w->quant, w->rows, w->cols, &f)) return -1;
     if ((uintptr_t)w->data & 15u) return fail("weight data not 16-byte aligned");
+    // the quantized kernels read the activations in 16-byte pieces
+    if (w->quant != 0 && ((uintptr_t)x & 15u)) return fail("x must be 16-byte aligned");
     DevGuard g(c->device);
     const uint32_t rb = w->quant == 0 ? w->cols * 4 : (w->cols / 256) * fmt_block_bytes(f);
     const MatD W = {(const uint8_t*)w->data, w->quant == 0 ? -1 : f, w->rows, w->cols, rb};
@@ -2825,8 +2827,8 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
     if (L->top_k == 0 || L->top_k > 8 || L->top_k > E->n) return fail("top_k %u out of range", L->top_k);
     if (!L->router && !logits) return fail("neither router nor logits given");
     if (((uintptr_t)L->router | (uintptr_t)x | (uintptr_t)out | (uintptr_t)L->shared_router |
-         (uintptr_t)L->norm_w) & 15u)
-        return fail("router, shared_router, norm_w, x and out must be 16-byte aligned");
+         (uintptr_t)L->norm_w | (uintptr_t)residual) & 15u)
+        return fail("router, shared_router, norm_w, x, residual and out must be 16-byte aligned");
     const bool has_sh = L->shared_gate.data != nullptr;
     MatD sg = {nullptr, 0, 0, 0, 0}, su = sg, sd = sg;
     uint32_t mgu = E->tmask_gu, mdn = E->tmask_dn;
@@ -3100,6 +3102,8 @@ int qw6_hip_output_greedy(qw6_hip_ctx_t* c, const qw6_hip_matrix_t* w, const flo
     int f;
     if (check_matrix(w->quant, w->rows, w->cols, &f)) return -1;
     if ((uintptr_t)w->data & 15u) return fail("weight data not 16-byte aligned");
+    // the head kernels read x and the norm weight in 16-byte pieces
+    if (((uintptr_t)x | (uintptr_t)norm_w) & 15u) return fail("x and norm_w must be 16-byte aligned");
     DevGuard g(c->device);
     const hipStream_t st = (hipStream_t)stream;
     if (ensure_argmax_ws(c)) return -1;

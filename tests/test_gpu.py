@@ -385,6 +385,19 @@ def test_error_paths(torch_dev, ctx, layers):
     shp[1] = (shp[1][0], shp[1][1], 1024, shp[1][3])
     with pytest.raises(Q.Qw6HipError, match="shape"):
         ctx.experts(L.mats[0], L.mats[1], shp)
+    # activations are read in 16-byte pieces: a pointer 4 bytes off is refused
+    # on the host, before any launch (the layer's residual, the device matvec's
+    # input, the output head's input and norm weight)
+    buf = torch.zeros(2048 + 4, dtype=torch.float32, device="cuda")
+    off = buf[1:1 + 2048]
+    with pytest.raises(Q.Qw6HipError, match="aligned"):
+        ctx.moe_forward(L.desc, x[:1], out[:1], n_tok=1, residual=off)
+    with pytest.raises(Q.Qw6HipError, match="aligned"):
+        ctx.matvec(L.mats[0][0], off, torch.zeros(512, dtype=torch.float32, device="cuda"))
+    with pytest.raises(Q.Qw6HipError, match="aligned"):   # expert 0's down: 2048 x 512
+        ctx.output_greedy(L.mats[2][0], off[:512], torch.zeros(2048, dtype=torch.float32, device="cuda"),
+                          torch.zeros(1, dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
 
 
 def test_given_logits_on_a_layer_with_router(torch_dev, ctx, layers):
