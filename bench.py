@@ -261,8 +261,9 @@ def summarize_trace(trace_dir, bench_json, command, plain_json=None):
     """Per-kernel duration statistics of a decode run's kernel trace, split
     into the run's phases by dispatch order (bench_decode's dispatch_plan:
     every layer step dispatches each of the three kernels once, in order).
-    The headline's instantiations are taken (HEADLINE_KERNELS), and of each
-    the first dispatches the plan counts: the headline workload runs first."""
+    Of each of the three kernels the instantiation dispatched first is taken
+    (the run's first decode workload: the headline's, HEADLINE_KERNELS, in the
+    default run), and of it the first dispatches the plan counts."""
     import numpy as np
     with open(bench_json) as fh:
         line = [l for l in fh if l.startswith("{")][-1]
@@ -276,14 +277,20 @@ def summarize_trace(trace_dir, bench_json, command, plain_json=None):
         with open(f) as fh:
             for r in csv.DictReader(fh):
                 name = r["Kernel_Name"]
-                if not any(v in name for v in HEADLINE_KERNELS.values()):
+                if _short_kernel(name).split("<")[0] not in HEADLINE_KERNELS:
                     continue
                 per.setdefault(name, []).append(
                     (int(r["Start_Timestamp"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    first = {}   # base kernel name -> its instantiation dispatched first
+    for name, d in per.items():
+        base = _short_kernel(name).split("<")[0]
+        if base not in first or min(d)[0] < min(per[first[base]])[0]:
+            first[base] = name
+    per = {name: per[name] for name in first.values()}
     total = sum(n for _, n in plan)
     if len(per) != 3:
         raise SystemExit("expected the three decode kernels, found %s" % sorted(per))
-    for name in per:   # the headline's dispatches come first
+    for name in per:   # the first workload's dispatches come first
         per[name] = sorted(per[name])[:total]
     order = sorted(per, key=lambda k: min(t for t, _ in per[k]))
     print("# Kernel durations of `%s` by phase (rocprofv3 kernel trace, %d dispatches per kernel)\n"
