@@ -144,16 +144,8 @@ __host__ __device__ inline uint16_t f2h_rne(float f) {
 }
 
 // ---- LDS byte readers ---------------------------------------------------------
-// s: LDS viewed as 32-bit words; off: byte offset. 2-byte-aligned dwords are
-// rebuilt from two aligned words (the staging buffers carry 16 bytes of pad).
+// s: LDS viewed as 32-bit words; off: byte offset.
 
-__device__ __forceinline__ uint32_t lds32(const uint32_t* s, uint32_t off) {
-    const uint32_t i = off >> 2;
-    return __builtin_amdgcn_alignbyte(s[i + 1], s[i], off & 3);
-}
-__device__ __forceinline__ uint32_t lds16(const uint32_t* s, uint32_t off) {
-    return (s[off >> 2] >> ((off & 2) * 8)) & 0xffffu;
-}
 __device__ __forceinline__ uint32_t lds8(const uint32_t* s, uint32_t off) {
     return (s[off >> 2] >> ((off & 3) * 8)) & 0xffu;
 }
