@@ -1374,7 +1374,6 @@ __global__ __launch_bounds__(512, 4) void k_mx_gate_up(MoeArgs a) {
     const uint32_t tid = threadIdx.x, wave = tid >> 6, lane = tid & 63u, nw = blockDim.x >> 6;
     const uint32_t ntile = a.inter / 16;
     const bool shared_wg = blockIdx.x < a.n_sh_wg;
-    const uint32_t nkb = a.hidden / 256;
     // routing waves load their logits first; every wave then loads the A
     // operands of its first block, which do not depend on the routing
     uint32_t keys[4];
@@ -2065,12 +2064,6 @@ int check_matrix(int quant, uint32_t rows, uint32_t cols, int* fmt) {
 }
 
 bool fast_k(uint32_t K) { return K == 256 || K == 512 || K == 1024 || K == 2048; }
-
-uint32_t min_rows_align(uint32_t rb) {   // rows r such that r * rb % 16 == 0
-    uint32_t r = 1;
-    while ((r * rb) & 15u) r <<= 1;
-    return r;
-}
 
 template <int V> using IC = std::integral_constant<int, V>;
 
