@@ -23,9 +23,12 @@
 //                 (+ residual), a fixed order: deterministic, no atomics.
 //
 // Numerics of the contraction (rel-L2 ~1e-5 against the fp32 CPU path):
-//  - weights enter the MFMA as their integer codes (qw6_tile.h);
-//  - activations enter as bf16 hi + lo (hi = bf16(x), lo = bf16(x - hi)), two
-//    MFMAs per 32-column sub-block;
+//  - weights enter the MFMA as their integer codes (qw6_tile.h; the IQ
+//    formats as their signed lattice values);
+//  - activations enter as P bf16 parts, one MFMA each per 32-column
+//    sub-block: hi + lo (hi = bf16(x), lo = bf16(x - hi)) for calls of
+//    kPrefill3PartBelow tokens or more, hi + mid + lo (24 significant bits)
+//    below that;
 //  - the fp32 sub-block scale d*sc multiplies each sub-block's 16x16 MFMA
 //    result; the code bias (128 or 160) and the K-quant minimum dmin*m, both
 //    of the form (per-row integer) x (per-token sub-block sum of x), take one
@@ -33,8 +36,9 @@
 //    eight sub-block sums in k-slots 0-7, 8-15, 16-23, B the integers.
 // Weight codes are decoded from the raw block bytes in LDS just before their
 // MFMAs, two sub-blocks at a time, so a wave keeps 4 row tiles in flight.
-// Sub-blocks are 32 columns in every format handled here (Q4_K, Q5_K, and
-// Q6_K under qw6's even-scale rule, qw6.c:1567-1570).
+// Sub-blocks are 32 columns in every format handled here (Q6_K under qw6's
+// even-scale rule, qw6.c:1567-1570; IQ2_S's two 16-column scales take one
+// MFMA pair each).
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
