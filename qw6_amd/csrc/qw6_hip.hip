@@ -11,6 +11,10 @@
 //                  expert into LDS with direct-to-LDS 16-byte loads,
 //                  dequantizing step s while step s+1 is in flight; writes
 //                  silu(gate) * up. One workgroup publishes the slot table.
+//                  k_moe_gate_up1 is its one-token form: each workgroup takes
+//                  one row tile of every selected expert and of the shared
+//                  one, a wave per matrix pair, each routed wave selecting
+//                  its own expert from the logits.
 //   k_moe_down   : one workgroup per tile of output rows, one wave per
 //                  selected expert (plus the shared one); per-expert row sums
 //                  meet in LDS and are combined in selection order, with the
