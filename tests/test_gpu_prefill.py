@@ -271,6 +271,38 @@ def test_grouped_full_batch_vs_per_token_kernels_and_oracle(torch_dev, ctx, laye
         assert cases.rel_l2(d_out[t], oo) <= 1e-5
 
 
+def test_grouped_long_batch_vs_per_token_kernels_and_oracle(torch_dev):
+    """T = 1500, a long prompt: not a multiple of the 16-entry tile, and its
+    12,000 (token, k) pairs take k_pre_sort three passes over its registers
+    (4,096 pairs a pass). Grouped result vs the fp32 per-token kernels for
+    every token (indices and gate weights equal), and vs the oracle on a
+    sample of tokens, in a context sized for it."""
+    from qw6_amd.workload import SynthLayer
+    c = Q.Context(0, max_tokens=1500)
+    L = SynthLayer(c, 62, 0, "q4k")
+    try:
+        T = 1500
+        lg = S.zipf_logits(64, T)
+        xs = np.stack([cases.token_x(64, 5, t) for t in range(T)])
+        g_out, g_idx, g_w = run(torch_dev, c, L, xs, logits=lg, mode=2)
+        d_out, d_idx, d_w = run(torch_dev, c, L, xs, logits=lg, mode=1)
+        assert np.array_equal(g_idx, d_idx)
+        assert np.abs(g_w - d_w).max() <= 2e-6
+        rels = [cases.rel_l2(g_out[t], d_out[t]) for t in range(T)]
+        say("T=1500 grouped vs per-token: max %.2e mean %.2e" % (max(rels), np.mean(rels)))
+        assert max(rels) <= TOL_BF16 and np.mean(rels) <= TOL_MEAN
+        sample = [0, 1, 511, 512, 1023, 1024, 1499]
+        want = oracle_tokens(L, xs, lg, sample)
+        for t in sample:
+            oo, oi, _ = want[t]
+            assert np.array_equal(g_idx[t], oi)
+            assert cases.rel_l2(g_out[t], oo) <= TOL_BF16
+            assert cases.rel_l2(d_out[t], oo) <= 1e-5
+    finally:
+        L.free()
+        c.close()
+
+
 def test_grouped_mixed_formats_vs_oracle(torch_dev, ctx):
     """Experts of different formats in one layer (qw6.h:160-162): IQ2_XXS
     gate/up, IQ3_S downs for even and IQ2_S downs for odd experts, shared
