@@ -145,8 +145,9 @@ typedef struct {
  * [n_tok x hidden] added to the output (hidden = resid + ffn, qw6.c:2482).
  * x, out, residual and the layer's router, shared_router and norm_w are
  * 16-byte aligned (a call with another alignment fails). Tokens are processed
- * per launch of up to 4 tokens (decode, MTP verification) or by the grouped
- * bf16-MFMA kernels (prefill); see qw6_hip_set_mode. */
+ * by the per-token kernels in launches of up to 16 tokens (decode, MTP
+ * verification, small batches) or by the grouped bf16-MFMA kernels
+ * (prefill); see qw6_hip_set_mode. */
 int qw6_hip_moe_forward(qw6_hip_ctx_t *ctx, const qw6_hip_moe_layer_t *layer,
                         const float *x, const float *logits,
                         const float *residual, uint32_t n_tok, float *out,
@@ -155,12 +156,12 @@ int qw6_hip_moe_forward(qw6_hip_ctx_t *ctx, const qw6_hip_moe_layer_t *layer,
 /* qw6_hip_moe_forward without any allocation, for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving
  * loops). No counterpart in the reference. Same arguments, results and
- * per-token kernels (launches of up to 4 tokens; never the grouped kernels,
- * so mode 2 is refused); the kernels' workspace (router logits, selection
- * table, expert intermediates, MFMA operands) is a 4 MiB static device array
- * of the library instead of context allocations (every shape the per-token
- * kernels take, hidden and inter up to 2048, needs at most 3.5 MB; a layer
- * needing more would be refused with an error). Each device has one
+ * per-token kernels (launches of up to 16 tokens, 4 in mode 3; never the
+ * grouped kernels, so mode 2 is refused); the kernels' workspace (router
+ * logits, selection tables, expert intermediates, MFMA operands) is a 4 MiB
+ * static device array of the library instead of context allocations (every
+ * shape the per-token kernels take, hidden and inter up to 2048, needs at
+ * most 3.7 MB; a layer needing more would be refused with an error). Each device has one
  * such array, shared by every context and call on that device: calls that
  * overlap on one device race, so issue them on one stream (or otherwise
  * order them). */
@@ -172,14 +173,14 @@ int qw6_hip_moe_forward_noalloc(qw6_hip_ctx_t *ctx,
                                 void *stream);
 
 /* Path selection for qw6_hip_moe_forward:
- * 0 = automatic (default): the fp32 per-token kernels for launches of 1-2
- *     tokens (and 3 when each matrix kind has one format), the small-batch
- *     MFMA per-token kernels for 4 (and 3 with mixed formats), the grouped
- *     MFMA kernels from 5 tokens on (one launch per expert format present,
- *     so layers whose experts differ in format take them too);
- * 1 = always the fp32 per-token kernels;
+ * 0 = automatic (default): the fp32 per-token kernels for calls of up to 15
+ *     tokens (10 when the layer holds IQ formats), the grouped MFMA kernels
+ *     from 16 (11) tokens on (one launch per expert format present, so layers
+ *     whose experts differ in format take them too);
+ * 1 = always the fp32 per-token kernels (launches of up to 16 tokens);
  * 2 = always the grouped MFMA kernels;
- * 3 = always the small-batch MFMA per-token kernels.
+ * 3 = always the small-batch MFMA per-token kernels (launches of up to 4
+ *     tokens).
  * Returns -1 for another value. */
 int qw6_hip_set_mode(qw6_hip_ctx_t *ctx, int mode);
 

@@ -4,25 +4,26 @@
 // boundary is the cheapest grid-wide dependency on this GPU):
 //   k_moe_router : router GEMV over all experts (one wave per expert row),
 //                  optional RMSNorm of the input, shared-expert gate weight.
-//   k_moe_gate_up: the shared expert's workgroups stream at once; every routed
-//                  workgroup routes the tokens itself from the logits (softmax
-//                  top-k; distinct selected experts numbered in first-use
-//                  order, "slots"), then streams gate/up rows of its slot's
-//                  expert into LDS with direct-to-LDS 16-byte loads,
-//                  dequantizing step s while step s+1 is in flight; writes
-//                  silu(gate) * up. One workgroup publishes the slot table.
-//                  k_moe_gate_up1 is its one-token form: each workgroup takes
-//                  one row tile of every selected expert and of the shared
-//                  one, a wave per matrix pair, each routed wave selecting
-//                  its own expert from the logits.
+//   k_moe_gate_up1: each workgroup takes one row tile of every selected
+//                  expert and of the shared one, a wave per matrix pair; each
+//                  routed wave selects its own expert from the logits (softmax
+//                  top-k), then streams its gate/up rows into LDS with
+//                  direct-to-LDS 16-byte loads, dequantizing step s while step
+//                  s+1 is in flight; writes silu(gate) * up. Wave 0 of
+//                  workgroup 0 routes fully and publishes the slot table.
 //   k_moe_down   : one workgroup per tile of output rows, one wave per
 //                  selected expert (plus the shared one); per-expert row sums
 //                  meet in LDS and are combined in selection order, with the
 //                  residual -- no atomics, deterministic.
-// In the automatic mode, calls of 5 tokens or more take the grouped bf16-MFMA
-// kernels of qw6_prefill.hip (one launch per expert format present); other
-// calls run in per-token launches of up to 4 tokens, 4 (and 3 for mixed
-// formats) on the small-batch MFMA kernels k_mx_*, fewer on the fp32 ones.
+// A launch of several tokens (up to 16) runs the same kernels with one row of
+// the grid per token (token_view): each token's workgroups do exactly a
+// one-token call's work, and a token's workgroup b shares an XCD with every
+// other token's workgroup b, so experts that several tokens select, and the
+// shared expert, are read from HBM about once. In the automatic mode, calls
+// of 16 tokens or more (11 for layers holding IQ formats) take the grouped
+// bf16-MFMA kernels of qw6_prefill.hip (one launch per expert format
+// present); mode 3 runs the small-batch MFMA kernels k_mx_* in launches of up
+// to 4 tokens.
 // Routing never leaves the device (qw6's Vulkan path reads idx/w back to the
 // host per layer, qw6_vk.c:3371-3374).
 //
@@ -56,9 +57,13 @@ namespace {
 __device__ const IqTables g_tabs = make_tables();
 
 constexpr int kWG = 256;           // threads per workgroup (4 waves)
-constexpr uint32_t kMaxTok = 4;    // tokens per decode launch
-constexpr uint32_t kGroupedMinTokens = 5;    // automatic switch to the grouped MFMA path
-constexpr uint32_t kMxMinTokens = 4;         // per-token launches of 4 tokens: k_mx_*
+constexpr uint32_t kMaxTok = 4;         // tokens per launch of the small-batch MFMA kernels
+constexpr uint32_t kSplitMaxTok = 16;   // tokens per launch of the fp32 kernels (one grid row each)
+// Automatic switch to the grouped MFMA path: calls of this many tokens or
+// more (where the two paths' timings cross on one MI355X: Q4_K / Q6_K
+// layers at 16 tokens, layers holding IQ formats at 11)
+constexpr uint32_t kGroupedMinTokens = 16;
+constexpr uint32_t kGroupedMinTokensIq = 11;
 constexpr uint32_t kLdsBudget = 64 * 1024;   // dynamic LDS per workgroup
 constexpr uint32_t kMxLdsBudget = 150 * 1024;   // k_mx_*: gfx950 has 160 KB per workgroup
 constexpr int kProfEv = 6;         // events per profiled MoE call (3 kernels x start/stop)
@@ -344,26 +349,28 @@ __global__ __launch_bounds__(64) void k_route(const float* __restrict__ logits, 
 // dependency on this GPU; in-kernel grid barriers cost several times more):
 //   k_moe_router : router GEMV, one wave per expert row (+ optional RMSNorm of
 //                  the input, + the shared-expert gate weight).
-//   k_moe_gate_up: workgroups of the shared expert start streaming at once;
-//                  the routed ones route the tokens themselves from the logits
-//                  (1 KB per token), then stream gate/up rows of one selected
-//                  expert; silu(gate) * up -> mid. Workgroup 0 also publishes
-//                  the slot table (selected experts resolved to matrices).
+//   k_moe_gate_up1: every selected expert's gate/up rows of one row tile per
+//                  workgroup, each routed wave routing the token itself from
+//                  the logits (1 KB per token); silu(gate) * up -> mid.
+//                  Workgroup 0 also publishes the slot table (selected
+//                  experts resolved to matrices).
 //   k_moe_down   : one workgroup per tile of output rows, one wave per
 //                  selected expert (the shared one first, it needs no routing);
 //                  row sums meet in LDS and are combined in a fixed order with
 //                  the residual -- no atomics, deterministic.
 
-// Row steps per wave of k_moe_gate_up: 4 for two tokens, whose 17 matrix
-// pairs then take 544 workgroups, all resident at once (3 per CU).
-template <int T>
-__host__ __device__ constexpr int gu_steps() { return T == 2 ? 4 : 2; }
+constexpr int kStepsGu = 2;     // row steps per wave, gate/up
 constexpr int kStepsDn = 2;     // row steps per wave, down
 constexpr uint32_t kMaxSlots = kMaxTok * 8;
 constexpr uint32_t kSlotBytes = 2048;   // LDS slot of one step group (8 blocks <= 1680 B)
+// rows of inter floats in the mid workspace: the small-batch kernels' (max_u + 1)
+// x T, the fp32 kernels' (top_k + 1) per token
+constexpr uint32_t kMidRows = (kMaxSlots + 1) * kMaxTok > 9 * kSplitMaxTok ? (kMaxSlots + 1) * kMaxTok
+                                                                           : 9 * kSplitMaxTok;
 
-// The slot table k_moe_gate_up publishes for k_moe_down: distinct selected
-// experts in first-use order with their down matrix and per-token weights.
+// The slot table the gate/up kernels publish for the down kernels: distinct
+// selected experts in first-use order with their down matrix and per-token
+// weights (k_moe_gate_up1: one table per token, the selection itself).
 struct SlotTable {
     uint32_t n;                    // number of slots in use
     uint32_t pad[3];
@@ -382,7 +389,7 @@ struct MoeArgs {
     const float* shared_router;   // nullptr: shared weight 1
     const float* norm_w;          // RMSNorm weight or nullptr
     float norm_eps;
-    uint32_t n_sh_wg;             // shared-expert workgroups in k_moe_gate_up
+    uint32_t n_sh_wg;             // shared-expert workgroups in k_mx_gate_up
     const ExpertEnt* experts;
     PackRef pk[3];
     MatD sg, su, sd;              // shared expert; sg.p == nullptr: none
@@ -396,7 +403,7 @@ struct MoeArgs {
     uint32_t* idx_out;
     float* w_out;
     uint32_t tmask_gu, tmask_dn;
-    uint32_t gu_pb;               // k_moe_gate_up: LDS bytes of one (gate, up) step pair
+    uint32_t gu_pb;               // k_moe_gate_up1: LDS bytes of one (gate, up) step pair
     int xl_dn;                    // a format with every routed down matrix's
                                   // activation layout, or -1 (x_layout)
     // small-batch MFMA path (k_mx_*): operands of the expert input and of mid
@@ -408,6 +415,23 @@ struct MoeArgs {
     uint32_t mx_sb;               // k_mx_down: LDS bytes of one staged block
     uint32_t mx_nsl;              // k_mx_down: staged blocks per round
 };
+
+// k_moe_gate_up1 and k_moe_down<1> launched for several tokens hold token t's
+// workgroups at blockIdx.y = t (one token per row of the grid, so a token's
+// workgroup b still runs on XCD b % 8). a becomes token t's view: the
+// buffers the kernels always have offset as for a one-token call of its own
+// (slot table t, its (max_u + 1) x inter block of mid, max_u = top_k); the
+// optional ones (residual, idx_out, w_out) are offset where they are used,
+// so no branch on them delays the first loads. One-token launches have t = 0.
+__device__ __forceinline__ void token_view(MoeArgs& a) {
+    const uint32_t t = blockIdx.y;
+    a.route_logits += (size_t)t * a.n_experts;
+    a.xin += (size_t)t * a.hidden;
+    a.out += (size_t)t * a.hidden;
+    a.sw += t;
+    a.slots += t;
+    a.mid += (size_t)t * (a.max_u + 1) * a.inter;
+}
 
 // Addresses are formed from an index below n_experts whatever the routing
 // gave (a routing result is always below it; the bound keeps every weight
@@ -779,6 +803,69 @@ __global__ __launch_bounds__(64) void k_moe_router(MoeArgs a) {
     }
 }
 
+// k_moe_router for launches of more than kMaxTok tokens (a.T of them, the
+// fp32 kernels' launches): the same per token, in groups of kMaxTok, with the
+// router row and the norm weight loaded once.
+template <int NV>
+__global__ __launch_bounds__(64) void k_moe_router_n(MoeArgs a) {
+    constexpr int G = kMaxTok;
+    const uint32_t lane = threadIdx.x, e = blockIdx.x;
+    const uint32_t H = 256 * NV;   // NV float4 per lane
+    const float* wrow = e < a.n_experts ? a.router : e == a.n_experts ? a.shared_router : nullptr;
+    if (wrow && e < a.n_experts) wrow += (size_t)e * H;
+    float4 wv[NV], nw[NV];
+#pragma unroll
+    for (uint32_t i = 0; i < NV; i++) {
+        if (wrow) wv[i] = ((const float4*)wrow)[64 * i + lane];
+        if (a.norm_w) nw[i] = ((const float4*)a.norm_w)[64 * i + lane];
+    }
+    const uint32_t nq = H / 4, nwv = a.n_experts + (a.shared_router ? 1u : 0u);
+    const uint32_t per = (nq + nwv - 1) / nwv;   // float4s of the normalised input per wave
+    for (uint32_t t0 = 0; t0 < a.T; t0 += G) {
+        float4 xv[G][NV];
+#pragma unroll
+        for (int t = 0; t < G; t++)
+#pragma unroll
+            for (uint32_t i = 0; i < NV; i++)
+                xv[t][i] = t0 + t < a.T ? ((const float4*)(a.x + (size_t)(t0 + t) * H))[64 * i + lane]
+                                        : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int t = 0; t < G; t++) {
+            if (t0 + t >= a.T) break;
+            if (a.norm_w) {
+                float ss = 0.f;
+#pragma unroll
+                for (uint32_t i = 0; i < NV; i++) {
+                    ss = fmaf(xv[t][i].x, xv[t][i].x, ss); ss = fmaf(xv[t][i].y, xv[t][i].y, ss);
+                    ss = fmaf(xv[t][i].z, xv[t][i].z, ss); ss = fmaf(xv[t][i].w, xv[t][i].w, ss);
+                }
+                ss = group_sum<64>(ss);
+                const float sc = 1.0f / sqrtf(ss / (float)H + a.norm_eps);
+#pragma unroll
+                for (uint32_t i = 0; i < NV; i++) {
+                    xv[t][i].x = xv[t][i].x * sc * nw[i].x; xv[t][i].y = xv[t][i].y * sc * nw[i].y;
+                    xv[t][i].z = xv[t][i].z * sc * nw[i].z; xv[t][i].w = xv[t][i].w * sc * nw[i].w;
+                    const uint32_t q = 64 * i + lane;
+                    if (q >= e * per && q < (e + 1) * per)
+                        ((float4*)(a.xn + (size_t)(t0 + t) * H))[q] = xv[t][i];
+                }
+            }
+            if (!wrow) continue;
+            float acc = 0.f;
+#pragma unroll
+            for (uint32_t i = 0; i < NV; i++) {
+                acc = fmaf(wv[i].x, xv[t][i].x, acc); acc = fmaf(wv[i].y, xv[t][i].y, acc);
+                acc = fmaf(wv[i].z, xv[t][i].z, acc); acc = fmaf(wv[i].w, xv[t][i].w, acc);
+            }
+            acc = group_sum<64>(acc);
+            if (lane == 0) {
+                if (e < a.n_experts) a.logits[(size_t)(t0 + t) * a.n_experts + e] = acc;
+                else a.sw[t0 + t] = 1.0f / (1.0f + expf(-acc));
+            }
+        }
+    }
+}
+
 // gate/up/silu of one wave: S steps of rps rows starting at row0 of the pair
 // (G, Up) -> mid[T][inter]. slots: S LDS pair slots of pb bytes. x: the T
 // input rows (hidden values each); this lane's activations are requested
@@ -791,7 +878,7 @@ __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint
                                              float* mid, uint32_t inter, uint8_t* slots,
                                              const uint32_t* lds, uint32_t slot_off, uint32_t pb,
                                              const uint32_t* tab) {
-    constexpr int S = gu_steps<T>();
+    constexpr int S = kStepsGu;
     const int f = FF >= 0 ? FF : G.fmt;
     constexpr uint32_t U = KU, rps = 64 / KU;
     const uint32_t lane = threadIdx.x & 63;
@@ -848,131 +935,6 @@ __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint
     TRACE_MARK(2, 3);
 }
 
-// Routed + shared gate/up/SiLU. Blocks [0, n_sh_wg) stream the shared
-// expert right away; the others route the tokens (each workgroup on its
-// own), then take (slot u, row tile). 4 waves x S steps per block.
-template <int T, int FG, int KU>
-__global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
-    TRACE_SCOPE(2);
-    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-    __shared__ uint32_t s_idx[kMaxSlots], s_slot_e[kMaxSlots], s_n;
-    __shared__ float s_w[kMaxSlots], s_wt[kMaxSlots * kMaxTok];
-    __shared__ uint2 s_route[T * kRouteScr];   // routing scratch, one per routing wave
-    const uint32_t wave = threadIdx.x >> 6;
-    constexpr int S = gu_steps<T>();
-    constexpr uint32_t rps = 64 / KU;
-    constexpr uint32_t rows_wg = 4 * S * rps;
-    const uint32_t ntile = (a.inter + rows_wg - 1) / rows_wg;
-    const uint32_t toff = tab_bytes(a.tmask_gu);
-    uint8_t* wslots = smem + toff + wave * S * a.gu_pb;
-    const uint32_t slot_off = toff + wave * S * a.gu_pb;
-    const bool shared_wg = blockIdx.x < a.n_sh_wg;
-    // Waves t < T of a routed block route token t. Their logits load is the
-    // block's first memory operation (loads complete in issue order, so
-    // nothing queued ahead of it delays the routing); the other waves stage
-    // the lattice tables meanwhile.
-    const bool rwave = !shared_wg && wave < (uint32_t)T;
-    uint32_t keys[4];
-    if (rwave) route_keys(a.route_logits + (size_t)wave * a.n_experts, a.n_experts, keys);
-    TRACE_MARK_IF(rwave, 2, 4);
-    // (with T = 4 every wave routes, and the routing waves stage the tables too)
-    const uint32_t tw0 = shared_wg || T >= 4 ? 0u : (uint32_t)T;
-    stage_tables_from(smem, a.tmask_gu, tw0);
-    // Routed blocks: the staging waves wait for their table loads before the
-    // routing's barrier, which then makes the tables visible. Shared blocks
-    // issue their weight loads first and wait afterwards (wave_gate_up's bar).
-    // The activations are loaded in one place, wave_gate_up, just ahead of the
-    // weights: loads at several sites would meet in register copies that wait
-    // for every load in flight.
-    if (a.tmask_gu && !shared_wg && (!rwave || tw0 == 0)) wait_vm(0);
-    const bool bar = a.tmask_gu != 0 && shared_wg;
-    const float* xw = a.xin;
-    MatD G, Up;
-    uint32_t row0;
-    float* midp;
-    if (shared_wg) {
-        G = a.sg;
-        Up = a.su;
-        row0 = (blockIdx.x * 4 + wave) * S * rps;
-        midp = a.mid + (size_t)a.max_u * T * a.inter;
-    } else if (T > 1 && blockIdx.x != a.n_sh_wg) {
-        // several tokens, not the publishing block: only this block's slot
-        const uint32_t b = blockIdx.x - a.n_sh_wg;
-        const uint32_t u = b / ntile, tile = b % ntile;
-        uint32_t e;
-        if (!route_slot_select<T>(a, keys, u, e, s_route, s_idx)) return;
-        TRACE_MARK(2, 0);
-        G = expert_mat_wave(a, e, 0);
-        Up = expert_mat_wave(a, e, 1);
-        row0 = (tile * 4 + wave) * S * rps;
-        midp = a.mid + (size_t)u * T * a.inter;
-    } else if (T == 1 && blockIdx.x != a.n_sh_wg) {
-        // one token, not the publishing block: only the expert of this block's
-        // rank is needed (no gate weights, no slot table)
-        const uint32_t b = blockIdx.x - a.n_sh_wg;
-        const uint32_t u = b / ntile, tile = b % ntile;
-        if (wave == 0) {
-            const uint32_t e = wave_route_select(keys, a.top_k, u, s_route);
-            if ((threadIdx.x & 63u) == 0) s_n = e;
-        }
-        __syncthreads();
-        TRACE_MARK(2, 0);
-        const uint32_t e = s_n;
-        G = expert_mat_wave(a, e, 0);
-        Up = expert_mat_wave(a, e, 1);
-        row0 = (tile * 4 + wave) * S * rps;
-        midp = a.mid + (size_t)u * T * a.inter;
-    } else {
-        route_prologue<T>(a, keys, s_route, s_idx, s_w, s_slot_e, s_wt, &s_n);   // ends with a barrier
-        TRACE_MARK(2, 0);
-        const uint32_t b = blockIdx.x - a.n_sh_wg;
-        const uint32_t u = b / ntile, tile = b % ntile;
-        const uint32_t nslot = s_n;
-        if (b == 0) {   // publish the routing and the slot table for k_moe_down
-            const uint32_t tid = threadIdx.x;
-            if (tid < T * a.top_k) {
-                if (a.idx_out) a.idx_out[tid] = s_idx[tid];
-                if (a.w_out) a.w_out[tid] = s_w[tid];
-            }
-            if (tid < a.max_u) {
-                SlotTable* st = a.slots;
-                // entries past the count name slot 0's matrix (weight 0 for every
-                // token): each k_moe_down wave stages its first matrix before it
-                // knows the count, so every entry a wave may take must be a real
-                // matrix (nslot >= 1: top_k >= 1)
-                const MatD D = expert_mat(a, s_slot_e[tid < nslot ? tid : 0u], 2);
-                st->p[tid] = D.p; st->fmt[tid] = D.fmt; st->rb[tid] = D.rb;
-#pragma unroll
-                for (uint32_t t = 0; t < kMaxTok; t++) st->wt[tid][t] = s_wt[tid * kMaxTok + t];
-            }
-            if (tid == 0) a.slots->n = nslot;
-        }
-        if (u >= nslot) return;
-        const uint32_t e = s_slot_e[u];
-        G = expert_mat_wave(a, e, 0);
-        Up = expert_mat_wave(a, e, 1);
-        row0 = (tile * 4 + wave) * S * rps;
-        midp = a.mid + (size_t)u * T * a.inter;
-    }
-    if (row0 >= a.inter) {   // (not for the shapes the host accepts)
-        if (bar) {   // still take part in the shared block's barrier
-            wait_vm(0);
-            lds_barrier();
-        }
-        return;
-    }
-    const uint32_t* lds = (const uint32_t*)smem;
-    if (FG >= 0) {
-        wave_gate_up<T, FG, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds);
-        return;
-    }
-    // mixed formats: one switch per wave, each body specialised
-    by_fmt<FG>(G.fmt, [&](auto fc) {
-        wave_gate_up<T, decltype(fc)::value, KU>(G, Up, row0, xw, a.hidden, bar, midp, a.inter, wslots, lds,
-                                                 slot_off, a.gu_pb, lds);
-    });
-}
-
 // One token, every gate/up pair of the layer in each workgroup: workgroup b
 // takes rows [b R, (b + 1) R) (R = 2 rps, two row steps) of every selected
 // expert and of the shared one. Wave w < top_k works on the expert of rank w
@@ -981,17 +943,18 @@ __global__ __launch_bounds__(kWG) void k_moe_gate_up(MoeArgs a) {
 // selection and the slot table. Wave top_k (when present) streams the shared
 // expert from the start. Every workgroup moves the same bytes and there is
 // one per row tile: at hidden 2048 / inter 512, 256 workgroups of 9 waves,
-// one per CU (the 4-wave layout of k_moe_gate_up puts 576 workgroups on the
-// 256 CUs, three on a quarter of them).
-template <int FG, int KU>
+// one per CU (a 4-wave workgroup per (expert, row tile) put 576 workgroups on
+// the 256 CUs, three on a quarter of them).
+template <int FG, int KU, bool MT = false>
 __global__ __launch_bounds__(64 * 9) void k_moe_gate_up1(MoeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ uint32_t s_idx[8];
     __shared__ float s_w[8];
     __shared__ uint2 s_route[8 * kRouteScr];   // one per routed wave
-    constexpr int S = gu_steps<1>();
+    constexpr int S = kStepsGu;
     constexpr uint32_t rps = 64 / KU;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
+    if constexpr (MT) token_view(a);
     const bool shared_w = wave >= a.top_k;
     const uint32_t toff = tab_bytes(a.tmask_gu);
     const uint32_t slot_off = toff + wave * S * a.gu_pb;
@@ -1015,8 +978,9 @@ __global__ __launch_bounds__(64 * 9) void k_moe_gate_up1(MoeArgs a) {
             wave_route_keys(keys, a.top_k, s_route, s_idx, s_w);
             __builtin_amdgcn_wave_barrier();
             if (lane < a.top_k) {
-                if (a.idx_out) a.idx_out[lane] = s_idx[lane];
-                if (a.w_out) a.w_out[lane] = s_w[lane];
+                const uint32_t o = (MT ? blockIdx.y * a.top_k : 0u) + lane;   // token_view's token
+                if (a.idx_out) a.idx_out[o] = s_idx[lane];
+                if (a.w_out) a.w_out[o] = s_w[lane];
                 SlotTable* st = a.slots;
                 const MatD D = expert_mat(a, s_idx[lane], 2);
                 st->p[lane] = D.p; st->fmt[lane] = D.fmt; st->rb[lane] = D.rb;
@@ -1089,7 +1053,7 @@ __device__ __forceinline__ void down_rows(const uint32_t* lds, uint32_t boff0, i
     }
 }
 
-template <int T, int FD, int KU>
+template <int T, int FD, int KU, bool MT = false>
 __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
     TRACE_SCOPE(3);
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -1097,6 +1061,8 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
     constexpr int S = kStepsDn;
     constexpr uint32_t U = KU, rps = 64 / KU;
     constexpr uint32_t R = S * rps;
+    static_assert(!MT || T == 1, "launches over several tokens run the one-token kernel");
+    if constexpr (MT) token_view(a);
     const uint32_t r0 = blockIdx.x * R;
     const uint32_t nw = blockDim.x >> 6;
     // wave index as a wave-uniform value: the slot-table reads below then
@@ -1130,7 +1096,7 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
     float resid = 0.f, shw = 1.0f;
     if (threadIdx.x < R * T) {
         const uint32_t rl = threadIdx.x / T, t = threadIdx.x % T;
-        if (a.residual) resid = a.residual[(size_t)t * a.hidden + r0 + rl];
+        if (a.residual) resid = a.residual[((size_t)t + (MT ? blockIdx.y : 0u)) * a.hidden + r0 + rl];
         if (has_sh && a.shared_router) shw = a.sw[t];
     }
     const uint32_t ntot = nslot + has_sh;
@@ -1196,7 +1162,7 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
 }
 
 // ---- small-batch MFMA kernels ------------------------------------------------------
-// k_mx_gate_up and k_mx_down compute the same layer as k_moe_gate_up and
+// k_mx_gate_up and k_mx_down compute the same layer as k_moe_gate_up1 and
 // k_moe_down for T <= 4 tokens, with bf16 MFMA 16x16x32 on the operands above:
 // the weights' per-lane decode work (qw6_tile.h) no longer grows with T, and
 // the registers no longer hold every token's activations.
@@ -1287,7 +1253,7 @@ __device__ __forceinline__ void mx_block_fmt(int f, const uint32_t* s, const uin
 
 // Routing of one routed block of a gate/up kernel (tiles per slot: ntile):
 // its slot u and tile, the slot's expert e, and for the first routed block the
-// published selection and slot table (as k_moe_gate_up). False: unused slot.
+// published selection and slot table. False: unused slot.
 template <int T>
 __device__ __forceinline__ bool mx_route_block(const MoeArgs& a, uint32_t (&keys)[4], uint32_t ntile,
                                                uint32_t& u, uint32_t& tile, uint32_t& e) {
@@ -2287,11 +2253,11 @@ size_t carve_decode_ws(uint8_t* base, uint32_t hidden, uint32_t inter, DecodeWs*
         return p;
     };
     DecodeWs d;
-    d.logits = (float*)take((size_t)kMaxTok * 256 * 4);
-    d.sw = (float*)take(kMaxTok * 4);
-    d.xn = (float*)take((size_t)kMaxTok * hidden * 4);
-    d.slots = (SlotTable*)take(sizeof(SlotTable));
-    d.mid = (float*)take((size_t)(kMaxSlots + 1) * kMaxTok * inter * 4);
+    d.logits = (float*)take((size_t)kSplitMaxTok * 256 * 4);
+    d.sw = (float*)take(kSplitMaxTok * 4);
+    d.xn = (float*)take((size_t)kSplitMaxTok * hidden * 4);
+    d.slots = (SlotTable*)take(kSplitMaxTok * sizeof(SlotTable));   // one per token (fp32 kernels)
+    d.mid = (float*)take((size_t)kMidRows * inter * 4);
     d.mxa = (uint4*)take((size_t)(hidden / 32) * 64 * 16);
     d.mxs = (uint16_t*)take((size_t)(hidden / 256) * 192 * 2);
     d.mma = (uint4*)take((size_t)(kMaxSlots + 1) * (inter / 32) * 64 * 16);
@@ -2595,15 +2561,15 @@ int ensure_ws(qw6_hip_ctx_t* c, uint32_t hidden, uint32_t inter) {
     hidden = hidden > c->ws_hidden ? hidden : c->ws_hidden;
     inter = inter > c->ws_inter ? inter : c->ws_inter;
     void* p;
-    if (alloc_owned(c, (size_t)kMaxTok * 256 * 4, &p)) return -1;
+    if (alloc_owned(c, (size_t)kSplitMaxTok * 256 * 4, &p)) return -1;
     c->logits = (float*)p;
-    if (alloc_owned(c, kMaxTok * 4, &p)) return -1;
+    if (alloc_owned(c, kSplitMaxTok * 4, &p)) return -1;
     c->sw = (float*)p;
-    if (alloc_owned(c, (size_t)kMaxTok * hidden * 4, &p)) return -1;
+    if (alloc_owned(c, (size_t)kSplitMaxTok * hidden * 4, &p)) return -1;
     c->xn = (float*)p;
-    if (alloc_owned(c, sizeof(SlotTable), &p)) return -1;
+    if (alloc_owned(c, kSplitMaxTok * sizeof(SlotTable), &p)) return -1;
     c->slots = (SlotTable*)p;
-    if (alloc_owned(c, (size_t)(kMaxSlots + 1) * kMaxTok * inter * 4, &p)) return -1;
+    if (alloc_owned(c, (size_t)kMidRows * inter * 4, &p)) return -1;
     c->mid = (float*)p;
     c->ws_hidden = hidden;
     c->ws_inter = inter;
@@ -2682,13 +2648,13 @@ int ensure_prefill_ws(qw6_hip_ctx_t* c, uint32_t hidden, uint32_t inter, uint32_
 // events, no extra queue packets) when ev is given.
 template <typename... Args>
 int launch_k(void (*kern)(Args...), uint32_t grid, uint32_t block, size_t lds, hipStream_t st,
-             hipEvent_t* ev, const MoeArgs& a) {
+             hipEvent_t* ev, const MoeArgs& a, uint32_t gy = 1) {
     if (ev) {
         void* args[] = {(void*)&a};
-        CK(hipExtLaunchKernel((const void*)kern, dim3(grid), dim3(block), args, lds, st, ev[0],
+        CK(hipExtLaunchKernel((const void*)kern, dim3(grid, gy), dim3(block), args, lds, st, ev[0],
                               ev[1], 0));
     } else {
-        kern<<<grid, block, lds, st>>>(a);
+        kern<<<dim3(grid, gy), block, lds, st>>>(a);
         CK(hipGetLastError());
     }
     return 0;
@@ -2697,7 +2663,7 @@ int launch_k(void (*kern)(Args...), uint32_t grid, uint32_t block, size_t lds, h
 struct MoeLaunch {
     bool router;             // k_moe_router runs
     bool mx;                 // the small-batch MFMA kernels (k_mx_*)
-    bool gu1;                // one token: k_moe_gate_up1 (every matrix pair per workgroup)
+    uint32_t gy;             // grid rows of k_moe_gate_up1 / k_moe_down<1>: one per token
     uint32_t grid_r;
     uint32_t grid_b1, nw_b1;
     size_t lds_b1;
@@ -2714,35 +2680,25 @@ struct MoeLaunch {
 constexpr uint32_t kSetGateUpIq2m = (1u << F_Q4K) | (1u << F_IQ2XXS);
 constexpr uint32_t kSetDownIq2m = (1u << F_Q6K) | (1u << F_IQ2S) | (1u << F_IQ3S);
 
-// Run fn(IC<T>, IC<F>, IC<KU>) for the expert-kernel instantiation of T
-// tokens, format f (mask: the formats present) and KU = K/32 units per row:
-// format- and size-specialised kernels for 1-2 tokens at the model's row
-// length KU_fast (one format, or one of the sets above), the generic
-// (six-format switch) kernel otherwise.
+// Run fn(IC<F>, IC<KU>) for the expert-kernel instantiation of format f
+// (mask: the formats present) and KU = K/32 units per row: format- and
+// size-specialised kernels at the model's row length KU_fast (one format, or
+// the set above), the generic (six-format switch) kernel otherwise.
 template <int KU_fast, uint32_t kSet, typename Fn>
-void launch_expert_kernel(int f, uint32_t mask, uint32_t T, uint32_t KU, Fn fn) {
-    if (T <= 2 && f >= 0 && KU == (uint32_t)KU_fast) {
-        launch_by_fmt(f, T, [&](auto tc, auto fc) { fn(tc, fc, IC<KU_fast>{}); });
+void launch_expert_kernel(int f, uint32_t mask, uint32_t KU, Fn fn) {
+    if (f >= 0 && KU == (uint32_t)KU_fast) {
+        launch_by_fmt(f, 1, [&](auto, auto fc) { fn(fc, IC<KU_fast>{}); });
         return;
     }
-    if (T <= 2 && f < 0 && KU == (uint32_t)KU_fast && mask == kSet) {
-        if (T == 1) fn(IC<1>{}, IC<fmt_set(kSet)>{}, IC<KU_fast>{});
-        else fn(IC<2>{}, IC<fmt_set(kSet)>{}, IC<KU_fast>{});
+    if (f < 0 && KU == (uint32_t)KU_fast && mask == kSet) {
+        fn(IC<fmt_set(kSet)>{}, IC<KU_fast>{});
         return;
     }
-    auto by_ku = [&](auto tc) {
-        switch (KU) {
-        case 8: fn(tc, IC<-1>{}, IC<8>{}); break;
-        case 16: fn(tc, IC<-1>{}, IC<16>{}); break;
-        case 32: fn(tc, IC<-1>{}, IC<32>{}); break;
-        default: fn(tc, IC<-1>{}, IC<64>{}); break;
-        }
-    };
-    switch (T) {
-    case 1: by_ku(IC<1>{}); break;
-    case 2: by_ku(IC<2>{}); break;
-    case 3: by_ku(IC<3>{}); break;
-    default: by_ku(IC<4>{}); break;
+    switch (KU) {
+    case 8: fn(IC<-1>{}, IC<8>{}); break;
+    case 16: fn(IC<-1>{}, IC<16>{}); break;
+    case 32: fn(IC<-1>{}, IC<32>{}); break;
+    default: fn(IC<-1>{}, IC<64>{}); break;
     }
 }
 
@@ -2758,11 +2714,20 @@ int launch_moe(const MoeArgs& a, const MoeLaunch& m, hipStream_t st, hipEvent_t*
             default: rc = launch_k(k_moe_router<T, 8>, m.grid_r, 64, 0, st, ev, a); break;
             }
         };
+        auto by_nv_loop = [&]() {   // more than kMaxTok tokens: groups of kMaxTok
+            switch (a.hidden / 256) {
+            case 1: rc = launch_k(k_moe_router_n<1>, m.grid_r, 64, 0, st, ev, a); break;
+            case 2: rc = launch_k(k_moe_router_n<2>, m.grid_r, 64, 0, st, ev, a); break;
+            case 4: rc = launch_k(k_moe_router_n<4>, m.grid_r, 64, 0, st, ev, a); break;
+            default: rc = launch_k(k_moe_router_n<8>, m.grid_r, 64, 0, st, ev, a); break;
+            }
+        };
         switch (a.T) {
         case 1: by_nv(IC<1>{}); break;
         case 2: by_nv(IC<2>{}); break;
         case 3: by_nv(IC<3>{}); break;
-        default: by_nv(IC<4>{}); break;
+        case 4: by_nv(IC<4>{}); break;
+        default: by_nv_loop(); break;
         }
         if (rc) return rc;
     } else if (ev) {
@@ -2786,22 +2751,22 @@ int launch_moe(const MoeArgs& a, const MoeLaunch& m, hipStream_t st, hipEvent_t*
         }
         return rc;
     }
-    if (m.gu1) {
-        launch_expert_kernel<64, kSetGateUpIq2m>(m.fg, m.mg, 1, a.hidden / 32, [&](auto, auto fc, auto kc) {
-            rc = launch_k(k_moe_gate_up1<decltype(fc)::value, decltype(kc)::value>, m.grid_b1,
-                          64 * m.nw_b1, m.lds_b1, st, ev ? ev + 2 : nullptr, a);
+    // the fp32 kernels; the multi-token instantiations (MT) read their
+    // token's buffers by token_view
+    auto fp32 = [&](auto mt) {
+        constexpr bool MT = decltype(mt)::value;
+        launch_expert_kernel<64, kSetGateUpIq2m>(m.fg, m.mg, a.hidden / 32, [&](auto fc, auto kc) {
+            rc = launch_k(k_moe_gate_up1<decltype(fc)::value, decltype(kc)::value, MT>, m.grid_b1,
+                          64 * m.nw_b1, m.lds_b1, st, ev ? ev + 2 : nullptr, a, m.gy);
         });
-    } else {
-        launch_expert_kernel<64, kSetGateUpIq2m>(m.fg, m.mg, a.T, a.hidden / 32, [&](auto tc, auto fc, auto kc) {
-            rc = launch_k(k_moe_gate_up<decltype(tc)::value, decltype(fc)::value, decltype(kc)::value>,
-                          m.grid_b, kWG, m.lds_b, st, ev ? ev + 2 : nullptr, a);
+        if (rc) return;
+        launch_expert_kernel<16, kSetDownIq2m>(m.fd, m.md, a.inter / 32, [&](auto fc, auto kc) {
+            rc = launch_k(k_moe_down<1, decltype(fc)::value, decltype(kc)::value, MT>, m.grid_c,
+                          64 * m.nw_c, m.lds_c, st, ev ? ev + 4 : nullptr, a, m.gy);
         });
-    }
-    if (rc) return rc;
-    launch_expert_kernel<16, kSetDownIq2m>(m.fd, m.md, a.T, a.inter / 32, [&](auto tc, auto fc, auto kc) {
-        rc = launch_k(k_moe_down<decltype(tc)::value, decltype(fc)::value, decltype(kc)::value>,
-                      m.grid_c, 64 * m.nw_c, m.lds_c, st, ev ? ev + 4 : nullptr, a);
-    });
+    };
+    if (m.gy > 1) fp32(std::true_type{});
+    else fp32(std::false_type{});
     return rc;
 }
 
@@ -2861,7 +2826,8 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
         return fail("the grouped MFMA path needs context workspace: not available without allocation");
     if (c->mode == 2 && !grouped_ok)
         return fail("grouped MFMA path: an expert matrix has a format the grouped kernels do not decode");
-    if (!noalloc && grouped_ok && (c->mode == 2 || (c->mode == 0 && n_tok >= kGroupedMinTokens))) {
+    const uint32_t min_grouped = (mgu | mdn) ? kGroupedMinTokensIq : kGroupedMinTokens;
+    if (!noalloc && grouped_ok && (c->mode == 2 || (c->mode == 0 && n_tok >= min_grouped))) {
         if (ensure_prefill_ws(c, L->hidden, L->inter, E->n, L->top_k)) return -1;
         PrefillLayer P;
         memset(&P, 0, sizeof P);
@@ -2878,7 +2844,7 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
     }
     // per-token path: the fp32 kernels (k_moe_*) or the small-batch MFMA
     // kernels (k_mx_*: mode 3, or automatic for more than one token per launch)
-    const bool mx_any = c->mode == 3 || c->mode == 0;
+    const bool mx_any = c->mode == 3;
     DecodeWs ws;
     if (noalloc) {
         const size_t need = carve_decode_ws(nullptr, L->hidden, L->inter, nullptr);
@@ -2932,7 +2898,7 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
     m.mg = (E->fmask_gu & ((1u << F_NFMT) - 1u)) | (has_sh ? 1u << sg.fmt : 0u);
     m.md = (E->fmask_dn & ((1u << F_NFMT) - 1u)) | (has_sh ? 1u << sd.fmt : 0u);
     const uint32_t rpsg = 64 / (L->hidden / 32), rpsd = 64 / (L->inter / 32);
-    // k_moe_gate_up: LDS pair slot of the widest (gate, up) step pair in use
+    // k_moe_gate_up1: LDS pair slot of the widest (gate, up) step pair in use
     uint32_t pl = has_sh ? pair_loads(sg.fmt) : 1u;
     for (int f = 0; f < F_NFMT; f++)
         if (E->fmt_gu < 0 || E->fmt_gu == f) pl = std::max(pl, pair_loads(f));
@@ -2944,21 +2910,24 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
     m.router = (!logits && L->router) || L->shared_router != nullptr || L->norm_w != nullptr;
     m.grid_r = E->n + (L->shared_router ? 1u : 0u);
 
+    // The fp32 kernels (k_moe_gate_up1, k_moe_down<1>) take launches of up to
+    // kSplitMaxTok tokens, one row of their grids per token (token_view);
+    // mode 3 the small-batch MFMA kernels, launches of up to kMaxTok tokens.
+    const bool mx = c->mode == 3;
+    const uint32_t chunk = mx ? kMaxTok : kSplitMaxTok;
+    // k_moe_gate_up1: one workgroup per kStepsGu row steps of every matrix pair
+    m.nw_b1 = L->top_k + (has_sh ? 1u : 0u);
+    m.grid_b1 = (L->inter + kStepsGu * rpsg - 1) / (kStepsGu * rpsg);
+    m.lds_b1 = (size_t)tab_bytes(mgu) + (size_t)m.nw_b1 * kStepsGu * a.gu_pb;
+    if (!mx && m.lds_b1 > kMxLdsBudget) return fail("gate/up tile exceeds the LDS budget");
     const uint32_t grid_c_valu = m.grid_c;
-    for (uint32_t t0 = 0; t0 < n_tok; t0 += kMaxTok) {
-        const uint32_t T = n_tok - t0 < kMaxTok ? n_tok - t0 : kMaxTok;
+    for (uint32_t t0 = 0; t0 < n_tok; t0 += chunk) {
+        const uint32_t T = n_tok - t0 < chunk ? n_tok - t0 : chunk;
         a.T = T;
-        a.max_u = T * L->top_k;
-        // automatic: the MFMA kernels for 4 tokens, and for 3 when the layer's
-        // formats are mixed (the fp32 kernels then dispatch per matrix)
-        m.mx = c->mode == 3 ||
-               (c->mode == 0 && (T >= kMxMinTokens || (T == kMxMinTokens - 1 && (m.fg < 0 || m.fd < 0))));
-        a.xa = m.mx ? ws.mxa : nullptr;   // k_moe_router writes the operands
-        const uint32_t S = T == 2 ? 4u : 2u;                   // gu_steps<T>()
-        const uint32_t rows_wg = 4 * S * rpsg;                 // gate/up rows per workgroup
-        const uint32_t ntile_b = (L->inter + rows_wg - 1) / rows_wg;
-        a.n_sh_wg = has_sh ? ntile_b : 0;
-        m.lds_b = (size_t)tab_bytes(mgu) + 4 * S * a.gu_pb;
+        m.mx = mx;
+        a.max_u = mx ? T * L->top_k : L->top_k;   // the fp32 kernels: per token
+        a.xa = mx ? ws.mxa : nullptr;   // k_moe_router writes the operands
+        m.gy = mx ? 1u : T;
         m.grid_c = grid_c_valu;
         a.x = x + (size_t)t0 * L->hidden;
         a.xin = L->norm_w ? ws.xn : a.x;
@@ -2968,24 +2937,14 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
         a.out = out + (size_t)t0 * L->hidden;
         a.idx_out = idx ? idx + (size_t)t0 * L->top_k : nullptr;
         a.w_out = w ? w + (size_t)t0 * L->top_k : nullptr;
-        m.grid_b = a.n_sh_wg + a.max_u * ntile_b;
-        // one token: every matrix pair in each workgroup, one workgroup per
-        // two row steps (k_moe_gate_up1)
-        m.gu1 = T == 1;
-        m.nw_b1 = L->top_k + (has_sh ? 1u : 0u);
-        m.grid_b1 = (L->inter + S * rpsg - 1) / (S * rpsg);
-        m.lds_b1 = (size_t)tab_bytes(mgu) + (size_t)m.nw_b1 * S * a.gu_pb;
-        if (m.gu1 && m.lds_b1 > kMxLdsBudget) m.gu1 = false;
         const uint32_t ntot = a.max_u + (has_sh ? 1u : 0u);
-        const uint32_t nw_max = T == 1 ? down_waves<1>() : T == 2 ? down_waves<2>() : down_waves<3>();
-        m.nw_c = ntot < nw_max ? ntot : nw_max;
+        m.nw_c = ntot < down_waves<1>() ? ntot : down_waves<1>();
         m.lds_c = (size_t)tab_bytes(mdn) + (size_t)m.nw_c * kStepsDn * kSlotBytes +
-                  (size_t)ntot * R_c * T * 4 + 16;
-        if (!m.mx && m.lds_c > kLdsBudget) return fail("down tile exceeds the LDS budget");
-        if (!m.mx && m.lds_b > kMxLdsBudget) return fail("gate/up tile exceeds the LDS budget");
+                  (size_t)ntot * R_c * 4 + 16;
+        if (!mx && m.lds_c > kLdsBudget) return fail("down tile exceeds the LDS budget");
         m.router = (!logits && L->router) || L->shared_router != nullptr || L->norm_w != nullptr;
         m.grid_r = E->n + (L->shared_router ? 1u : 0u);
-        if (m.mx) {
+        if (mx) {
             // gate/up: blocks of 16 rows, one wave per 256-column block (up to 8)
             const uint32_t nbw = (nkb_gu + mx_nw_b - 1) / mx_nw_b;
             a.n_sh_wg = has_sh ? L->inter / 16 : 0u;

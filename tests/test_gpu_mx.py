@@ -1,6 +1,6 @@
-"""Small-batch MFMA kernels (k_mx_gate_up / k_mx_down; qw6_hip_set_mode 3, and
-the automatic choice for 4 tokens per launch, 3 with mixed formats) against
-the oracle, through the C ABI.
+"""Small-batch MFMA kernels (k_mx_gate_up / k_mx_down; qw6_hip_set_mode 3)
+against the oracle, through the C ABI, and the automatic choice at the same
+token counts (the fp32 kernels, one grid row per token).
 
 Same bars as the fp32 per-token kernels: expert indices bit-exact, outputs
 rel-L2 <= 1e-5 (the activations enter as three bf16 parts and the weights as
@@ -258,14 +258,12 @@ def test_mx_graph_replay_matches_eager(torch_dev, ctx):
 
 
 def test_auto_mode_mixed_chunks_vs_oracle(torch_dev, ctx):
-    """The per-token chunk loop on a mixed-format layer (IQ2_XXS gate/up,
-    IQ3_S / IQ2_S down): the call without allocation (which never takes the
-    grouped kernels) runs launches of up to 4 tokens -- 5 tokens = 4 on the
-    MFMA kernels then 1 on the fp32 kernels, 6 = 4 (MFMA) + 2 (fp32), 7 = 4
-    (MFMA) + 3 (MFMA, as for mixed formats); the automatic path of the same
-    calls takes the grouped kernels (one launch per down format, held to the
-    fp32 bar 1e-5 as every grouped call below 64 tokens). A uniform Q4_K layer
-    under the per-token mode (1) takes 4 + 1 on the fp32 kernels."""
+    """Calls of 5-7 tokens on a mixed-format layer (IQ2_XXS gate/up, IQ3_S /
+    IQ2_S down), through the call without allocation (which never takes the
+    grouped kernels) and the automatic path: both run one launch of the fp32
+    kernels, one grid row per token (the grouped kernels start at 11 tokens
+    for layers holding IQ formats). A uniform Q4_K layer under the per-token
+    mode (1) takes 5 tokens in one launch too."""
     torch = torch_dev
     from qw6_amd.workload import SynthLayer
     L = SynthLayer(ctx, 67, 0, "iq2m")
@@ -298,8 +296,8 @@ def test_auto_mode_mixed_chunks_vs_oracle(torch_dev, ctx):
 def test_auto_mode_mixed_formats_vs_oracle(torch_dev, ctx):
     """Automatic path selection on a mixed-format layer (IQ2_XXS routed with a
     Q4_K shared gate/up, IQ3_S / IQ2_S routed down with a Q6_K shared down):
-    2 tokens take the fp32 kernels' per-matrix format dispatch, 3 and 4 the
-    MFMA kernels."""
+    2-4 tokens take the fp32 kernels' per-matrix format dispatch, one grid row
+    per token."""
     from qw6_amd.workload import SynthLayer
     L = SynthLayer(ctx, 68, 0, "iq2m")
     try:

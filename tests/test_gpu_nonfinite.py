@@ -13,10 +13,12 @@ so qw6 picks index 0 in every round; an infinite column makes the logits
 order, so the selection is exact on every path.
 
 Paths: the fp32 per-token kernels (mode 1) and the small-batch MFMA kernels
-(mode 3) at T = 1-4, the automatic choice (mode 0) at T = 1-4, the grouped
-MFMA kernels (mode 2) at T = 5 and at 64 (the poisoned tokens among 59 finite
-ones); and the fused RMSNorm with the residual added (the decode-step glue)
-at T = 1 and 5. Bars: indices bit-exact; gate weights NaN where the oracle's
+(mode 3) at T = 1-4, the automatic choice (mode 0) at T = 1-4, the fp32
+kernels' launches of more tokens (6 and 16 in one launch, the router in
+groups of four; 18 = 16 + 2), the grouped MFMA kernels (mode 2) at T = 5 and
+at 64 (the poisoned tokens among 59 finite ones); and the fused RMSNorm with
+the residual added (the decode-step glue) at T = 1, 6 and 16 on the fp32
+kernels and 5 on the grouped ones. Bars: indices bit-exact; gate weights NaN where the oracle's
 are, within 2e-5 elsewhere; outputs finite exactly where the oracle's are,
 the finite tokens within rel-L2 1e-5 (2e-3 for the grouped call of 64).
 """
@@ -166,6 +168,15 @@ def test_nonfinite_tokens_per_token_paths(torch_dev, ctx, case, mode, T):
         check(c, toks, out, idx, w, 1e-5, False, "mode %d T=%d" % (mode, T))
 
 
+@pytest.mark.parametrize("T", [6, 16, 18])
+def test_nonfinite_tokens_fp32_launches(torch_dev, ctx, case, T):
+    c = case
+    toks = list(range(T))
+    say("non-finite fp32 kernels T=%d" % T)
+    out, idx, w = run(torch_dev, ctx, c, toks, 1, False)
+    check(c, toks, out, idx, w, 1e-5, False, "mode 1 T=%d" % T)
+
+
 @pytest.mark.parametrize("T", [5, 64])
 def test_nonfinite_tokens_grouped(torch_dev, ctx, case, T):
     c = case
@@ -176,10 +187,11 @@ def test_nonfinite_tokens_grouped(torch_dev, ctx, case, T):
     check(c, toks, out, idx, w, 1e-5 if T < 64 else 2e-3, False, "grouped T=%d" % T)
 
 
-@pytest.mark.parametrize("T,mode", [(1, 1), (5, 2)], ids=["decode", "grouped"])
+@pytest.mark.parametrize("T,mode", [(1, 1), (6, 1), (16, 1), (5, 2)],
+                         ids=["decode", "fp32-6", "fp32-16", "grouped"])
 def test_nonfinite_tokens_with_norm_and_residual(torch_dev, ctx, case, T, mode):
     c = case
-    n = 6
+    n = 6 if T <= 6 else T
     for t0 in range(0, n, T):
         toks = [(t0 + j) % n for j in range(T)]
         say("non-finite glue mode %d T=%d tokens %s" % (mode, T, [c.names[t] for t in toks]))

@@ -15,8 +15,10 @@ put each of those cases in one token of a 256-expert layer:
   - an all -inf token, and three finite logits among -inf.
 
 Paths: the fp32 per-token kernels (mode 1) and the small-batch MFMA kernels
-(mode 3) at T = 1-4, the automatic choice at T = 1-4, and the grouped MFMA
-kernels (mode 2) at T = 5 and 64, on a Q4_K / Q6_K layer and on the IQ2_M
+(mode 3) at T = 1-4, the automatic choice at T = 1-4, the fp32 kernels'
+launches of more tokens (6 and 16 in one launch, 18 = 16 + 2; the automatic
+choice at 10), and the grouped MFMA kernels (mode 2) at T = 5 and 64, on a
+Q4_K / Q6_K layer and on the IQ2_M
 mix. Bars: indices bit-exact for every token; gate weights NaN where the
 oracle's are and within 2e-5 elsewhere; outputs NaN exactly where the
 oracle's are, and the finite ones within rel-L2 1e-5 (per-token kernels and
@@ -132,6 +134,16 @@ def test_route_rules_per_token_paths(torch_dev, ctx, case, mode, T):
         say("route mode %d T=%d tokens %s" % (mode, T, [c.names[t] for t in toks]))
         out, idx, w = run(torch_dev, ctx, c.L, c.xs[toks], c.lg[toks], mode)
         check(c, toks, out, idx, w, TOL[mode], "mode %d T=%d" % (mode, T))
+
+
+@pytest.mark.parametrize("T,mode", [(6, 1), (16, 1), (18, 1), (10, 0)])
+def test_route_rules_fp32_launches(torch_dev, ctx, case, T, mode):
+    c = case
+    nv = len(cases.route_vectors())
+    toks = [nv - T // 2 + j for j in range(T)]   # the last route vectors, then Zipf tokens
+    say("route mode %d T=%d" % (mode, T))
+    out, idx, w = run(torch_dev, ctx, c.L, c.xs[toks], c.lg[toks], mode)
+    check(c, toks, out, idx, w, 1e-5, "mode %d T=%d" % (mode, T))
 
 
 @pytest.mark.parametrize("T", [5, 64])

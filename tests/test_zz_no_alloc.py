@@ -25,7 +25,7 @@ def test_noalloc_matches_moe_forward():
     import torch
     from qw6_amd.workload import SynthLayer
     assert torch.cuda.is_available(), "no GPU visible"
-    ctx = Q.Context(0, max_tokens=8)
+    ctx = Q.Context(0, max_tokens=18)
     big = SynthLayer(ctx, 11, 0, "q4k")
     small = SynthLayer(ctx, 31, 0, "iq2m", hidden=1024, inter=256, n_experts=64, top_k=4)
     try:
@@ -34,11 +34,13 @@ def test_noalloc_matches_moe_forward():
         dbig.norm_w, dbig.norm_eps = nw.data_ptr(), 1e-6
         # (layer, hidden, tokens, residual, mode): both entry points run the
         # same per-token kernels in the same mode (the regular one would take
-        # the grouped kernels for 5 tokens in mode 0). 8 tokens in mode 3 and
-        # 4 in mode 0 run the small-batch MFMA kernels (k_mx_*) on the static
-        # array's operand regions, in two 4-token launches and in one.
-        calls = [(dbig, 2048, 3, True, 0), (dbig, 2048, 8, True, 3), (dbig, 2048, 4, True, 0),
-                 (dbig, 2048, 5, True, 1), (small.desc, 1024, 1, False, 0)]
+        # the grouped kernels for 16 tokens or more in mode 0). 8 tokens and 4
+        # in mode 3 run the small-batch MFMA kernels (k_mx_*) on the static
+        # array's operand regions, in two 4-token launches and in one; 18 in
+        # mode 1 the fp32 kernels in launches of 16 and 2 tokens.
+        calls = [(dbig, 2048, 3, True, 0), (dbig, 2048, 8, True, 3), (dbig, 2048, 4, True, 3),
+                 (dbig, 2048, 18, True, 1), (dbig, 2048, 6, True, 0),
+                 (small.desc, 1024, 1, False, 0)]
         # warm both paths once (first-use allocations of the regular path
         # and of the runtime happen here, not in the measured calls)
         for d, H, T, res, mode in calls:
