@@ -35,7 +35,7 @@ pair) and single-token steps of the 40-layer stack.
                 grouped bf16-MFMA kernels, Q4_K / Q6_K experts: us/layer,
                 TFLOP/s, MFMA fraction, HBM GB/s;
   mtp_T2        two tokens (MTP draft verification) with the router GEMV, and
-                small batches (3, 4, 8 tokens) through the automatic path;
+                small batches (3, 4, 8, 16 tokens) through the automatic path;
   prefill_T512_iq2xxs_iq3s  the grouped kernels on an IQ layer (IQ2_XXS
                 gate/up, IQ3_S down, Q4_K / Q6_K shared expert);
   output_head   the greedy next-token head: final RMSNorm, Q6_K [248320 x
@@ -59,6 +59,9 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 HIDDEN, INTER, N_EXPERTS, TOP_K = 2048, 512, 256, 8
+# calls of this many tokens or more take the grouped kernels on a Q4_K / Q6_K
+# layer in the automatic mode (qw6_hip_set_mode)
+GROUPED_MIN_TOKENS = 16
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "moe_gate_up_q4k_decode_traffic.json")
 # The headline's kernel instantiations in a trace or counter file (the
 # one-token kernels of the Q4_K / Q6_K layer at hidden 2048, inter 512:
@@ -66,8 +69,9 @@ TRAFFIC_FILE = os.path.join(HERE, "profiles", "moe_gate_up_q4k_decode_traffic.js
 # row>, down <T = 1, format 2 = Q6_K, 16 units>). The default run dispatches
 # them first; other workloads of the same run use other instantiations or
 # come later.
-HEADLINE_KERNELS = {"k_moe_router": "k_moe_router<1, 8>", "k_moe_gate_up1": "k_moe_gate_up1<0, 64>",
-                    "k_moe_down": "k_moe_down<1, 2, 16>"}
+HEADLINE_KERNELS = {"k_moe_router": "k_moe_router<1, 8>",
+                    "k_moe_gate_up1": "k_moe_gate_up1<0, 64, false>",
+                    "k_moe_down": "k_moe_down<1, 2, 16, false>"}
 
 
 # --prefill-mix layer kinds and the formats they hold
@@ -896,11 +900,10 @@ def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
               "roofline": hbm_roofline(b2m, us2),
               "workload": "T=2 through the per-token fp32 kernels with the router GEMV, "
                           "Q4_K/Q6_K layer pool"}
-    # small batches through the automatic path: 3 tokens per launch take the
-    # fp32 per-token kernels (one format per matrix kind), 4 the small-batch
-    # MFMA kernels, 8 the grouped ones
+    # small batches through the automatic path: up to 15 tokens take the
+    # fp32 per-token kernels (one grid row per token), 16 the grouped ones
     small, small_roof = {}, {}
-    for Ts in (3, 4, 8):
+    for Ts in (3, 4, 8, 16):
         Xs = torch.empty(len(pool), Ts, HIDDEN, dtype=torch.float32, device="cuda")
         for j in range(len(pool)):
             Q.synth_normal(Xs[j], Ts * HIDDEN, 1.0, 4010 + Ts, S.stream_id(j, S.K_X))
@@ -914,13 +917,13 @@ def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
         us_s = 1e6 * secs / len(pool)
         small["T%d" % Ts] = round(us_s, 3)
         # bytes one call must read: the distinct selected experts' matrices,
-        # the shared expert, the router and the inputs (the 8-token calls
+        # the shared expert, the router and the inputs (the 16-token calls
         # take the grouped kernels: their roof is the lower of HBM and MFMA)
         ss = is_.cpu().numpy()
         bs = float(np.mean([sum(L.expert_bytes(int(e)) for e in np.unique(ss[j])) + L.shared_bytes()
                             + N_EXPERTS * HIDDEN * 4 + 2 * Ts * HIDDEN * 4
                             for j, L in enumerate(pool)]))
-        if Ts >= 5:
+        if Ts >= GROUPED_MIN_TOKENS:
             fl = 2.0 * (Ts * TOP_K + Ts) * 3 * HIDDEN * INTER
             small_roof["T%d" % Ts] = flop_roofline(fl, bs, us_s)
         else:
@@ -970,7 +973,7 @@ def main():
         del a, b
     want_prefill = args.workload in ("all", "prefill")
     cpu_cfg = None if args.no_cpu else {}
-    ctx = Q.Context(0, max_tokens=args.prefill_tokens if want_prefill else 4)
+    ctx = Q.Context(0, max_tokens=max(args.prefill_tokens, 16) if want_prefill else 4)
     P = args.pool
     mix = ("iq2m" if args.workload == "iq2m" else
            args.prefill_mix if args.workload == "prefill" else "q4k")
