@@ -61,7 +61,7 @@ MFMA_BF16_PEAK_TFLOPS = 2500.0
 HIDDEN, INTER, N_EXPERTS, TOP_K = 2048, 512, 256, 8
 # calls of this many tokens or more take the grouped kernels on a Q4_K / Q6_K
 # layer in the automatic mode (qw6_hip_set_mode)
-GROUPED_MIN_TOKENS = 16
+GROUPED_MIN_TOKENS = 17
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "moe_gate_up_q4k_decode_traffic.json")
 # The headline's kernel instantiations in a trace or counter file (the
 # one-token kernels of the Q4_K / Q6_K layer at hidden 2048, inter 512:
@@ -900,8 +900,8 @@ def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
               "roofline": hbm_roofline(b2m, us2),
               "workload": "T=2 through the per-token fp32 kernels with the router GEMV, "
                           "Q4_K/Q6_K layer pool"}
-    # small batches through the automatic path: up to 15 tokens take the
-    # fp32 per-token kernels (one grid row per token), 16 the grouped ones
+    # small batches through the automatic path: up to 16 tokens take the
+    # fp32 per-token kernels (one grid row per token) on this layer
     small, small_roof = {}, {}
     for Ts in (3, 4, 8, 16):
         Xs = torch.empty(len(pool), Ts, HIDDEN, dtype=torch.float32, device="cuda")
@@ -917,8 +917,8 @@ def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
         us_s = 1e6 * secs / len(pool)
         small["T%d" % Ts] = round(us_s, 3)
         # bytes one call must read: the distinct selected experts' matrices,
-        # the shared expert, the router and the inputs (the 16-token calls
-        # take the grouped kernels: their roof is the lower of HBM and MFMA)
+        # the shared expert, the router and the inputs (calls that take the
+        # grouped kernels: the lower of the HBM and MFMA roofs)
         ss = is_.cpu().numpy()
         bs = float(np.mean([sum(L.expert_bytes(int(e)) for e in np.unique(ss[j])) + L.shared_bytes()
                             + N_EXPERTS * HIDDEN * 4 + 2 * Ts * HIDDEN * 4

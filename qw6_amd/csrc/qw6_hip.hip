@@ -20,7 +20,7 @@
 // one-token call's work, and a token's workgroup b shares an XCD with every
 // other token's workgroup b, so experts that several tokens select, and the
 // shared expert, are read from HBM about once. In the automatic mode, calls
-// of 16 tokens or more (11 for layers holding IQ formats) take the grouped
+// of 17 tokens or more (14 for layers holding IQ formats) take the grouped
 // bf16-MFMA kernels of qw6_prefill.hip (one launch per expert format
 // present); mode 3 runs the small-batch MFMA kernels k_mx_* in launches of up
 // to 4 tokens.
@@ -61,9 +61,9 @@ constexpr uint32_t kMaxTok = 4;         // tokens per launch of the small-batch 
 constexpr uint32_t kSplitMaxTok = 16;   // tokens per launch of the fp32 kernels (one grid row each)
 // Automatic switch to the grouped MFMA path: calls of this many tokens or
 // more (where the two paths' timings cross on one MI355X: Q4_K / Q6_K
-// layers at 16 tokens, layers holding IQ formats at 11)
-constexpr uint32_t kGroupedMinTokens = 16;
-constexpr uint32_t kGroupedMinTokensIq = 11;
+// layers past the 16 tokens of one launch, layers holding IQ formats at 14)
+constexpr uint32_t kGroupedMinTokens = 17;
+constexpr uint32_t kGroupedMinTokensIq = 14;
 constexpr uint32_t kLdsBudget = 64 * 1024;   // dynamic LDS per workgroup
 constexpr uint32_t kMxLdsBudget = 150 * 1024;   // k_mx_*: gfx950 has 160 KB per workgroup
 constexpr int kProfEv = 6;         // events per profiled MoE call (3 kernels x start/stop)
@@ -505,16 +505,19 @@ __host__ __device__ constexpr uint32_t pair_loads(int f) { return (16u * fmt_blo
 
 // Stage the step groups g (gate) and u (up) of gbytes each (8 blocks, a
 // multiple of 16 bytes) into one LDS pair slot, gate at +0 and up at +gbytes,
-// with nl 16-byte direct-to-LDS loads per lane; lanes past the pair's end
-// reload the gate group's first chunk into the slot's tail.
+// with nl 16-byte direct-to-LDS loads per lane (the slot holds exactly the
+// pair's 2 gbytes).
 __device__ __forceinline__ void stage_pair(uint8_t* slot, const uint8_t* g, const uint8_t* u,
                                            uint32_t gbytes, uint32_t nl) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t n16 = gbytes >> 4;
     for (uint32_t i = 0; i < nl; i++) {
         const uint32_t c = 64u * i + lane;
-        const uint8_t* src = c < n16 ? g + 16ull * c : c < 2 * n16 ? u + 16ull * (c - n16) : g;
-        __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(slot + 1024u * i), 16, 0, 0);
+        const uint8_t* src = c < n16 ? g + 16ull * c : u + 16ull * (c - n16);
+        // lanes past the pair's end stay idle (every load has an active
+        // lane: nl = ceil(2 n16 / 64)), so the slot is the pair's bytes
+        if (c < 2 * n16)
+            __builtin_amdgcn_global_load_lds((glb_void_t*)src, (lds_void_t*)(slot + 1024u * i), 16, 0, 0);
     }
 }
 
@@ -2899,10 +2902,10 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
     m.md = (E->fmask_dn & ((1u << F_NFMT) - 1u)) | (has_sh ? 1u << sd.fmt : 0u);
     const uint32_t rpsg = 64 / (L->hidden / 32), rpsd = 64 / (L->inter / 32);
     // k_moe_gate_up1: LDS pair slot of the widest (gate, up) step pair in use
-    uint32_t pl = has_sh ? pair_loads(sg.fmt) : 1u;
+    uint32_t pbb = has_sh ? fmt_block_bytes(sg.fmt) : 0u;   // widest block in use
     for (int f = 0; f < F_NFMT; f++)
-        if (E->fmt_gu < 0 || E->fmt_gu == f) pl = std::max(pl, pair_loads(f));
-    a.gu_pb = 1024u * pl;
+        if (E->fmt_gu < 0 || E->fmt_gu == f) pbb = std::max(pbb, fmt_block_bytes(f));
+    a.gu_pb = 16u * pbb;   // 8 blocks of gate and of up
     const uint32_t R_c = kStepsDn * rpsd;
     m.grid_c = (L->hidden + R_c - 1) / R_c;
     // the router kernel runs when it has work: the router GEMV (no logits
@@ -2938,7 +2941,11 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
         a.idx_out = idx ? idx + (size_t)t0 * L->top_k : nullptr;
         a.w_out = w ? w + (size_t)t0 * L->top_k : nullptr;
         const uint32_t ntot = a.max_u + (has_sh ? 1u : 0u);
-        m.nw_c = ntot < down_waves<1>() ? ntot : down_waves<1>();
+        // k_moe_down: 9 waves (8 routed matrices + the shared one); 8 from 4
+        // tokens on (3 for layers without IQ formats; one wave takes two
+        // matrices), where 24 waves fit three workgroups per CU instead of two
+        const uint32_t nw_dn = T >= 4 || (T == 3 && mdn == 0) ? 8u : down_waves<1>();
+        m.nw_c = ntot < nw_dn ? ntot : nw_dn;
         m.lds_c = (size_t)tab_bytes(mdn) + (size_t)m.nw_c * kStepsDn * kSlotBytes +
                   (size_t)ntot * R_c * 4 + 16;
         if (!mx && m.lds_c > kLdsBudget) return fail("down tile exceeds the LDS budget");

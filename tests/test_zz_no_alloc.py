@@ -34,7 +34,7 @@ def test_noalloc_matches_moe_forward():
         dbig.norm_w, dbig.norm_eps = nw.data_ptr(), 1e-6
         # (layer, hidden, tokens, residual, mode): both entry points run the
         # same per-token kernels in the same mode (the regular one would take
-        # the grouped kernels for 16 tokens or more in mode 0). 8 tokens and 4
+        # the grouped kernels for 17 tokens or more in mode 0). 8 tokens and 4
         # in mode 3 run the small-batch MFMA kernels (k_mx_*) on the static
         # array's operand regions, in two 4-token launches and in one; 18 in
         # mode 1 the fp32 kernels in launches of 16 and 2 tokens.
