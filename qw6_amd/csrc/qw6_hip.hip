@@ -1108,11 +1108,12 @@ __global__ __launch_bounds__(64 * down_waves<T>()) void k_moe_down(MoeArgs a) {
     // lattice tables visible, and a loop around it (or a branch on the
     // count) would make the compiler wait for earlier loads (the gate
     // weights, residual, lattice tables, the count) before its activation
-    // loads. The launch has nw <= max_u + has_sh waves, but tokens that
-    // share experts (or select expert 0 at several ranks) leave fewer
-    // matrices: a wave past them takes slot-table entry wave - has_sh,
-    // which repeats slot 0's matrix, and writes its ybuf row, which the
-    // combine does not read (m < nw, so the row is inside the allocation).
+    // loads. The launch has nw <= max_u + has_sh waves, and k_moe_gate_up1
+    // publishes every rank of its token (n = max_u = top_k), so each wave's
+    // first matrix is a selected one. (A table's entries past its count
+    // repeat slot 0's matrix: a wave past the count would stream real
+    // weights into a ybuf row the combine does not read, m < nw keeping
+    // the row inside the allocation.)
     auto matrix = [&](uint32_t m, bool first) {
         const bool sh = has_sh && m == 0;
         const uint32_t u = m - has_sh;
