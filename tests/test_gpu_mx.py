@@ -41,7 +41,7 @@ def torch_dev():
 
 @pytest.fixture(scope="module")
 def ctx(torch_dev):
-    c = Q.Context(0, max_tokens=8)
+    c = Q.Context(0, max_tokens=16)
     yield c
     c.close()
 
@@ -161,6 +161,30 @@ def test_mx_narrow_hidden_vs_oracle(torch_dev, ctx, hidden, mix):
             out, idx = run(torch_dev, ctx, L, xs, 3)
             n += check_tokens(L, xs, out, idx, router=router)
         assert n >= 8
+    finally:
+        L.free()
+
+
+@pytest.mark.parametrize("hidden,inter,n_exp,top_k,mix",
+                         [(512, 256, 32, 8, "q4k"), (1024, 256, 64, 4, "iq2m"),
+                          (256, 256, 32, 8, "iq2b"), (2048, 1024, 64, 6, "q5k")])
+def test_token_rows_other_shapes_vs_oracle(torch_dev, ctx, hidden, inter, n_exp, top_k, mix):
+    """The fp32 kernels' launches of several tokens (one grid row per token,
+    mode 1) on other layer shapes: 256-2048 columns per gate/up row (the
+    generic row-length instantiations), top_k 4 and 6 (per-token slot tables
+    and mid blocks of top_k + 1 rows, down workgroups of fewer waves), a
+    Q5_K layer. T = 2, 5 and 16 against the oracle."""
+    from qw6_amd.workload import SynthLayer
+    say("token rows", hidden, inter, n_exp, top_k, mix)
+    L = SynthLayer(ctx, 73, 0, mix, hidden=hidden, inter=inter, n_experts=n_exp, top_k=top_k)
+    try:
+        router = L.router_host()
+        n = 0
+        for T in (2, 5, 16):
+            xs = np.stack([cases.token_x(730 + T, 2, t, hidden=hidden) for t in range(T)])
+            out, idx = run(torch_dev, ctx, L, xs, 1)
+            n += check_tokens(L, xs, out, idx, router=router)
+        assert n >= 18
     finally:
         L.free()
 
