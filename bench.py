@@ -885,7 +885,8 @@ def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
     def fwd2(sp):
         for j in range(len(pool)):
             ctx.moe_forward(pool[j].desc, X2[j], o2[j], n_tok=2, idx=i2[j], stream=sp)
-    sec2, _ = graph_time(torch, fwd2, max(1, args.steps // len(pool)))
+    # at least 10 replays of the pool (16 layers each), whatever --steps is
+    sec2, _ = graph_time(torch, fwd2, max(10, args.steps // len(pool)))
     us2 = 1e6 * sec2 / len(pool)
     sel = i2.cpu().numpy()
     b2 = []
@@ -913,7 +914,7 @@ def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
         def fwds(sp, Ts=Ts, Xs=Xs, os_=os_, is_=is_):
             for j in range(len(pool)):
                 ctx.moe_forward(pool[j].desc, Xs[j], os_[j], n_tok=Ts, idx=is_[j], stream=sp)
-        secs, _ = graph_time(torch, fwds, max(1, args.steps // len(pool)))
+        secs, _ = graph_time(torch, fwds, max(10, args.steps // len(pool)))
         us_s = 1e6 * secs / len(pool)
         small["T%d" % Ts] = round(us_s, 3)
         # bytes one call must read: the distinct selected experts' matrices,
