@@ -174,8 +174,8 @@ int qw6_hip_moe_forward_noalloc(qw6_hip_ctx_t *ctx,
 
 /* Path selection for qw6_hip_moe_forward:
  * 0 = automatic (default): the fp32 per-token kernels for calls of up to 16
- *     tokens (13 when the layer holds IQ formats), the grouped MFMA kernels
- *     from 17 (14) tokens on (one launch per expert format present, so layers
+ *     tokens (15 when the layer holds IQ formats), the grouped MFMA kernels
+ *     from 17 (16) tokens on (one launch per expert format present, so layers
  *     whose experts differ in format take them too);
  * 1 = always the fp32 per-token kernels (launches of up to 16 tokens);
  * 2 = always the grouped MFMA kernels;

@@ -20,7 +20,7 @@
 // one-token call's work, and a token's workgroup b shares an XCD with every
 // other token's workgroup b, so experts that several tokens select, and the
 // shared expert, are read from HBM about once. In the automatic mode, calls
-// of 17 tokens or more (14 for layers holding IQ formats) take the grouped
+// of 17 tokens or more (16 for layers holding IQ formats) take the grouped
 // bf16-MFMA kernels of qw6_prefill.hip (one launch per expert format
 // present); mode 3 runs the small-batch MFMA kernels k_mx_* in launches of up
 // to 4 tokens.
@@ -61,9 +61,9 @@ constexpr uint32_t kMaxTok = 4;         // tokens per launch of the small-batch 
 constexpr uint32_t kSplitMaxTok = 16;   // tokens per launch of the fp32 kernels (one grid row each)
 // Automatic switch to the grouped MFMA path: calls of this many tokens or
 // more (where the two paths' timings cross on one MI355X: Q4_K / Q6_K
-// layers past the 16 tokens of one launch, layers holding IQ formats at 14)
+// layers past the 16 tokens of one launch, layers holding IQ formats at 16)
 constexpr uint32_t kGroupedMinTokens = 17;
-constexpr uint32_t kGroupedMinTokensIq = 14;
+constexpr uint32_t kGroupedMinTokensIq = 16;
 constexpr uint32_t kLdsBudget = 64 * 1024;   // dynamic LDS per workgroup
 constexpr uint32_t kMxLdsBudget = 150 * 1024;   // k_mx_*: gfx950 has 160 KB per workgroup
 constexpr int kProfEv = 6;         // events per profiled MoE call (3 kernels x start/stop)
@@ -736,11 +736,23 @@ __device__ __forceinline__ bool route_slot_select(const MoeArgs& a, uint32_t (&k
 // sigmoid(shared_router . x) (qw6.c:2267-2285). NV = hidden / 256 float4 per
 // lane, a template constant so that every load is unconditional. With a.xa
 // set, waves e < hidden / 32 also write the small-batch MFMA operands.
-template <int T, int NV>
+// MT: one token per row of the grid (blockIdx.y; T = 1), as the expert
+// kernels' launches of several tokens; the grid's x extent is rounded up to a
+// multiple of 8, so router row e is read on XCD e % 8 for every token.
+template <int T, int NV, bool MT = false>
 __global__ __launch_bounds__(64) void k_moe_router(MoeArgs a) {
     TRACE_SCOPE(0);
     const uint32_t lane = threadIdx.x, e = blockIdx.x;
     const uint32_t H = 256 * NV;   // NV float4 per lane
+    if constexpr (MT) {
+        static_assert(T == 1, "one token per grid row");
+        if (e >= a.n_experts + (a.shared_router ? 1u : 0u)) return;   // the rounding's workgroups
+        const uint32_t t = blockIdx.y;
+        a.x += (size_t)t * H;
+        a.xn += (size_t)t * H;
+        a.logits += (size_t)t * a.n_experts;
+        a.sw += t;
+    }
     float4 xv[T][NV];
 #pragma unroll
     for (int t = 0; t < T; t++)
@@ -802,69 +814,6 @@ __global__ __launch_bounds__(64) void k_moe_router(MoeArgs a) {
         if (lane == 0) {
             if (e < a.n_experts) a.logits[(size_t)t * a.n_experts + e] = acc;
             else a.sw[t] = 1.0f / (1.0f + expf(-acc));
-        }
-    }
-}
-
-// k_moe_router for launches of more than kMaxTok tokens (a.T of them, the
-// fp32 kernels' launches): the same per token, in groups of kMaxTok, with the
-// router row and the norm weight loaded once.
-template <int NV>
-__global__ __launch_bounds__(64) void k_moe_router_n(MoeArgs a) {
-    constexpr int G = kMaxTok;
-    const uint32_t lane = threadIdx.x, e = blockIdx.x;
-    const uint32_t H = 256 * NV;   // NV float4 per lane
-    const float* wrow = e < a.n_experts ? a.router : e == a.n_experts ? a.shared_router : nullptr;
-    if (wrow && e < a.n_experts) wrow += (size_t)e * H;
-    float4 wv[NV], nw[NV];
-#pragma unroll
-    for (uint32_t i = 0; i < NV; i++) {
-        if (wrow) wv[i] = ((const float4*)wrow)[64 * i + lane];
-        if (a.norm_w) nw[i] = ((const float4*)a.norm_w)[64 * i + lane];
-    }
-    const uint32_t nq = H / 4, nwv = a.n_experts + (a.shared_router ? 1u : 0u);
-    const uint32_t per = (nq + nwv - 1) / nwv;   // float4s of the normalised input per wave
-    for (uint32_t t0 = 0; t0 < a.T; t0 += G) {
-        float4 xv[G][NV];
-#pragma unroll
-        for (int t = 0; t < G; t++)
-#pragma unroll
-            for (uint32_t i = 0; i < NV; i++)
-                xv[t][i] = t0 + t < a.T ? ((const float4*)(a.x + (size_t)(t0 + t) * H))[64 * i + lane]
-                                        : make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int t = 0; t < G; t++) {
-            if (t0 + t >= a.T) break;
-            if (a.norm_w) {
-                float ss = 0.f;
-#pragma unroll
-                for (uint32_t i = 0; i < NV; i++) {
-                    ss = fmaf(xv[t][i].x, xv[t][i].x, ss); ss = fmaf(xv[t][i].y, xv[t][i].y, ss);
-                    ss = fmaf(xv[t][i].z, xv[t][i].z, ss); ss = fmaf(xv[t][i].w, xv[t][i].w, ss);
-                }
-                ss = group_sum<64>(ss);
-                const float sc = 1.0f / sqrtf(ss / (float)H + a.norm_eps);
-#pragma unroll
-                for (uint32_t i = 0; i < NV; i++) {
-                    xv[t][i].x = xv[t][i].x * sc * nw[i].x; xv[t][i].y = xv[t][i].y * sc * nw[i].y;
-                    xv[t][i].z = xv[t][i].z * sc * nw[i].z; xv[t][i].w = xv[t][i].w * sc * nw[i].w;
-                    const uint32_t q = 64 * i + lane;
-                    if (q >= e * per && q < (e + 1) * per)
-                        ((float4*)(a.xn + (size_t)(t0 + t) * H))[q] = xv[t][i];
-                }
-            }
-            if (!wrow) continue;
-            float acc = 0.f;
-#pragma unroll
-            for (uint32_t i = 0; i < NV; i++) {
-                acc = fmaf(wv[i].x, xv[t][i].x, acc); acc = fmaf(wv[i].y, xv[t][i].y, acc);
-                acc = fmaf(wv[i].z, xv[t][i].z, acc); acc = fmaf(wv[i].w, xv[t][i].w, acc);
-            }
-            acc = group_sum<64>(acc);
-            if (lane == 0) {
-                if (e < a.n_experts) a.logits[(size_t)(t0 + t) * a.n_experts + e] = acc;
-                else a.sw[t0 + t] = 1.0f / (1.0f + expf(-acc));
-            }
         }
     }
 }
@@ -2718,20 +2667,24 @@ int launch_moe(const MoeArgs& a, const MoeLaunch& m, hipStream_t st, hipEvent_t*
             default: rc = launch_k(k_moe_router<T, 8>, m.grid_r, 64, 0, st, ev, a); break;
             }
         };
-        auto by_nv_loop = [&]() {   // more than kMaxTok tokens: groups of kMaxTok
+        auto by_nv_rows = [&]() {   // one token per grid row
+            const uint32_t gx = (m.grid_r + 7u) & ~7u;
             switch (a.hidden / 256) {
-            case 1: rc = launch_k(k_moe_router_n<1>, m.grid_r, 64, 0, st, ev, a); break;
-            case 2: rc = launch_k(k_moe_router_n<2>, m.grid_r, 64, 0, st, ev, a); break;
-            case 4: rc = launch_k(k_moe_router_n<4>, m.grid_r, 64, 0, st, ev, a); break;
-            default: rc = launch_k(k_moe_router_n<8>, m.grid_r, 64, 0, st, ev, a); break;
+            case 1: rc = launch_k(k_moe_router<1, 1, true>, gx, 64, 0, st, ev, a, a.T); break;
+            case 2: rc = launch_k(k_moe_router<1, 2, true>, gx, 64, 0, st, ev, a, a.T); break;
+            case 4: rc = launch_k(k_moe_router<1, 4, true>, gx, 64, 0, st, ev, a, a.T); break;
+            default: rc = launch_k(k_moe_router<1, 8, true>, gx, 64, 0, st, ev, a, a.T); break;
             }
         };
-        switch (a.T) {
-        case 1: by_nv(IC<1>{}); break;
-        case 2: by_nv(IC<2>{}); break;
-        case 3: by_nv(IC<3>{}); break;
-        case 4: by_nv(IC<4>{}); break;
-        default: by_nv_loop(); break;
+        if (!m.mx && a.T > 1) {   // the fp32 kernels' launches of several tokens
+            by_nv_rows();
+        } else {
+            switch (a.T) {
+            case 1: by_nv(IC<1>{}); break;
+            case 2: by_nv(IC<2>{}); break;
+            case 3: by_nv(IC<3>{}); break;
+            default: by_nv(IC<4>{}); break;
+            }
         }
         if (rc) return rc;
     } else if (ev) {

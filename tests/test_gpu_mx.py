@@ -285,7 +285,7 @@ def test_auto_mode_mixed_chunks_vs_oracle(torch_dev, ctx):
     """Calls of 5-7 tokens on a mixed-format layer (IQ2_XXS gate/up, IQ3_S /
     IQ2_S down), through the call without allocation (which never takes the
     grouped kernels) and the automatic path: both run one launch of the fp32
-    kernels, one grid row per token (the grouped kernels start at 14 tokens
+    kernels, one grid row per token (the grouped kernels start at 16 tokens
     for layers holding IQ formats). A uniform Q4_K layer under the per-token
     mode (1) takes 5 tokens in one launch too."""
     torch = torch_dev

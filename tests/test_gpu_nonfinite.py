@@ -14,8 +14,8 @@ order, so the selection is exact on every path.
 
 Paths: the fp32 per-token kernels (mode 1) and the small-batch MFMA kernels
 (mode 3) at T = 1-4, the automatic choice (mode 0) at T = 1-4, the fp32
-kernels' launches of more tokens (6 and 16 in one launch, the router in
-groups of four; 18 = 16 + 2), the grouped MFMA kernels (mode 2) at T = 5 and
+kernels' launches of more tokens (6 and 16 in one launch, the router with
+one grid row per token too; 18 = 16 + 2), the grouped MFMA kernels (mode 2) at T = 5 and
 at 64 (the poisoned tokens among 59 finite ones); and the fused RMSNorm with
 the residual added (the decode-step glue) at T = 1, 6 and 16 on the fp32
 kernels and 5 on the grouped ones. Bars: indices bit-exact; gate weights NaN where the oracle's
