@@ -191,15 +191,16 @@ def test_token_rows_other_shapes_vs_oracle(torch_dev, ctx, hidden, inter, n_exp,
 
 def test_mx_no_shared_given_logits_residual(torch_dev, ctx):
     """No shared expert, router logits given (Zipf), residual added: the router
-    kernel then only writes the operands."""
+    kernel then only writes the operands (mode 3), or does not run (the fp32
+    kernels, one grid row per token, at 3 and 9 tokens)."""
     from qw6_amd.workload import SynthLayer
     L = SynthLayer(ctx, 64, 0, "q4k", shared=False, router=False)
     try:
-        for T in (1, 3):
+        for T, mode in ((1, 3), (3, 3), (3, 1), (9, 1)):
             lg = S.zipf_logits(640 + T, T)
             xs = np.stack([cases.token_x(640 + T, 1, t) for t in range(T)])
             res = np.stack([cases.token_x(641 + T, 1, t) for t in range(T)])
-            out, idx = run(torch_dev, ctx, L, xs, 3, logits=lg, residual=res)
+            out, idx = run(torch_dev, ctx, L, xs, mode, logits=lg, residual=res)
             assert check_tokens(L, xs, out, idx, logits=lg, resid=res) == T
     finally:
         L.free()
