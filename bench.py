@@ -35,7 +35,8 @@ pair) and single-token steps of the 40-layer stack.
                 grouped bf16-MFMA kernels, Q4_K / Q6_K experts: us/layer,
                 TFLOP/s, MFMA fraction, HBM GB/s;
   mtp_T2        two tokens (MTP draft verification) with the router GEMV, and
-                small batches (3, 4, 8, 16 tokens) through the automatic path;
+                small batches (3, 4, 8, 16 tokens) through the automatic path
+                (--workload mtp: these alone);
   prefill_T512_iq2xxs_iq3s  the grouped kernels on an IQ layer (IQ2_XXS
                 gate/up, IQ3_S down, Q4_K / Q6_K shared expert);
   output_head   the greedy next-token head: final RMSNorm, Q6_K [248320 x
@@ -89,7 +90,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--pool", type=int, default=16)
     ap.add_argument("--workload", default="all",
-                    choices=["all", "q4k", "iq2m", "stack", "prefill", "head", "floor", "gguf"])
+                    choices=["all", "q4k", "iq2m", "stack", "prefill", "mtp", "head", "floor",
+                             "gguf"])
     ap.add_argument("--stack-steps", type=int, default=128)
     ap.add_argument("--prefill-tokens", type=int, default=512)
     ap.add_argument("--prefill-mix", default="q4k", choices=sorted(PREFILL_FORMATS),
@@ -99,6 +101,9 @@ def parse():
     ap.add_argument("--no-small-batch", action="store_true",
                     help="with --workload prefill: time the prefill_T512 case only (no T=2 and "
                          "small-batch cases), for a kernel profile of that workload alone")
+    ap.add_argument("--small-batch-sizes", default="3,4,8,16",
+                    help="token counts of the small-batch rows beside the two-token case "
+                         "(comma-separated; 'none' for the two-token case alone)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0,
                     help="CPU-baseline budget over all workloads (the oracle port, one thread "
                          "and OpenMP)")
@@ -822,11 +827,13 @@ def bench_stack(torch, Q, S, ctx, args, cpu=None):
 
 
 def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
-                  formats=PREFILL_FORMATS["q4k"], cpu=None):
-    """T tokens with Zipf-skewed logits through the grouped MFMA kernels, plus
-    (with_t2) the T=2 MTP case through the per-token kernels with the router
-    GEMV."""
+                  formats=PREFILL_FORMATS["q4k"], cpu=None, with_grouped=True):
+    """T tokens with Zipf-skewed logits through the grouped MFMA kernels
+    (with_grouped), plus (with_t2) the T=2 MTP case through the per-token
+    kernels with the router GEMV and the small-batch rows."""
     import numpy as np
+    if not with_grouped:
+        return None, bench_mtp(torch, Q, S, ctx, pool, args)
     T = args.prefill_tokens
     P = min(2, len(pool))
     lg_h = [S.zipf_logits(4000 + j, T) for j in range(P)]
@@ -874,8 +881,13 @@ def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
                                                          args.cpu_seconds * 0.15, T)
     if not with_t2:
         return res, None
+    return res, bench_mtp(torch, Q, S, ctx, pool, args)
 
-    # T = 2 (MTP draft verification): router GEMV + per-token kernels
+
+def bench_mtp(torch, Q, S, ctx, pool, args):
+    """T = 2 (MTP draft verification) through the per-token kernels with the
+    router GEMV, then the small-batch rows (--small-batch-sizes)."""
+    import numpy as np
     X2 = torch.empty(len(pool), 2, HIDDEN, dtype=torch.float32, device="cuda")
     for j in range(len(pool)):
         Q.synth_normal(X2[j], 2 * HIDDEN, 1.0, 4002, S.stream_id(j, S.K_X))
@@ -904,7 +916,9 @@ def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
     # small batches through the automatic path: up to 16 tokens take the
     # fp32 per-token kernels (one grid row per token) on this layer
     small, small_roof = {}, {}
-    for Ts in (3, 4, 8, 16):
+    sizes = [] if args.small_batch_sizes in ("", "none") else \
+        [int(v) for v in args.small_batch_sizes.split(",")]
+    for Ts in sizes:
         Xs = torch.empty(len(pool), Ts, HIDDEN, dtype=torch.float32, device="cuda")
         for j in range(len(pool)):
             Q.synth_normal(Xs[j], Ts * HIDDEN, 1.0, 4010 + Ts, S.stream_id(j, S.K_X))
@@ -931,7 +945,7 @@ def bench_prefill(torch, Q, S, ctx, pool, args, with_t2=True,
             small_roof["T%d" % Ts] = hbm_roofline(bs, us_s)
     res_t2["small_batch_us_per_layer"] = small
     res_t2["small_batch_roofline"] = small_roof
-    return res, res_t2
+    return res_t2
 
 
 def main():
@@ -972,7 +986,7 @@ def main():
             torch.mul(a, 2.0, out=b)
         torch.cuda.synchronize()
         del a, b
-    want_prefill = args.workload in ("all", "prefill")
+    want_prefill = args.workload in ("all", "prefill", "mtp")
     cpu_cfg = None if args.no_cpu else {}
     ctx = Q.Context(0, max_tokens=max(args.prefill_tokens, 16) if want_prefill else 4)
     P = args.pool
@@ -981,7 +995,7 @@ def main():
     secondary = {}
     res_main = None
     pool = []
-    if args.workload in ("all", "q4k", "iq2m", "prefill", "gguf"):
+    if args.workload in ("all", "q4k", "iq2m", "prefill", "mtp", "gguf"):
         if args.workload == "prefill":
             P = 2   # the prefill figure alternates two layers
         log("building %d synthetic layers (%s)" % (P, mix))
@@ -992,16 +1006,18 @@ def main():
         out = torch.empty(P, HIDDEN, dtype=torch.float32, device="cuda")
         idx = torch.zeros(P, TOP_K, dtype=torch.int32, device="cuda")
         torch.cuda.synchronize()
-        if args.workload != "prefill":
+        if args.workload not in ("prefill", "mtp"):
             res_main = bench_decode(torch, Q, S, ctx, pool, X, out, idx, args)
             log("decode %s: %s" % (mix, json.dumps(res_main)))
     if want_prefill:
         pf, t2 = bench_prefill(torch, Q, S, ctx, pool, args,
                                with_t2=not args.no_small_batch and mix == "q4k",
                                formats=PREFILL_FORMATS[mix],
-                               cpu=cpu_cfg if mix == "q4k" else None)
-        secondary["prefill_T%d%s" % (args.prefill_tokens, "" if mix == "q4k" else "_" + mix)] = pf
-        log("prefill: %s" % json.dumps(pf))
+                               cpu=cpu_cfg if mix == "q4k" else None,
+                               with_grouped=args.workload != "mtp")
+        if pf is not None:
+            secondary["prefill_T%d%s" % (args.prefill_tokens, "" if mix == "q4k" else "_" + mix)] = pf
+            log("prefill: %s" % json.dumps(pf))
         if t2 is not None:
             secondary["mtp_T2"] = t2
             log("T=2: %s" % json.dumps(t2))
@@ -1010,7 +1026,7 @@ def main():
         gg = bench_gguf(torch, Q, S, ctx, pool, X, out, idx)
         secondary["gguf_layer"] = gg
         log("gguf layer: %s" % json.dumps(gg))
-    if cpu_cfg is not None and pool and mix == "q4k" and args.workload != "prefill":
+    if cpu_cfg is not None and pool and mix == "q4k" and args.workload not in ("prefill", "mtp"):
         xh = X.cpu().numpy()
         cpu_cfg["q4k_matvec_512x2048"] = cpu_matvec(args.cpu_seconds * 0.05)
         cpu_cfg["decode_layer_q4k"] = cpu_decode_layer(pool[0], xh, args.cpu_seconds * 0.2,
