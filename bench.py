@@ -70,7 +70,7 @@ TRAFFIC_FILE = os.path.join(HERE, "profiles", "moe_gate_up_q4k_decode_traffic.js
 # row>, down <T = 1, format 2 = Q6_K, 16 units>). The default run dispatches
 # them first; other workloads of the same run use other instantiations or
 # come later.
-HEADLINE_KERNELS = {"k_moe_router": "k_moe_router<1, 8>",
+HEADLINE_KERNELS = {"k_moe_router": "k_moe_router<1, 8, false>",
                     "k_moe_gate_up1": "k_moe_gate_up1<0, 64, false>",
                     "k_moe_down": "k_moe_down<1, 2, 16, false>"}
 
