@@ -189,6 +189,29 @@ def test_token_rows_other_shapes_vs_oracle(torch_dev, ctx, hidden, inter, n_exp,
         L.free()
 
 
+@pytest.mark.parametrize("mix", ["q4k", "iq2m"])
+def test_auto_switch_points_vs_oracle(torch_dev, mix):
+    """The automatic mode on both sides of its switch to the grouped kernels
+    (17 tokens for a Q4_K / Q6_K layer, 16 for one holding IQ formats): 15,
+    16 and 17 tokens against the oracle, at the fp32 bar (the grouped kernels
+    take three activation parts below 64 tokens)."""
+    from qw6_amd.workload import SynthLayer
+    c = Q.Context(0, max_tokens=17)
+    L = SynthLayer(c, 75, 0, mix)
+    try:
+        router = L.router_host()
+        n = 0
+        for T in (15, 16, 17):
+            say("auto switch", mix, T)
+            xs = np.stack([cases.token_x(750 + T, 2, t) for t in range(T)])
+            out, idx = run(torch_dev, c, L, xs, 0)
+            n += check_tokens(L, xs, out, idx, router=router)
+        assert n >= 40
+    finally:
+        L.free()
+        c.close()
+
+
 def test_mx_no_shared_given_logits_residual(torch_dev, ctx):
     """No shared expert, router logits given (Zipf), residual added: the router
     kernel then only writes the operands (mode 3), or does not run (the fp32
