@@ -968,6 +968,7 @@ __global__ __launch_bounds__(64 * 9) void k_moe_gate_up1(MoeArgs a) {
 // its wave starts streaming at once), then the slots in first-use order.
 // Wave w takes matrices w, w + nw, ...; row sums meet in LDS and are
 // combined as out = sum_u wt[u] * y[u] + sw * y[shared] (+ residual).
+// (9: the 8 routed matrices of a token and the shared one)
 template <int T>
 __host__ __device__ constexpr uint32_t down_waves() { return T <= 2 ? 9u : 8u; }
 
@@ -2627,7 +2628,7 @@ struct MoeLaunch {
 };
 
 // The format sets with their own instantiations of the mixed-format expert
-// kernels (1-2 tokens, the model's row length): the IQ2_M layer's, IQ2_XXS
+// kernels (at the model's row length): the IQ2_M layer's, IQ2_XXS
 // routed gate/up beside a Q4_K shared one, and IQ3_S / IQ2_S routed downs
 // beside a Q6_K shared one. Other mixes take the six-format switch.
 constexpr uint32_t kSetGateUpIq2m = (1u << F_Q4K) | (1u << F_IQ2XXS);
