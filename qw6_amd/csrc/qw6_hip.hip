@@ -59,6 +59,10 @@ __device__ const IqTables g_tabs = make_tables();
 constexpr int kWG = 256;           // threads per workgroup (4 waves)
 constexpr uint32_t kMaxTok = 4;         // tokens per launch of the small-batch MFMA kernels
 constexpr uint32_t kSplitMaxTok = 16;   // tokens per launch of the fp32 kernels (one grid row each)
+// waves per router row for one token (hidden 512 to 2048): two halve each
+// wave's loads and sums (the 40-layer stack with its fused norm 17.70 ->
+// 17.35 us per layer; four measured the same as two)
+constexpr int kRouterWaves = 2;
 // Automatic switch to the grouped MFMA path: calls of this many tokens or
 // more (where the two paths' timings cross on one MI355X: Q4_K / Q6_K
 // layers past the 16 tokens of one launch, layers holding IQ formats at 16)
@@ -815,6 +819,72 @@ __global__ __launch_bounds__(64) void k_moe_router(MoeArgs a) {
             if (e < a.n_experts) a.logits[(size_t)t * a.n_experts + e] = acc;
             else a.sw[t] = 1.0f / (1.0f + expf(-acc));
         }
+    }
+}
+
+// k_moe_router for one token on W waves per router row: wave h takes the
+// float4 columns [h NV/W, (h + 1) NV/W) of the row, the input and the norm
+// weight; the parts' sums (of squares for the norm, of products for the
+// logit) meet in LDS and are added in wave order.
+template <int NV, int W>
+__global__ __launch_bounds__(64 * W) void k_moe_router_w(MoeArgs a) {
+    constexpr int NH = NV / W;   // float4 per lane per wave
+    static_assert(NH >= 1 && NH * W == NV, "W divides the row's float4 per lane");
+    __shared__ float s_part[2][W];   // [sum of squares, dot product][wave]
+    const uint32_t lane = threadIdx.x & 63u, h = threadIdx.x >> 6, e = blockIdx.x;
+    const uint32_t H = 256 * NV;
+    float4 xv[NH];
+#pragma unroll
+    for (int i = 0; i < NH; i++) xv[i] = ((const float4*)a.x)[64 * (h * NH + i) + lane];
+    const float* wrow = e < a.n_experts ? a.router : e == a.n_experts ? a.shared_router : nullptr;
+    if (wrow && e < a.n_experts) wrow += (size_t)e * H;
+    float4 wv[NH];
+#pragma unroll
+    for (int i = 0; i < NH; i++)
+        if (wrow) wv[i] = ((const float4*)wrow)[64 * (h * NH + i) + lane];
+    if (a.norm_w) {
+        float4 nw[NH];
+#pragma unroll
+        for (int i = 0; i < NH; i++) nw[i] = ((const float4*)a.norm_w)[64 * (h * NH + i) + lane];
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < NH; i++) {
+            ss = fmaf(xv[i].x, xv[i].x, ss); ss = fmaf(xv[i].y, xv[i].y, ss);
+            ss = fmaf(xv[i].z, xv[i].z, ss); ss = fmaf(xv[i].w, xv[i].w, ss);
+        }
+        ss = group_sum<64>(ss);
+        if (lane == 0) s_part[0][h] = ss;
+        __syncthreads();
+        float sst = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; w++) sst += s_part[0][w];
+        const float sc = 1.0f / sqrtf(sst / (float)H + a.norm_eps);
+        const uint32_t nq = H / 4, nwv = a.n_experts + (a.shared_router ? 1u : 0u);
+        const uint32_t per = (nq + nwv - 1) / nwv;
+#pragma unroll
+        for (int i = 0; i < NH; i++) {
+            xv[i].x = xv[i].x * sc * nw[i].x; xv[i].y = xv[i].y * sc * nw[i].y;
+            xv[i].z = xv[i].z * sc * nw[i].z; xv[i].w = xv[i].w * sc * nw[i].w;
+            const uint32_t q = 64 * (h * NH + i) + lane;
+            if (q >= e * per && q < (e + 1) * per) ((float4*)a.xn)[q] = xv[i];
+        }
+    }
+    if (!wrow) return;   // the same for every wave
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < NH; i++) {
+        acc = fmaf(wv[i].x, xv[i].x, acc); acc = fmaf(wv[i].y, xv[i].y, acc);
+        acc = fmaf(wv[i].z, xv[i].z, acc); acc = fmaf(wv[i].w, xv[i].w, acc);
+    }
+    acc = group_sum<64>(acc);
+    if (lane == 0) s_part[1][h] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; w++) v += s_part[1][w];
+        if (e < a.n_experts) a.logits[e] = v;
+        else a.sw[0] = 1.0f / (1.0f + expf(-v));
     }
 }
 
@@ -2679,6 +2749,12 @@ int launch_moe(const MoeArgs& a, const MoeLaunch& m, hipStream_t st, hipEvent_t*
         };
         if (!m.mx && a.T > 1) {   // the fp32 kernels' launches of several tokens
             by_nv_rows();
+        } else if (!m.mx && a.hidden >= 512) {   // one token, kRouterWaves waves per router row
+            switch (a.hidden / 256) {
+            case 2: rc = launch_k(k_moe_router_w<2, kRouterWaves>, m.grid_r, 64 * kRouterWaves, 0, st, ev, a); break;
+            case 4: rc = launch_k(k_moe_router_w<4, kRouterWaves>, m.grid_r, 64 * kRouterWaves, 0, st, ev, a); break;
+            default: rc = launch_k(k_moe_router_w<8, kRouterWaves>, m.grid_r, 64 * kRouterWaves, 0, st, ev, a); break;
+            }
         } else {
             switch (a.T) {
             case 1: by_nv(IC<1>{}); break;
