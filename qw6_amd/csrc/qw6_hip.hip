@@ -826,13 +826,23 @@ __global__ __launch_bounds__(64) void k_moe_router(MoeArgs a) {
 // float4 columns [h NV/W, (h + 1) NV/W) of the row, the input and the norm
 // weight; the parts' sums (of squares for the norm, of products for the
 // logit) meet in LDS and are added in wave order.
-template <int NV, int W>
+// MT: one token per row of the grid (blockIdx.y), the grid's x extent a
+// multiple of 8, as k_moe_router<1, NV, true>.
+template <int NV, int W, bool MT = false>
 __global__ __launch_bounds__(64 * W) void k_moe_router_w(MoeArgs a) {
     constexpr int NH = NV / W;   // float4 per lane per wave
     static_assert(NH >= 1 && NH * W == NV, "W divides the row's float4 per lane");
     __shared__ float s_part[2][W];   // [sum of squares, dot product][wave]
     const uint32_t lane = threadIdx.x & 63u, h = threadIdx.x >> 6, e = blockIdx.x;
     const uint32_t H = 256 * NV;
+    if constexpr (MT) {
+        if (e >= a.n_experts + (a.shared_router ? 1u : 0u)) return;   // the rounding's workgroups
+        const uint32_t t = blockIdx.y;
+        a.x += (size_t)t * H;
+        a.xn += (size_t)t * H;
+        a.logits += (size_t)t * a.n_experts;
+        a.sw += t;
+    }
     float4 xv[NH];
 #pragma unroll
     for (int i = 0; i < NH; i++) xv[i] = ((const float4*)a.x)[64 * (h * NH + i) + lane];
@@ -2740,11 +2750,12 @@ int launch_moe(const MoeArgs& a, const MoeLaunch& m, hipStream_t st, hipEvent_t*
         };
         auto by_nv_rows = [&]() {   // one token per grid row
             const uint32_t gx = (m.grid_r + 7u) & ~7u;
+            constexpr uint32_t B = 64 * kRouterWaves;
             switch (a.hidden / 256) {
             case 1: rc = launch_k(k_moe_router<1, 1, true>, gx, 64, 0, st, ev, a, a.T); break;
-            case 2: rc = launch_k(k_moe_router<1, 2, true>, gx, 64, 0, st, ev, a, a.T); break;
-            case 4: rc = launch_k(k_moe_router<1, 4, true>, gx, 64, 0, st, ev, a, a.T); break;
-            default: rc = launch_k(k_moe_router<1, 8, true>, gx, 64, 0, st, ev, a, a.T); break;
+            case 2: rc = launch_k(k_moe_router_w<2, kRouterWaves, true>, gx, B, 0, st, ev, a, a.T); break;
+            case 4: rc = launch_k(k_moe_router_w<4, kRouterWaves, true>, gx, B, 0, st, ev, a, a.T); break;
+            default: rc = launch_k(k_moe_router_w<8, kRouterWaves, true>, gx, B, 0, st, ev, a, a.T); break;
             }
         };
         if (!m.mx && a.T > 1) {   // the fp32 kernels' launches of several tokens
