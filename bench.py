@@ -7,9 +7,11 @@ router [256 x 2048], one shared expert of the same shapes; synthetic seeded
 weights resident in HBM. A step is one token through one MoE layer (router
 GEMV, softmax top-8, 8 experts + shared expert gate/up/SiLU/down,
 gate-weighted combine). Steps cycle through a pool of independently seeded
-layers (default 16 x ~522 MB) and inputs, so the 256 MB Infinity Cache cannot
-serve repeats. `value` is microseconds per MoE layer of the HIP-graph-replayed
-kernels, inputs already in HBM.
+layers (default 40 x ~522 MB) and inputs: the rows one pass over the pool
+reads (40 x 20.5 MB of selected experts) exceed the 256 MB Infinity Cache
+(MALL) three times over, so repeats come from HBM (with 16 layers, 328 MB,
+part of them were served from the MALL). `value` is microseconds per MoE
+layer of the HIP-graph-replayed kernels, inputs already in HBM.
 
 `roofline` is for the dominant kernel (gate/up/SiLU over the 8 selected
 experts + shared): algorithmic bytes per launch over its average duration,
@@ -88,7 +90,7 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=32)
-    ap.add_argument("--pool", type=int, default=16)
+    ap.add_argument("--pool", type=int, default=40)
     ap.add_argument("--workload", default="all",
                     choices=["all", "q4k", "iq2m", "stack", "prefill", "mtp", "head", "floor",
                              "gguf"])
