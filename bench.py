@@ -68,11 +68,11 @@ GROUPED_MIN_TOKENS = 17
 TRAFFIC_FILE = os.path.join(HERE, "profiles", "moe_gate_up_q4k_decode_traffic.json")
 # The headline's kernel instantiations in a trace or counter file (the
 # one-token kernels of the Q4_K / Q6_K layer at hidden 2048, inter 512:
-# router <T = 1, 8 float4 per lane>, gate/up <format 0 = Q4_K, 64 units per
-# row>, down <T = 1, format 2 = Q6_K, 16 units>). The default run dispatches
-# them first; other workloads of the same run use other instantiations or
-# come later.
-HEADLINE_KERNELS = {"k_moe_router": "k_moe_router<1, 8, false>",
+# router <8 float4 per lane, 2 waves per router row>, gate/up <format 0 =
+# Q4_K, 64 units per row>, down <T = 1, format 2 = Q6_K, 16 units>), keyed by
+# the names the bench line gives them. The default run dispatches them first;
+# other workloads of the same run use other instantiations or come later.
+HEADLINE_KERNELS = {"k_moe_router": "k_moe_router_w<8, 2, false>",
                     "k_moe_gate_up1": "k_moe_gate_up1<0, 64, false>",
                     "k_moe_down": "k_moe_down<1, 2, 16, false>"}
 
@@ -283,12 +283,13 @@ def summarize_trace(trace_dir, bench_json, command, plain_json=None):
     files = glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)
     if not files:
         raise SystemExit("no kernel_trace.csv under %s" % trace_dir)
+    bases = {v.split("<")[0] for v in HEADLINE_KERNELS.values()}
     per = {}
     for f in files:
         with open(f) as fh:
             for r in csv.DictReader(fh):
                 name = r["Kernel_Name"]
-                if _short_kernel(name).split("<")[0] not in HEADLINE_KERNELS:
+                if _short_kernel(name).split("<")[0] not in bases:
                     continue
                 per.setdefault(name, []).append(
                     (int(r["Start_Timestamp"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
