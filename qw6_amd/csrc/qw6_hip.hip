@@ -2,10 +2,12 @@
 //
 // Decode path (fp32 accumulation), three kernels per MoE layer (a kernel
 // boundary is the cheapest grid-wide dependency on this GPU):
-//   k_moe_router : router GEMV over all experts (one wave per expert row),
-//                  optional RMSNorm of the input, shared-expert gate weight.
+//   k_moe_router : router GEMV over all experts (k_moe_router_w: two waves
+//                  per expert row for one token), optional RMSNorm of the
+//                  input, shared-expert gate weight.
 //   k_moe_gate_up1: each workgroup takes one row tile of every selected
-//                  expert and of the shared one, a wave per matrix pair; each
+//                  expert and of the shared one, a wave per matrix pair (two
+//                  for the shared pair on IQ layers at one token); each
 //                  routed wave selects its own expert from the logits (softmax
 //                  top-k), then streams its gate/up rows into LDS with
 //                  direct-to-LDS 16-byte loads, dequantizing step s while step
@@ -351,8 +353,9 @@ __global__ __launch_bounds__(64) void k_route(const float* __restrict__ logits, 
 //
 // Three kernels per layer (a kernel boundary is the cheapest grid-wide
 // dependency on this GPU; in-kernel grid barriers cost several times more):
-//   k_moe_router : router GEMV, one wave per expert row (+ optional RMSNorm of
-//                  the input, + the shared-expert gate weight).
+//   k_moe_router : router GEMV, one wave per expert row, or two in
+//                  k_moe_router_w (+ optional RMSNorm of the input, + the
+//                  shared-expert gate weight).
 //   k_moe_gate_up1: every selected expert's gate/up rows of one row tile per
 //                  workgroup, each routed wave routing the token itself from
 //                  the logits (1 KB per token); silu(gate) * up -> mid.
@@ -904,13 +907,12 @@ __global__ __launch_bounds__(64 * W) void k_moe_router_w(MoeArgs a) {
 // just before the weights, so both round trips overlap. bar: wait for the
 // block's earlier LDS-direct loads (the lattice tables) and meet the other
 // waves before reading them.
-template <int T, int FF, int KU>
+template <int T, int FF, int KU, int S = kStepsGu>
 __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint32_t row0,
                                              const float* x, uint32_t hidden, bool bar,
                                              float* mid, uint32_t inter, uint8_t* slots,
                                              const uint32_t* lds, uint32_t slot_off, uint32_t pb,
                                              const uint32_t* tab) {
-    constexpr int S = kStepsGu;
     const int f = FF >= 0 ? FF : G.fmt;
     constexpr uint32_t U = KU, rps = 64 / KU;
     const uint32_t lane = threadIdx.x & 63;
@@ -972,24 +974,40 @@ __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint
 // expert and of the shared one. Wave w < top_k works on the expert of rank w
 // (slot w), which it selects itself from the logits (no barrier); in
 // workgroup 0, wave 0 runs the full routing instead and publishes the
-// selection and the slot table. Wave top_k (when present) streams the shared
-// expert from the start. Every workgroup moves the same bytes and there is
-// one per row tile: at hidden 2048 / inter 512, 256 workgroups of 9 waves,
-// one per CU (a 4-wave workgroup per (expert, row tile) put 576 workgroups on
-// the 256 CUs, three on a quarter of them).
+// selection and the slot table. The waves past top_k (when the layer has a
+// shared expert) stream the shared expert from the start (its waves:
+// gate_up1_shared_waves). Every workgroup moves the same bytes and there is
+// one per row tile: at hidden 2048 / inter 512, 256 workgroups of 9 or 10
+// waves, one per CU (a 4-wave workgroup per (expert, row tile) put 576
+// workgroups on the 256 CUs, three on a quarter of them).
+//
+// The shared expert takes two waves of one row step each for one token on
+// layers whose gate/up formats include an IQ one: with nine waves one SIMD
+// ran two routed waves and the whole shared expert, and the IQ units' decode
+// made it the last to finish. K-quant layers, and the launches of several
+// tokens (MT), whose workgroups share a CU three at a time, keep one wave of
+// both row steps.
+__host__ __device__ constexpr uint32_t gate_up1_shared_waves(bool mt, int fg) {
+    return !mt && (fmt_in(fg, F_IQ2XXS) || fmt_in(fg, F_IQ2S) || fmt_in(fg, F_IQ3S)) ? 2u : 1u;
+}
+
 template <int FG, int KU, bool MT = false>
-__global__ __launch_bounds__(64 * 9) void k_moe_gate_up1(MoeArgs a) {
+__global__ __launch_bounds__(64 * (8 + gate_up1_shared_waves(MT, FG))) void k_moe_gate_up1(MoeArgs a) {
     extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
     __shared__ uint32_t s_idx[8];
     __shared__ float s_w[8];
     __shared__ uint2 s_route[8 * kRouteScr];   // one per routed wave
     constexpr int S = kStepsGu;
+    constexpr int SS = S / (int)gate_up1_shared_waves(MT, FG);   // row steps of a shared wave
+    static_assert(SS * (int)gate_up1_shared_waves(MT, FG) == S, "the shared waves split the row steps");
     constexpr uint32_t rps = 64 / KU;
     const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63u;
     if constexpr (MT) token_view(a);
     const bool shared_w = wave >= a.top_k;
+    const uint32_t sh_i = shared_w ? wave - a.top_k : 0u;   // a shared wave's share of the steps
     const uint32_t toff = tab_bytes(a.tmask_gu);
-    const uint32_t slot_off = toff + wave * S * a.gu_pb;
+    // LDS pair slots: S per routed wave, then SS per shared wave
+    const uint32_t slot_off = toff + (shared_w ? S * a.top_k + SS * sh_i : S * wave) * a.gu_pb;
     // the logits load is a routed wave's first memory operation; every wave
     // then stages its share of the lattice tables
     uint32_t keys[4];
@@ -1029,18 +1047,27 @@ __global__ __launch_bounds__(64 * 9) void k_moe_gate_up1(MoeArgs a) {
         Up = expert_mat_wave(a, e, 1);
         midp = a.mid + (size_t)wave * a.inter;
     }
-    const uint32_t row0 = blockIdx.x * S * rps;
+    const uint32_t row0 = (blockIdx.x * S + sh_i * SS) * rps;
     const uint32_t* lds = (const uint32_t*)smem;
     uint8_t* wslots = smem + slot_off;
-    if (FG >= 0) {
-        wave_gate_up<1, FG, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off, a.gu_pb, lds);
-        return;
+    auto body = [&](auto fc) {
+        constexpr int F = decltype(fc)::value;
+        if constexpr (SS == S) {
+            wave_gate_up<1, F, KU, S>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off,
+                                      a.gu_pb, lds);
+        } else if (shared_w) {
+            wave_gate_up<1, F, KU, SS>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off,
+                                       a.gu_pb, lds);
+        } else {
+            wave_gate_up<1, F, KU, S>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off,
+                                      a.gu_pb, lds);
+        }
+    };
+    if constexpr (FG >= 0) {
+        body(std::integral_constant<int, FG>{});
+    } else {   // mixed formats: one switch per wave, each body specialised
+        by_fmt<FG>(G.fmt, body);
     }
-    // mixed formats: one switch per wave, each body specialised
-    by_fmt<FG>(G.fmt, [&](auto fc) {
-        wave_gate_up<1, decltype(fc)::value, KU>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds,
-                                                 slot_off, a.gu_pb, lds);
-    });
 }
 
 // Down projection + combine for rows [r0, r0 + R), R = S * rps. Matrix m of
@@ -2699,7 +2726,8 @@ struct MoeLaunch {
     bool mx;                 // the small-batch MFMA kernels (k_mx_*)
     uint32_t gy;             // grid rows of k_moe_gate_up1 / k_moe_down<1>: one per token
     uint32_t grid_r;
-    uint32_t grid_b1, nw_b1;
+    uint32_t grid_b1;
+    bool has_sh;             // the layer has a shared expert
     size_t lds_b1;
     int fg, fd;              // format of the gate/up (down) kernels, -1: mixed
     uint32_t mg, md;         // the formats present (bit f: format f), gate/up and down
@@ -2801,8 +2829,10 @@ int launch_moe(const MoeArgs& a, const MoeLaunch& m, hipStream_t st, hipEvent_t*
     auto fp32 = [&](auto mt) {
         constexpr bool MT = decltype(mt)::value;
         launch_expert_kernel<64, kSetGateUpIq2m>(m.fg, m.mg, a.hidden / 32, [&](auto fc, auto kc) {
-            rc = launch_k(k_moe_gate_up1<decltype(fc)::value, decltype(kc)::value, MT>, m.grid_b1,
-                          64 * m.nw_b1, m.lds_b1, st, ev ? ev + 2 : nullptr, a, m.gy);
+            constexpr int F = decltype(fc)::value;
+            const uint32_t nw = a.top_k + (m.has_sh ? gate_up1_shared_waves(MT, F) : 0u);
+            rc = launch_k(k_moe_gate_up1<F, decltype(kc)::value, MT>, m.grid_b1, 64 * nw, m.lds_b1, st,
+                          ev ? ev + 2 : nullptr, a, m.gy);
         });
         if (rc) return;
         launch_expert_kernel<16, kSetDownIq2m>(m.fd, m.md, a.inter / 32, [&](auto fc, auto kc) {
@@ -2960,10 +2990,12 @@ int moe_forward_impl(qw6_hip_ctx_t* c, const qw6_hip_moe_layer_t* L, const float
     // mode 3 the small-batch MFMA kernels, launches of up to kMaxTok tokens.
     const bool mx = c->mode == 3;
     const uint32_t chunk = mx ? kMaxTok : kSplitMaxTok;
-    // k_moe_gate_up1: one workgroup per kStepsGu row steps of every matrix pair
-    m.nw_b1 = L->top_k + (has_sh ? 1u : 0u);
+    // k_moe_gate_up1: one workgroup per kStepsGu row steps of every matrix
+    // pair, kStepsGu LDS pair slots per matrix pair (the shared expert's
+    // split over its waves)
     m.grid_b1 = (L->inter + kStepsGu * rpsg - 1) / (kStepsGu * rpsg);
-    m.lds_b1 = (size_t)tab_bytes(mgu) + (size_t)m.nw_b1 * kStepsGu * a.gu_pb;
+    m.has_sh = has_sh;
+    m.lds_b1 = (size_t)tab_bytes(mgu) + (size_t)(L->top_k + (has_sh ? 1u : 0u)) * kStepsGu * a.gu_pb;
     if (!mx && m.lds_b1 > kMxLdsBudget) return fail("gate/up tile exceeds the LDS budget");
     const uint32_t grid_c_valu = m.grid_c;
     for (uint32_t t0 = 0; t0 < n_tok; t0 += chunk) {
