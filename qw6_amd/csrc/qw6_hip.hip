@@ -932,7 +932,12 @@ __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint
     // nothing that reads the activations may be scheduled among the staging
     // loads (its wait would hold back the loads after it)
     __builtin_amdgcn_sched_barrier(0);
-    if (bar) {   // the block's earlier LDS-direct loads (the tables) are complete
+    // A body that reads no lattice table (a K-quant format) meets the other
+    // waves after its products instead: its own table loads are older than
+    // its weights, so they have landed by then, and it computes while the
+    // routed IQ waves wait for their weights.
+    constexpr bool late_bar = FF >= 0 && !is_iq(FF);
+    if (bar && !late_bar) {   // the block's earlier LDS-direct loads (the tables) are complete
         wait_vm(nl * S + 8u * T);
         lds_barrier();
     }
@@ -966,6 +971,7 @@ __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint
         for (int t = 0; t < T; t++)
             mid[(size_t)t * inter + r] = gv[t] / (1.0f + expf(-gv[t])) * uv[t];
     }
+    if (bar && late_bar) lds_barrier();
     TRACE_MARK(2, 3);
 }
 
