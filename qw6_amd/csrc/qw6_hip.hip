@@ -907,7 +907,7 @@ __global__ __launch_bounds__(64 * W) void k_moe_router_w(MoeArgs a) {
 // just before the weights, so both round trips overlap. bar: wait for the
 // block's earlier LDS-direct loads (the lattice tables) and meet the other
 // waves before reading them.
-template <int T, int FF, int KU, int S = kStepsGu>
+template <int T, int FF, int KU, int S = kStepsGu, bool LATE = false>
 __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint32_t row0,
                                              const float* x, uint32_t hidden, bool bar,
                                              float* mid, uint32_t inter, uint8_t* slots,
@@ -932,11 +932,13 @@ __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint
     // nothing that reads the activations may be scheduled among the staging
     // loads (its wait would hold back the loads after it)
     __builtin_amdgcn_sched_barrier(0);
-    // A body that reads no lattice table (a K-quant format) meets the other
-    // waves after its products instead: its own table loads are older than
-    // its weights, so they have landed by then, and it computes while the
-    // routed IQ waves wait for their weights.
-    constexpr bool late_bar = FF >= 0 && !is_iq(FF);
+    // LATE: a body that reads no lattice table (a K-quant format) meets the
+    // other waves after its products instead: its own table loads are older
+    // than its weights, so they have landed by then, and it computes while
+    // the routed IQ waves wait for their weights. (The launches of several
+    // tokens, three workgroups per CU, keep the barrier first: measured
+    // slower there.)
+    constexpr bool late_bar = LATE && FF >= 0 && !is_iq(FF);
     if (bar && !late_bar) {   // the block's earlier LDS-direct loads (the tables) are complete
         wait_vm(nl * S + 8u * T);
         lds_barrier();
@@ -1059,14 +1061,14 @@ __global__ __launch_bounds__(64 * (8 + gate_up1_shared_waves(MT, FG))) void k_mo
     auto body = [&](auto fc) {
         constexpr int F = decltype(fc)::value;
         if constexpr (SS == S) {
-            wave_gate_up<1, F, KU, S>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off,
-                                      a.gu_pb, lds);
+            wave_gate_up<1, F, KU, S, !MT>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds,
+                                           slot_off, a.gu_pb, lds);
         } else if (shared_w) {
-            wave_gate_up<1, F, KU, SS>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off,
-                                       a.gu_pb, lds);
+            wave_gate_up<1, F, KU, SS, !MT>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds,
+                                            slot_off, a.gu_pb, lds);
         } else {
-            wave_gate_up<1, F, KU, S>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds, slot_off,
-                                      a.gu_pb, lds);
+            wave_gate_up<1, F, KU, S, !MT>(G, Up, row0, a.xin, a.hidden, bar, midp, a.inter, wslots, lds,
+                                           slot_off, a.gu_pb, lds);
         }
     };
     if constexpr (FG >= 0) {
