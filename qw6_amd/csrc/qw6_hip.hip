@@ -936,8 +936,8 @@ __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint
     // other waves after its products instead: its own table loads are older
     // than its weights, so they have landed by then, and it computes while
     // the routed IQ waves wait for their weights. (The launches of several
-    // tokens, three workgroups per CU, keep the barrier first: measured
-    // slower there.)
+    // tokens, two or three workgroups per CU, keep the barrier first:
+    // measured slower there.)
     constexpr bool late_bar = LATE && FF >= 0 && !is_iq(FF);
     if (bar && !late_bar) {   // the block's earlier LDS-direct loads (the tables) are complete
         wait_vm(nl * S + 8u * T);
@@ -993,8 +993,8 @@ __device__ __forceinline__ void wave_gate_up(const MatD& G, const MatD& Up, uint
 // layers whose gate/up formats include an IQ one: with nine waves one SIMD
 // ran two routed waves and the whole shared expert, and the IQ units' decode
 // made it the last to finish. K-quant layers, and the launches of several
-// tokens (MT), whose workgroups share a CU three at a time, keep one wave of
-// both row steps.
+// tokens (MT), whose workgroups share a CU two or three at a time, keep one
+// wave of both row steps.
 __host__ __device__ constexpr uint32_t gate_up1_shared_waves(bool mt, int fg) {
     return !mt && (fmt_in(fg, F_IQ2XXS) || fmt_in(fg, F_IQ2S) || fmt_in(fg, F_IQ3S)) ? 2u : 1u;
 }
